@@ -1,0 +1,287 @@
+"""Benchmark: exact kNN QPS of the MI355X FlatIndex backend.
+
+Workload (the headline): FlatIndex exact L2 over 1,000,000 x 128 fp32 SIFT-like integers
+in [0, 255] (clipped exponential, mean ~20), 10,000 queries of the same distribution,
+k = 10, synthetic and seeded. One step = one search_batch of the 10,000 queries with the
+queries already resident in HBM and results written to HBM (px_flat_search_device).
+
+Prints one JSON line. roofline.achieved = 2 * nq * N * D flop per scan launch divided by
+the scan kernel's mean duration, timed with HIP events on the library's stream around
+every timed launch. cpu_baseline times the CPU oracle (a C restatement of the reference's
+per-query scan, flat.rs:106-148 with distance.rs:3-39) on a bounded query sample on the
+host's cores, and the same sample checks parity of the GPU results.
+
+  python bench.py [--steps K] [--warmup W] [--k 10] [--workload flat|pq] [--gpus 1]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from proxima_amd import FlatIndex, Metric, PqIndex, _lib, datagen  # noqa: E402
+
+FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix peak
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Dev:
+    """Device buffers through the library's own HIP runtime (no second runtime)."""
+
+    def __init__(self):
+        self.lib = _lib.load()
+        self.ptrs = []
+
+    def put(self, arr: np.ndarray) -> ctypes.c_void_p:
+        p = ctypes.c_void_p()
+        rc = self.lib.px_dev_alloc(ctypes.byref(p), max(arr.nbytes, 16))
+        if rc:
+            raise RuntimeError(_lib.last_error())
+        self.ptrs.append(p)
+        if arr.nbytes and self.lib.px_dev_upload(p, arr.ctypes.data, arr.nbytes):
+            raise RuntimeError(_lib.last_error())
+        return p
+
+    def empty(self, nbytes: int) -> ctypes.c_void_p:
+        p = ctypes.c_void_p()
+        if self.lib.px_dev_alloc(ctypes.byref(p), max(nbytes, 16)):
+            raise RuntimeError(_lib.last_error())
+        self.ptrs.append(p)
+        return p
+
+    def get(self, p, arr: np.ndarray) -> np.ndarray:
+        if self.lib.px_dev_download(arr.ctypes.data, p, arr.nbytes):
+            raise RuntimeError(_lib.last_error())
+        return arr
+
+    def free(self):
+        for p in self.ptrs:
+            self.lib.px_dev_free(p)
+        self.ptrs = []
+
+
+def cpu_baseline(data, queries, k, metric, gpu_ids, gpu_d, budget_s, mask=None, pq=None):
+    """Time the oracle on growing query batches until ~budget_s of CPU work; check parity
+    of the same sample against the GPU results."""
+    import oracle
+
+    threads = oracle.max_threads()
+    done, spent = 0, 0.0
+    batch = 64
+    mism = 0
+    max_rel = 0.0
+    while done < len(queries) and spent < budget_s:
+        b = min(batch, len(queries) - done)
+        qs = queries[done:done + b]
+        t0 = time.perf_counter()
+        if pq is None:
+            o_ids, o_d, _ = oracle.flat_search(data, qs, k, metric, mask=mask)
+        else:
+            books, codes = pq
+            o_ids, o_d, _ = oracle.pq_search(books, codes, qs, k, metric, mask=mask)
+        spent += time.perf_counter() - t0
+        g_ids, g_d = gpu_ids[done:done + b], gpu_d[done:done + b]
+        mism += int((g_ids != o_ids).sum())
+        ok = o_ids >= 0
+        if ok.any():
+            r = np.abs(g_d[ok] - o_d[ok]) / np.maximum(np.abs(o_d[ok]), 1e-30)
+            max_rel = max(max_rel, float(r.max()))
+        done += b
+        batch = min(batch * 2, 1024)
+    return {"value": done / spent, "unit": "queries/s", "cores": threads, "kind": "port",
+            "sample": f"first {done} of {len(queries)} queries, full corpus, {threads} threads, "
+                      f"{spent:.1f} s"}, {"queries_checked": done, "id_mismatches": mism,
+                                           "max_rel_dist_err": max_rel}
+
+
+def read_traffic(name: str):
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    try:
+        with open(path) as fh:
+            return json.load(fh).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def bench_flat(args, dev):
+    n, dim, nq, k = args.n, 128, args.nq, args.k
+    log(f"[bench] generating corpus {n} x {dim} SIFT-like and {nq} queries")
+    data = datagen.sift_like(n, dim, 3001)
+    queries = datagen.sift_like(nq, dim, 3002)
+    idx = FlatIndex(dim, Metric.L2)
+    t0 = time.perf_counter()
+    idx.add(data)
+    log(f"[bench] add + upload {time.perf_counter() - t0:.2f} s")
+    lib = dev.lib
+    dq = dev.put(queries)
+    di = dev.empty(nq * k * 8)
+    dd = dev.empty(nq * k * 4)
+
+    def step():
+        rc = lib.px_flat_search_device(idx._h, dq, nq, k, None, di, dd)
+        if rc:
+            raise RuntimeError(_lib.last_error())
+
+    idx._timing(True)
+    for _ in range(args.warmup):
+        step()
+    log("[bench] warmup done")
+    scan_ms, total_ms = [], []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+        t = idx._last_timing()
+        scan_ms.append(t["scan_ms"])
+        total_ms.append(t["total_ms"])
+    elapsed = time.perf_counter() - t0
+    info = idx._last_timing()
+    log(f"[bench] {args.steps} steps in {elapsed:.3f} s; scan {np.mean(scan_ms):.3f} ms, "
+        f"pipeline {np.mean(total_ms):.3f} ms, splits {info['splits']}, blocks {info['blocks']}")
+    ids = dev.get(di, np.empty((nq, k), dtype=np.int64))
+    dists = dev.get(dd, np.empty((nq, k), dtype=np.float32))
+
+    flops = 2.0 * nq * n * dim
+    achieved = flops / (np.mean(scan_ms) * 1e-3) / 1e12
+    result = {
+        "metric": "exact kNN QPS (1M x 128 fp32, k=10, 10k-query batch); % fp32 MFMA peak",
+        "value": nq * args.steps / elapsed,
+        "unit": "queries/s",
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "dtype": "f32",
+        "config": {"workload": f"FlatIndex exact L2, corpus {n} x {dim} fp32 SIFT-like "
+                               f"integers in [0,255], {nq}-query batch, k={k}",
+                   "n": n, "dim": dim, "nq": nq, "k": k, "metric": "L2",
+                   "queries_resident_in_hbm": True},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
+                     "traffic": read_traffic("flat_scan_l2_1Mx128_traffic.json"),
+                     "kernel": "flat_scan_kernel", "kernel_ms": float(np.mean(scan_ms)),
+                     "algorithmic_flop_per_launch": flops},
+        "pipeline_ms": float(np.mean(total_ms)),
+    }
+    if args.cpu_seconds > 0:
+        log("[bench] CPU oracle baseline + parity sample")
+        import oracle
+
+        cb, par = cpu_baseline(data, queries, k, oracle.L2, ids, dists, args.cpu_seconds)
+        result["cpu_baseline"] = cb
+        result["parity_sample"] = par
+    return result
+
+
+def bench_pq(args, dev):
+    n, dim, nq, k, m = args.n, 128, args.nq, args.k, 16
+    log(f"[bench] generating PQ corpus {n} x {dim} N(0,1), training m={m}")
+    data = datagen.gaussian(n, dim, 4001)
+    queries = datagen.gaussian(nq, dim, 4002)
+    mask = datagen.mask(n, 0.5, 4003) if args.mask else None
+    pq = PqIndex(dim, Metric.L2, m=m, nbits=8, train_iters=25, train_sample=50_000)
+    t0 = time.perf_counter()
+    pq.train(data)
+    log(f"[bench] train {time.perf_counter() - t0:.1f} s")
+    t0 = time.perf_counter()
+    pq.add(data)
+    log(f"[bench] encode + upload {time.perf_counter() - t0:.1f} s")
+    lib = dev.lib
+    dq = dev.put(queries)
+    dm = dev.put(mask.view(np.uint8)) if mask is not None else None
+    di = dev.empty(nq * k * 8)
+    dd = dev.empty(nq * k * 4)
+
+    def step():
+        rc = lib.px_pq_search_device(pq._h, dq, nq, k, dm, di, dd)
+        if rc:
+            raise RuntimeError(_lib.last_error())
+
+    pq._timing(True)
+    for _ in range(args.warmup):
+        step()
+    scan_ms = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+        scan_ms.append(pq._last_timing()["scan_ms"])
+    elapsed = time.perf_counter() - t0
+    ids = dev.get(di, np.empty((nq, k), dtype=np.int64))
+    dists = dev.get(dd, np.empty((nq, k), dtype=np.float32))
+    n_eff = int(mask.sum()) if mask is not None else n
+    algo_bytes = nq * (n_eff * m + ((n + 7) // 8 if mask is not None else 0)) + nq * m * 256 * 4
+    achieved = algo_bytes / (np.mean(scan_ms) * 1e-3) / 1e9
+    result = {
+        "metric": "PqIndex ADC scan QPS (1M x m=16 x 8-bit codes, k=10, 10k-query batch); "
+                  "% HBM peak",
+        "value": nq * args.steps / elapsed,
+        "unit": "queries/s",
+        "ms_per_step": elapsed / args.steps * 1e3,
+        "dtype": "f32",
+        "config": {"workload": f"PqIndex ADC L2, {n} codes x m={m} x 8 bit, {nq}-query batch, "
+                               f"k={k}, mask={'50%' if mask is not None else 'none'}",
+                   "n": n, "m": m, "nq": nq, "k": k},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": read_traffic("pq_scan_1Mx16_traffic.json"),
+                     "kernel": "pq_scan_kernel", "kernel_ms": float(np.mean(scan_ms)),
+                     "algorithmic_bytes_per_launch": algo_bytes},
+    }
+    if args.cpu_seconds > 0:
+        import oracle
+
+        cb, par = cpu_baseline(None, queries, k, oracle.L2, ids, dists, args.cpu_seconds,
+                               mask=mask, pq=(pq.codebooks(), pq.codes()))
+        result["cpu_baseline"] = cb
+        result["parity_sample"] = par
+    return result
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--k", type=int, default=10)
+    ap.add_argument("--n", type=int, default=1_000_000)
+    ap.add_argument("--nq", type=int, default=10_000)
+    ap.add_argument("--workload", choices=["flat", "pq"], default="flat")
+    ap.add_argument("--mask", action="store_true", help="pq: 50%% filter bitmask")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="CPU oracle budget for the baseline (0 disables)")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this backend runs the whole search on a "
+              "single MI355X and has no multi-GPU path (sharding is described in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    if _lib.device_count() < 1:
+        print("bench.py needs a gfx950 GPU (none visible)", file=sys.stderr)
+        sys.exit(1)
+    dev = Dev()
+    try:
+        res = bench_flat(args, dev) if args.workload == "flat" else bench_pq(args, dev)
+    finally:
+        dev.free()
+    out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
+           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
+           "vs_baseline": None, "dtype": res.pop("dtype"), "data": "synthetic (seeded SplitMix64)",
+           "config": res.pop("config")}
+    out.update(res)
+    out["device"] = _lib.device_info(0)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

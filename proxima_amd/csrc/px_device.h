@@ -1,0 +1,136 @@
+// px_device.h -- device-side helpers shared by the flat and PQ kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace px {
+
+// Id sentinel for an empty list slot. Real ids (row numbers or compacted positions)
+// are < 2^31 - 1, so the sentinel sorts after every real candidate of equal key.
+constexpr int kIdNone = 0x7fffffff;
+
+// The IEEE-754 totalOrder mapping used by f32::total_cmp (crates/core/src/flat.rs:20):
+// negative numbers get their magnitude bits flipped, then keys compare as int32.
+__device__ __forceinline__ int total_key(float f) {
+    int b = __float_as_int(f);
+    return b ^ (int)(((unsigned)(b >> 31)) >> 1);
+}
+
+// Canonical candidate order: (key in total order, id) lexicographic.
+__device__ __forceinline__ bool cand_less(float ka, int ia, float kb, int ib) {
+    int ta = total_key(ka), tb = total_key(kb);
+    return ta < tb || (ta == tb && ia < ib);
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ int readlane_i(int v, int lane) {
+    return __builtin_amdgcn_readlane(v, lane);
+}
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
+
+// Wave-cooperative insertion of (ck, cid) into a sorted list of `kl` live slots
+// (capacity KP, a multiple of 64 or <= 64) held in LDS at lk/li. Lane s owns slots
+// s, s+64, ... The caller guarantees (ck, cid) is smaller than slot kl-1, so the new
+// element lands at some pos < kl and the old slot kl-1 falls off the end.
+// Returns the new last live slot (the list threshold) in every lane.
+template <int KP>
+__device__ __forceinline__ void list_insert(float* lk, int* li, int kl, float ck, int cid,
+                                            float& tau_k, int& tau_i) {
+    const int s = lane_id();
+    constexpr int U = KP > 64 ? KP / 64 : 1;
+    float okey[U], pkey[U];
+    int oid[U], pid[U];
+    unsigned long long after[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int slot = s + 64 * u;
+        const bool live = slot < kl;
+        okey[u] = live ? lk[slot] : __int_as_float(0x7f800000);
+        oid[u] = live ? li[slot] : kIdNone;
+        pkey[u] = (live && slot > 0) ? lk[slot - 1] : 0.f;
+        pid[u] = (live && slot > 0) ? li[slot - 1] : 0;
+        after[u] = __ballot(live && cand_less(ck, cid, okey[u], oid[u]));
+    }
+    int pos = kl;
+#pragma unroll
+    for (int u = U - 1; u >= 0; --u)
+        if (after[u]) pos = 64 * u + __builtin_ctzll(after[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int slot = s + 64 * u;
+        if (slot < kl) {
+            if (slot > pos) {
+                lk[slot] = pkey[u];
+                li[slot] = pid[u];
+            } else if (slot == pos) {
+                lk[slot] = ck;
+                li[slot] = cid;
+            }
+        }
+    }
+    // new threshold: slot kl-1 after the shift
+    const int last = kl - 1;
+    float nk;
+    int ni;
+    if (pos == last) {
+        nk = ck;
+        ni = cid;
+    } else {
+        // slot kl-1 now holds what was in slot kl-2, i.e. pkey of the lane owning kl-1
+        const int owner = last & 63, uu = last >> 6;
+        float pk = pkey[0];
+        int pi = pid[0];
+#pragma unroll
+        for (int u = 1; u < U; ++u)
+            if (uu == u) { pk = pkey[u]; pi = pid[u]; }
+        nk = readlane_f(pk, owner);
+        ni = readlane_i(pi, owner);
+    }
+    tau_k = nk;
+    tau_i = ni;
+}
+
+// ---------------------------------------------------------------------------
+// The reference's arithmetic (crates/core/src/distance.rs:3-39): eight lane
+// accumulators over chunks of 8, lane sum in order, then the remainder, no FMA.
+// Every translation unit is built with -ffp-contract=off; FMAs elsewhere are explicit.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float ref_l2_sqr(const float* a, const float* b, int n) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int chunks = n >> 3;
+    for (int c = 0; c < chunks; ++c) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            const float d = a[c * 8 + l] - b[c * 8 + l];
+            acc[l] = acc[l] + d * d;
+        }
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) sum = sum + acc[l];
+    for (int i = chunks * 8; i < n; ++i) {
+        const float d = a[i] - b[i];
+        sum = sum + d * d;
+    }
+    return sum;
+}
+
+__device__ __forceinline__ float ref_inner_product(const float* a, const float* b, int n) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int chunks = n >> 3;
+    for (int c = 0; c < chunks; ++c) {
+#pragma unroll
+        for (int l = 0; l < 8; ++l) acc[l] = acc[l] + a[c * 8 + l] * b[c * 8 + l];
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) sum = sum + acc[l];
+    for (int i = chunks * 8; i < n; ++i) sum = sum + a[i] * b[i];
+    return sum;
+}
+
+}  // namespace px

@@ -1,0 +1,440 @@
+// px_flat.hip -- exact kNN (FlatIndex) kernels for gfx950.
+//
+// Replaces the per-query full scan of crates/core/src/flat.rs:106-148 (and the CUDA
+// satellite crates/core/cuda/knn.cu:22-121) with a tiled fp32-MFMA contraction:
+//   L2 key  = ||x||^2 + ||q||^2 - 2 q.x   (precomputed corpus norms in HBM)
+//   IP key  = -q.x
+// Corpus tiles of 64 rows are staged through LDS; each wave keeps 32 queries' fragments
+// in registers (MFMA B operand) and a sorted candidate list per query in LDS, so the
+// distance matrix never reaches HBM. Candidates are ordered by (key total-order, id).
+// The split lists are merged by flat_merge_kernel, which re-ranks the survivors with the
+// reference's exact arithmetic (distance.rs:3-39) before the final order is taken.
+#include "px_device.h"
+#include "px_kernels.h"
+
+#include <float.h>
+
+namespace px {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kTileRows = 64;            // corpus rows per tile: two 32-row MFMA blocks
+constexpr int kChunk = 128;              // dims per staged K-chunk (16 groups of 8)
+constexpr int kLdsStride = kChunk + 4;   // row pitch in LDS; +4 floats keeps b128 reads conflict-free
+
+// v_mfma_f32_32x32x2f32 result layout: lane l, register r holds D[i][j] with
+// j = l % 32 and i = 8 * (r / 4) + 4 * (l / 32) + r % 4.
+__device__ __forceinline__ int mfma_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+__device__ __forceinline__ f32x16 mfma4(float4 a, float4 b, f32x16 c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, c, 0, 0, 0);
+    return c;
+}
+
+int flat_list_capacity(int kl) {
+    if (kl <= 16) return 16;
+    if (kl <= 32) return 32;
+    if (kl <= 64) return 64;
+    return 128;
+}
+int flat_waves(int kp) { return kp >= 128 ? 2 : 4; }
+int flat_queries_per_block(int kp) { return 32 * flat_waves(kp); }
+
+// One workgroup = WAVES waves = 32*WAVES queries x one corpus split.
+// MFMA operands: A = corpus rows (M), B = queries (N), K = dims. For the 4 sub-steps e of
+// dim group g, lane (i, h) feeds A[i][h] = x[row i][8g + 4h + e] and lane (j, h) feeds
+// B[h][j] = q[j][8g + 4h + e]: both sides agree on the dim of every K slot.
+template <int KP, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
+    constexpr int NT = WAVES * 64;
+    __shared__ __attribute__((aligned(16))) float tile[kTileRows * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float tnorm[kTileRows];
+    __shared__ float lkeys[WAVES][32][KP];
+    __shared__ int lids[WAVES][32][KP];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const int qt = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+    const int q = qt * (WAVES * 32) + wave * 32 + j;
+    const bool qvalid = q < a.nq;
+    const bool l2 = a.metric == 0;
+    const int64_t row0 = (int64_t)split * a.rows_per_split;
+    const int64_t row1 = min(a.n_eff, row0 + a.rows_per_split);
+    const float kInf = __int_as_float(0x7f800000);
+    const float kNaN = __int_as_float(0x7fc00000);
+
+    for (int x = lane; x < 32 * KP; x += 64) {
+        lkeys[wave][x / KP][x % KP] = kInf;
+        lids[wave][x / KP][x % KP] = kIdNone;
+    }
+    float tau_k = kInf;   // threshold of query j: its list's slot kl-1
+    int tau_i = kIdNone;
+    const float qn = (l2 && qvalid) ? a.qnorms[q] : 0.f;
+
+    const int nchunks = (a.dp + kChunk - 1) / kChunk;
+    const float* qrow = a.queries + (int64_t)(qvalid ? q : 0) * a.dp;
+    float4 b[16];
+    auto load_b = [&](int c) {
+        const int dc = min(kChunk, a.dp - c * kChunk);
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            const int d = g * 8 + h * 4;
+            b[g] = (qvalid && d < dc) ? *reinterpret_cast<const float4*>(qrow + c * kChunk + d)
+                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    if (nchunks == 1) load_b(0);
+
+    for (int64_t t0 = row0; t0 < row1; t0 += kTileRows) {
+        f32x16 acc0 = {0.f}, acc1 = {0.f};
+        for (int c = 0; c < nchunks; ++c) {
+            const int dc = min(kChunk, a.dp - c * kChunk);
+            const int f4_per_row = dc >> 2;
+            __syncthreads();  // previous tile (and its norms) fully consumed
+            for (int f = tid; f < kTileRows * f4_per_row; f += NT) {
+                const int rr = f / f4_per_row, cc = f - rr * f4_per_row;
+                const int64_t pos = t0 + rr;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (pos < row1) {
+                    const int64_t row = a.rowidx ? (int64_t)a.rowidx[pos] : pos;
+                    v = *reinterpret_cast<const float4*>(a.corpus + row * a.dp + c * kChunk + cc * 4);
+                }
+                *reinterpret_cast<float4*>(tile + rr * kLdsStride + cc * 4) = v;
+            }
+            if (c == 0 && tid < kTileRows) {
+                const int64_t pos = t0 + tid;
+                float nv = 0.f;
+                if (l2 && pos < row1) nv = a.norms[a.rowidx ? (int64_t)a.rowidx[pos] : pos];
+                tnorm[tid] = nv;
+            }
+            __syncthreads();
+            if (nchunks > 1) load_b(c);
+            const int ng = dc >> 3;
+            const float* ta0 = tile + j * kLdsStride + h * 4;
+            const float* ta1 = tile + (32 + j) * kLdsStride + h * 4;
+#pragma unroll
+            for (int g = 0; g < 16; ++g) {
+                if (g < ng) {
+                    const float4 a0 = *reinterpret_cast<const float4*>(ta0 + g * 8);
+                    const float4 a1 = *reinterpret_cast<const float4*>(ta1 + g * 8);
+                    acc0 = mfma4(a0, b[g], acc0);
+                    acc1 = mfma4(a1, b[g], acc1);
+                }
+            }
+        }
+
+        // Epilogue: keys for the 32 rows this lane holds for query j.
+        float key[32];
+        float kmin = kNaN;
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) {
+                const int lr = rb * 32 + 8 * r4 + 4 * h;  // rows lr .. lr+3
+                const float4 nv = *reinterpret_cast<const float4*>(tnorm + lr);
+                const float nn[4] = {nv.x, nv.y, nv.z, nv.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * r4 + e;
+                    const float dot = rb == 0 ? acc0[r] : acc1[r];
+                    float kv = l2 ? fmaxf(__builtin_fmaf(-2.0f, dot, nn[e] + qn), 0.0f) : -dot;
+                    if (!qvalid || t0 + lr + e >= row1) kv = kNaN;  // never selected
+                    key[rb * 16 + r] = kv;
+                    kmin = fminf(kmin, kv);
+                }
+            }
+        }
+
+        // Slow path: some lane holds a candidate at or below its query's threshold.
+        if (__ballot(kmin <= tau_k)) {
+#pragma unroll
+            for (int x = 0; x < 32; ++x) {
+                const int rb = x >> 4, r = x & 15;
+                unsigned long long m = __ballot(key[x] <= tau_k);
+                while (m) {
+                    const int src = __builtin_ctzll(m);
+                    m &= m - 1;
+                    const float ck = readlane_f(key[x], src);
+                    const int cid = (int)(t0 + rb * 32 + mfma_row(r, src >> 5));
+                    const float tk = readlane_f(tau_k, src);
+                    const int ti = readlane_i(tau_i, src);
+                    if (!cand_less(ck, cid, tk, ti)) continue;
+                    const int ql = src & 31;
+                    float nk;
+                    int ni;
+                    list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], a.kl, ck, cid, nk, ni);
+                    if (j == ql) {
+                        tau_k = nk;
+                        tau_i = ni;
+                    }
+                }
+            }
+        }
+    }
+
+    // Write this split's lists: part[q][split][0..kl)
+    const int qbase = qt * (WAVES * 32) + wave * 32;
+    for (int ql = 0; ql < 32; ++ql) {
+        const int qq = qbase + ql;
+        if (qq >= a.nq) break;
+        float* pk = a.part_keys + ((int64_t)qq * a.splits + split) * a.kl;
+        int* pi = a.part_ids + ((int64_t)qq * a.splits + split) * a.kl;
+        for (int s = lane; s < a.kl; s += 64) {
+            pk[s] = lkeys[wave][ql][s];
+            pi[s] = lids[wave][ql][s];
+        }
+    }
+}
+
+template <int KP, int WAVES>
+static hipError_t launch_scan_t(const FlatScanArgs& a, hipStream_t s) {
+    const int qpb = 32 * WAVES;
+    const int64_t qtiles = (a.nq + qpb - 1) / qpb;
+    const int64_t blocks = qtiles * a.splits;
+    hipLaunchKernelGGL((flat_scan_kernel<KP, WAVES>), dim3((unsigned)blocks), dim3(WAVES * 64), 0,
+                       s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s) {
+    switch (flat_list_capacity(a.kl)) {
+        case 16: return launch_scan_t<16, 4>(a, s);
+        case 32: return launch_scan_t<32, 4>(a, s);
+        case 64: return launch_scan_t<64, 4>(a, s);
+        default: return launch_scan_t<128, 2>(a, s);
+    }
+}
+
+// In-LDS bitonic sort (ascending by (key total-order, id)) of p = 2^x entries.
+__device__ void bitonic_sort(float* sk, int* si, int p) {
+    for (int size = 2; size <= p; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int x = threadIdx.x; x < (p >> 1); x += blockDim.x) {
+                const int lo = 2 * x - (x & (stride - 1));
+                const int hi = lo + stride;
+                const bool asc = (lo & size) == 0;
+                const float kl = sk[lo], kh = sk[hi];
+                const int il = si[lo], ih = si[hi];
+                if (cand_less(kh, ih, kl, il) == asc) {
+                    sk[lo] = kh; si[lo] = ih;
+                    sk[hi] = kl; si[hi] = il;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
+// One workgroup per query: sort all split candidates, keep the best kl, re-rank them
+// exactly (flat), sort again and emit the best k with the reference's finishing and
+// padding (flat.rs:229-237; gpu.rs:80-93 for raw keys).
+__global__ __launch_bounds__(256) void flat_merge_kernel(MergeArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char msmem[];
+    int p = 1;
+    while (p < a.width) p <<= 1;
+    float* sk = reinterpret_cast<float*>(msmem);
+    int* si = reinterpret_cast<int*>(sk + p);
+    float* rk = reinterpret_cast<float*>(si + p);
+    int* ri = reinterpret_cast<int*>(rk + kMaxList);
+
+    const int q = blockIdx.x;
+    const float kInf = __int_as_float(0x7f800000);
+    const float* pk = a.part_keys + (int64_t)q * a.width;
+    const int* pi = a.part_ids + (int64_t)q * a.width;
+    for (int x = threadIdx.x; x < p; x += blockDim.x) {
+        float kv = kInf;
+        int id = kIdNone;
+        if (x < a.width) {
+            kv = pk[x];
+            id = pi[x];
+            if (id != kIdNone && a.rowidx) id = a.rowidx[id];
+        }
+        sk[x] = kv;
+        si[x] = id;
+    }
+    bitonic_sort(sk, si, p);
+
+    int p2 = 1;
+    while (p2 < a.kl) p2 <<= 1;
+    for (int x = threadIdx.x; x < p2; x += blockDim.x) {
+        float kv = kInf;
+        int id = kIdNone;
+        if (x < a.kl && x < p) {
+            id = si[x];
+            kv = sk[x];
+            if (id != kIdNone && a.corpus) {
+                const float* qv = a.queries + (int64_t)q * a.dp;
+                const float* xv = a.corpus + (int64_t)id * a.dp;
+                kv = a.metric == 0 ? ref_l2_sqr(qv, xv, a.dim) : -ref_inner_product(qv, xv, a.dim);
+            }
+            if (id == kIdNone) kv = kInf;
+        }
+        rk[x] = kv;
+        ri[x] = id;
+    }
+    bitonic_sort(rk, ri, p2);
+
+    for (int x = threadIdx.x; x < a.k; x += blockDim.x) {
+        int64_t id = -1;
+        float d;
+        if (x < p2 && ri[x] != kIdNone) {
+            id = ri[x];
+            const float kv = rk[x];
+            d = a.raw_keys ? kv : (a.metric == 0 ? sqrtf(kv) : -kv);
+        } else {
+            d = a.raw_keys ? FLT_MAX : (a.metric == 0 ? FLT_MAX : -FLT_MAX);
+        }
+        a.out_ids[(int64_t)q * a.k + x] = id;
+        a.out_dists[(int64_t)q * a.k + x] = d;
+    }
+}
+
+hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {
+    int p = 1;
+    while (p < a.width) p <<= 1;
+    const size_t lds = (size_t)p * 8 + (size_t)kMaxList * 8;
+    hipLaunchKernelGGL(flat_merge_kernel, dim3((unsigned)a.nq), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Support kernels
+// ---------------------------------------------------------------------------
+__global__ void row_norms_kernel(const float* x, int64_t rows, int dp, float* out) {
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= rows) return;
+    const float4* v = reinterpret_cast<const float4*>(x + r * dp);
+    float s = 0.f;
+    for (int i = 0; i < (dp >> 2); ++i) {
+        const float4 t = v[i];
+        s = __builtin_fmaf(t.x, t.x, s);
+        s = __builtin_fmaf(t.y, t.y, s);
+        s = __builtin_fmaf(t.z, t.z, s);
+        s = __builtin_fmaf(t.w, t.w, s);
+    }
+    out[r] = s;
+}
+
+hipError_t launch_row_norms(const float* x, int64_t rows, int dp, float* out, hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    const int64_t blocks = (rows + 255) / 256;
+    hipLaunchKernelGGL(row_norms_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, rows, dp, out);
+    return hipGetLastError();
+}
+
+__global__ void pad_rows_kernel(const float* src, int64_t rows, int dim, int dp, float* dst) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= rows * dp) return;
+    const int64_t r = e / dp;
+    const int d = (int)(e - r * dp);
+    dst[e] = d < dim ? src[r * dim + d] : 0.f;
+}
+
+hipError_t launch_pad_rows(const float* src, int64_t rows, int dim, int dp, float* dst,
+                           hipStream_t s) {
+    if (rows <= 0) return hipSuccess;
+    const int64_t blocks = (rows * dp + 255) / 256;
+    hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, rows, dim,
+                       dp, dst);
+    return hipGetLastError();
+}
+
+// Ordered mask compaction: 4096 mask bytes per block of 256 threads (16 per thread).
+constexpr int kCompactPerBlock = 4096;
+
+int64_t mask_compact_scratch(int64_t n) {
+    return (n + kCompactPerBlock - 1) / kCompactPerBlock + 1;
+}
+
+__global__ __launch_bounds__(256) void mask_count_kernel(const uint8_t* mask, int64_t n,
+                                                         int* counts) {
+    __shared__ int wsum[4];
+    const int64_t base = (int64_t)blockIdx.x * kCompactPerBlock + threadIdx.x * 16;
+    int c = 0;
+    for (int i = 0; i < 16; ++i)
+        if (base + i < n && mask[base + i]) ++c;
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_down(c, off);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = c;
+    __syncthreads();
+    if (threadIdx.x == 0) counts[blockIdx.x] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+}
+
+// Exclusive scan of nb block counts in one workgroup; counts[nb] receives the total.
+__global__ __launch_bounds__(1024) void mask_scan_kernel(int* counts, int nb, int* d_count) {
+    __shared__ int buf[1024];
+    __shared__ int carry;
+    if (threadIdx.x == 0) carry = 0;
+    __syncthreads();
+    for (int base = 0; base < nb; base += 1024) {
+        const int i = base + threadIdx.x;
+        const int v = i < nb ? counts[i] : 0;
+        buf[threadIdx.x] = v;
+        __syncthreads();
+        for (int off = 1; off < 1024; off <<= 1) {
+            const int t = threadIdx.x >= off ? buf[threadIdx.x - off] : 0;
+            __syncthreads();
+            buf[threadIdx.x] += t;
+            __syncthreads();
+        }
+        if (i < nb) counts[i] = carry + buf[threadIdx.x] - v;
+        __syncthreads();
+        if (threadIdx.x == 1023) carry += buf[1023];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        counts[nb] = carry;
+        *d_count = carry;
+    }
+}
+
+__global__ __launch_bounds__(256) void mask_scatter_kernel(const uint8_t* mask, int64_t n,
+                                                           const int* offsets, int* rowidx) {
+    __shared__ int wsum[4];
+    const int64_t base = (int64_t)blockIdx.x * kCompactPerBlock + threadIdx.x * 16;
+    int c = 0;
+    for (int i = 0; i < 16; ++i)
+        if (base + i < n && mask[base + i]) ++c;
+    // inclusive scan of c across the workgroup
+    int incl = c;
+    const int lane = threadIdx.x & 63;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off);
+        if (lane >= off) incl += t;
+    }
+    if (lane == 63) wsum[threadIdx.x >> 6] = incl;
+    __syncthreads();
+    int wave_off = 0;
+    for (int w = 0; w < (int)(threadIdx.x >> 6); ++w) wave_off += wsum[w];
+    int out = offsets[blockIdx.x] + wave_off + incl - c;
+    for (int i = 0; i < 16; ++i)
+        if (base + i < n && mask[base + i]) rowidx[out++] = (int)(base + i);
+}
+
+hipError_t launch_mask_compact(const uint8_t* mask, int64_t n, int* rowidx, int* scratch,
+                               int* d_count, hipStream_t s) {
+    const int nb = (int)((n + kCompactPerBlock - 1) / kCompactPerBlock);
+    if (nb == 0) {
+        return hipMemsetAsync(d_count, 0, sizeof(int), s);
+    }
+    hipLaunchKernelGGL(mask_count_kernel, dim3(nb), dim3(256), 0, s, mask, n, scratch);
+    hipLaunchKernelGGL(mask_scan_kernel, dim3(1), dim3(1024), 0, s, scratch, nb, d_count);
+    hipLaunchKernelGGL(mask_scatter_kernel, dim3(nb), dim3(256), 0, s, mask, n, scratch, rowidx);
+    return hipGetLastError();
+}
+
+__global__ void copy_kernel(const float4* __restrict__ src, float4* __restrict__ dst, int64_t n4) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+         i += (int64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+hipError_t launch_copy(const float4* src, float4* dst, int64_t n4, hipStream_t s) {
+    hipLaunchKernelGGL(copy_kernel, dim3(4096), dim3(256), 0, s, src, dst, n4);
+    return hipGetLastError();
+}
+
+}  // namespace px

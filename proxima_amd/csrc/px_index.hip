@@ -1,0 +1,882 @@
+// px_index.hip -- host side of libproxima_px.so: FlatIndex / PqIndex handles and the C ABI.
+//
+// Mirrors the reference's core API (crates/core/src/flat.rs, pq.rs) and its GPU seam
+// (crates/core/src/gpu.rs:10-15, crates/core/cuda/knn.cu:123-180). Rows are appended on
+// the host and mirrored into HBM (row-major, dims padded to a multiple of 8, squared
+// norms alongside); searches run entirely on the GPU. There is no CPU search path: with
+// no gfx950 device a search fails with PX_ERR_DEVICE.
+#include "proxima_px.h"
+#include "px_host.h"
+#include "px_kernels.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cfloat>
+#include <cmath>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+#define PX_HIP(expr)                                                                        \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess)                                                               \
+            return fail((int)e_, std::string(#expr) + " failed: " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define PX_TRY(expr)             \
+    do {                         \
+        int rc_ = (expr);        \
+        if (rc_ != PX_OK) return rc_; \
+    } while (0)
+
+bool all_finite(const float* x, int64_t len) {
+    for (int64_t i = 0; i < len; ++i)
+        if (!std::isfinite(x[i])) return false;
+    return true;
+}
+
+// Grow-only device buffer.
+struct DevBuf {
+    void* p = nullptr;
+    size_t cap = 0;
+    int reserve(size_t bytes) {
+        if (bytes <= cap) return PX_OK;
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+        const size_t want = std::max<size_t>(bytes, 256);
+        PX_HIP(hipMalloc(&p, want));
+        cap = want;
+        return PX_OK;
+    }
+    void release() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        cap = 0;
+    }
+    template <class T>
+    T* as() const { return static_cast<T*>(p); }
+};
+
+struct DeviceInfo {
+    int device = -1;
+    int cus = 0;
+};
+
+// Binds the calling thread to the library's device (the one current when the first
+// handle bound it) and checks it is a gfx950.
+int bind_device(DeviceInfo& info) {
+    if (info.device >= 0) {
+        PX_HIP(hipSetDevice(info.device));
+        return PX_OK;
+    }
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count == 0)
+        return fail(PX_ERR_DEVICE, "no HIP device is visible: proxima_amd searches run only on a "
+                                   "gfx950 (MI355X) GPU and have no CPU path");
+    int dev = 0;
+    PX_HIP(hipGetDevice(&dev));
+    hipDeviceProp_t prop;
+    PX_HIP(hipGetDeviceProperties(&prop, dev));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(PX_ERR_DEVICE, std::string("device ") + std::to_string(dev) + " is " +
+                                       prop.gcnArchName + "; libproxima_px.so is built for gfx950");
+    info.device = dev;
+    info.cus = prop.multiProcessorCount;
+    return PX_OK;
+}
+
+struct Timing {
+    bool enabled = false;
+    hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
+    float scan_ms = 0.f, total_ms = 0.f;
+    int splits = 0, blocks = 0;
+    int ensure() {
+        if (!enabled) return PX_OK;
+        for (auto& e : ev)
+            if (!e) PX_HIP(hipEventCreate(&e));
+        return PX_OK;
+    }
+    void destroy() {
+        for (auto& e : ev)
+            if (e) (void)hipEventDestroy(e);
+    }
+};
+
+// Scratch shared by both index kinds for one search.
+struct Workspace {
+    DevBuf q, qn, mask, rowidx, scratch, count, part_k, part_i, out_ids, out_d;
+    int* h_count = nullptr;  // pinned
+    int ensure_pinned() {
+        if (!h_count) PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_count), sizeof(int)));
+        return PX_OK;
+    }
+    void release() {
+        for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids, &out_d})
+            b->release();
+        if (h_count) (void)hipHostFree(h_count);
+        h_count = nullptr;
+    }
+};
+
+// Compacts a device keep-mask into ascending row ids; returns the kept count in *n_eff.
+int compact_mask(Workspace& ws, const uint8_t* d_mask, int64_t n, hipStream_t s, int64_t* n_eff,
+                 const int** rowidx) {
+    PX_TRY(ws.rowidx.reserve(sizeof(int) * std::max<int64_t>(n, 1)));
+    PX_TRY(ws.scratch.reserve(sizeof(int) * px::mask_compact_scratch(n)));
+    PX_TRY(ws.count.reserve(sizeof(int)));
+    PX_TRY(ws.ensure_pinned());
+    PX_HIP(px::launch_mask_compact(d_mask, n, ws.rowidx.as<int>(), ws.scratch.as<int>(),
+                                   ws.count.as<int>(), s));
+    PX_HIP(hipMemcpyAsync(ws.h_count, ws.count.p, sizeof(int), hipMemcpyDeviceToHost, s));
+    PX_HIP(hipStreamSynchronize(s));
+    *n_eff = *ws.h_count;
+    *rowidx = ws.rowidx.as<int>();
+    return PX_OK;
+}
+
+// Number of corpus splits: enough workgroups to fill the GPU several times over, each
+// split at least min_rows long, and at most kMaxMerge candidates per query to merge.
+int choose_splits(int64_t n_eff, int64_t groups, int lists_per_split, int kl, int cus,
+                  int64_t min_rows) {
+    const int64_t target = 8LL * std::max(cus, 1);
+    int64_t s = (target + groups - 1) / std::max<int64_t>(groups, 1);
+    s = std::min<int64_t>(s, std::max<int64_t>(1, n_eff / std::max<int64_t>(min_rows, 1)));
+    s = std::min<int64_t>(s, px::kMaxMerge / std::max(1, lists_per_split * kl));
+    if (s >= 8) s = s / 8 * 8;  // consecutive blocks share a query tile; 8 XCDs
+    return (int)std::max<int64_t>(s, 1);
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------
+// Handles
+// ---------------------------------------------------------------------------------------
+struct px_flat {
+    int metric = 0;
+    int64_t dim = 0, dp = 0;
+    int64_t n = 0;                 // rows held (device + pending)
+    std::vector<float> pending;    // rows not yet mirrored, [rows][dim]
+    DeviceInfo dev;
+    hipStream_t stream = nullptr;
+    float* d_x = nullptr;          // [cap][dp]
+    float* d_norm = nullptr;       // [cap]
+    int64_t d_rows = 0, d_cap = 0;
+    Workspace ws;
+    Timing timing;
+    std::mutex mu;
+};
+
+struct px_pq {
+    int metric = 0;
+    int64_t dim = 0, m = 0, nbits = 0, ks = 0, dsub = 0;
+    bool trained = false;
+    std::vector<float> codebooks;  // [m][ks][dsub]
+    std::vector<uint8_t> codes;    // host copy of every code row, [n][m]
+    int64_t n = 0;
+    DeviceInfo dev;
+    hipStream_t stream = nullptr;
+    float* d_books = nullptr;
+    bool books_on_device = false;
+    uint8_t* d_codes = nullptr;
+    int64_t d_rows = 0, d_cap = 0;
+    Workspace ws;
+    Timing timing;
+    std::mutex mu;
+};
+
+struct PxGpuIndex {
+    px_flat* flat[2] = {nullptr, nullptr};  // one handle per metric, sharing nothing
+    const float* base = nullptr;
+};
+
+namespace {
+
+int flat_bind(px_flat* f) {
+    PX_TRY(bind_device(f->dev));
+    if (!f->stream) PX_HIP(hipStreamCreateWithFlags(&f->stream, hipStreamNonBlocking));
+    return PX_OK;
+}
+
+// Mirror pending rows into HBM: grow (doubling) if needed, upload with padding, norms.
+int flat_sync(px_flat* f) {
+    const int64_t add = (int64_t)(f->pending.size() / f->dim);
+    if (add == 0) return PX_OK;
+    PX_TRY(flat_bind(f));
+    const int64_t need = f->d_rows + add;
+    if (need > f->d_cap) {
+        const int64_t cap = std::max<int64_t>({need, f->d_cap * 2, 1024});
+        float *nx = nullptr, *nn = nullptr;
+        PX_HIP(hipMalloc(&nx, sizeof(float) * cap * f->dp));
+        if (hipMalloc(&nn, sizeof(float) * cap) != hipSuccess) {
+            (void)hipFree(nx);
+            return fail(hipErrorOutOfMemory, "hipMalloc of the corpus norms failed");
+        }
+        if (f->d_rows) {
+            PX_HIP(hipMemcpyAsync(nx, f->d_x, sizeof(float) * f->d_rows * f->dp,
+                                  hipMemcpyDeviceToDevice, f->stream));
+            PX_HIP(hipMemcpyAsync(nn, f->d_norm, sizeof(float) * f->d_rows,
+                                  hipMemcpyDeviceToDevice, f->stream));
+        }
+        PX_HIP(hipStreamSynchronize(f->stream));
+        if (f->d_x) (void)hipFree(f->d_x);
+        if (f->d_norm) (void)hipFree(f->d_norm);
+        f->d_x = nx;
+        f->d_norm = nn;
+        f->d_cap = cap;
+    }
+    float* dst = f->d_x + f->d_rows * f->dp;
+    if (f->dp != f->dim)
+        PX_HIP(hipMemsetAsync(dst, 0, sizeof(float) * add * f->dp, f->stream));
+    PX_HIP(hipMemcpy2DAsync(dst, sizeof(float) * f->dp, f->pending.data(), sizeof(float) * f->dim,
+                            sizeof(float) * f->dim, add, hipMemcpyHostToDevice, f->stream));
+    PX_HIP(px::launch_row_norms(dst, add, (int)f->dp, f->d_norm + f->d_rows, f->stream));
+    PX_HIP(hipStreamSynchronize(f->stream));
+    f->d_rows = need;
+    std::vector<float>().swap(f->pending);
+    return PX_OK;
+}
+
+// Runs the device pipeline. d_q: [nq][dp] on device. Outputs on device.
+int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
+             int64_t* d_ids, float* d_out, int raw_keys) {
+    Workspace& ws = f->ws;
+    hipStream_t s = f->stream;
+    int64_t n_eff = f->d_rows;
+    const int* rowidx = nullptr;
+    if (d_mask) PX_TRY(compact_mask(ws, d_mask, f->d_rows, s, &n_eff, &rowidx));
+
+    const int kl = (int)std::min<int64_t>(px::kMaxList, k + 8);
+    const int kp = px::flat_list_capacity(kl);
+    const int64_t qpb = px::flat_queries_per_block(kp);
+    const int64_t groups = (nq + qpb - 1) / qpb;
+    int splits = choose_splits(n_eff, groups, 1, kl, f->dev.cus, 256);
+    int64_t rps = (n_eff + splits - 1) / splits;
+    rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
+    splits = (int)std::max<int64_t>(1, (n_eff + rps - 1) / rps);
+
+    PX_TRY(ws.part_k.reserve(sizeof(float) * nq * splits * kl));
+    PX_TRY(ws.part_i.reserve(sizeof(int) * nq * splits * kl));
+    if (f->metric == 0) {
+        PX_TRY(ws.qn.reserve(sizeof(float) * nq));
+        PX_HIP(px::launch_row_norms(d_q, nq, (int)f->dp, ws.qn.as<float>(), s));
+    }
+    PX_TRY(f->timing.ensure());
+    if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[0], s));
+
+    px::FlatScanArgs a{};
+    a.corpus = f->d_x;
+    a.norms = f->d_norm;
+    a.queries = d_q;
+    a.qnorms = ws.qn.as<float>();
+    a.rowidx = rowidx;
+    a.n_eff = n_eff;
+    a.rows_per_split = rps;
+    a.dp = (int)f->dp;
+    a.nq = (int)nq;
+    a.kl = kl;
+    a.splits = splits;
+    a.metric = f->metric;
+    a.part_keys = ws.part_k.as<float>();
+    a.part_ids = ws.part_i.as<int>();
+    if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
+    if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[1], s));
+
+    px::MergeArgs mg{};
+    mg.part_keys = a.part_keys;
+    mg.part_ids = a.part_ids;
+    mg.rowidx = rowidx;
+    mg.width = n_eff > 0 ? splits * kl : 0;
+    mg.nq = (int)nq;
+    mg.kl = kl;
+    mg.k = (int)k;
+    mg.metric = f->metric;
+    mg.corpus = f->d_x;
+    mg.queries = d_q;
+    mg.dim = (int)f->dim;
+    mg.dp = (int)f->dp;
+    mg.out_ids = d_ids;
+    mg.out_dists = d_out;
+    mg.raw_keys = raw_keys;
+    PX_HIP(px::launch_merge(mg, s));
+    if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[2], s));
+    PX_HIP(hipStreamSynchronize(s));
+    if (f->timing.enabled) {
+        PX_HIP(hipEventElapsedTime(&f->timing.scan_ms, f->timing.ev[0], f->timing.ev[1]));
+        PX_HIP(hipEventElapsedTime(&f->timing.total_ms, f->timing.ev[0], f->timing.ev[2]));
+        f->timing.splits = splits;
+        f->timing.blocks = (int)(groups * splits);
+    }
+    return PX_OK;
+}
+
+void host_padding(int metric, int64_t nq, int64_t k, int64_t* ids, float* out, int raw_keys) {
+    for (int64_t i = 0; i < nq * k; ++i) {
+        ids[i] = -1;
+        out[i] = raw_keys ? FLT_MAX : (metric == 0 ? FLT_MAX : -FLT_MAX);
+    }
+}
+
+int check_search_args(const void* idx, const void* queries, int64_t nq, int64_t k,
+                      const void* ids, const void* dists) {
+    if (!idx) return fail(PX_ERR_ARG, "null index handle");
+    if (nq < 0) return fail(PX_ERR_ARG, "nq must be >= 0");
+    if (k < 0) return fail(PX_ERR_BAD_K, "k must be >= 0");
+    if (k > PX_MAX_K)
+        return fail(PX_ERR_BAD_K, "k=" + std::to_string(k) + " exceeds the GPU kernels' limit of " +
+                                      std::to_string(PX_MAX_K));
+    if (k > 0 && nq > 0 && (!queries || !ids || !dists))
+        return fail(PX_ERR_ARG, "null query or output pointer");
+    return PX_OK;
+}
+
+// Host-pointer search: upload, run, download.
+int flat_search_host(px_flat* f, const float* queries, int64_t nq, int64_t k, const uint8_t* mask,
+                     int64_t* out_ids, float* out_d, int raw_keys) {
+    if (!all_finite(queries, nq * f->dim))
+        return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
+    std::lock_guard<std::mutex> lock(f->mu);
+    if (f->n == 0) {
+        host_padding(f->metric, nq, k, out_ids, out_d, raw_keys);
+        return PX_OK;
+    }
+    PX_TRY(flat_sync(f));
+    Workspace& ws = f->ws;
+    hipStream_t s = f->stream;
+    PX_TRY(ws.q.reserve(sizeof(float) * nq * f->dp));
+    if (f->dp != f->dim) PX_HIP(hipMemsetAsync(ws.q.p, 0, sizeof(float) * nq * f->dp, s));
+    PX_HIP(hipMemcpy2DAsync(ws.q.p, sizeof(float) * f->dp, queries, sizeof(float) * f->dim,
+                            sizeof(float) * f->dim, nq, hipMemcpyHostToDevice, s));
+    const uint8_t* d_mask = nullptr;
+    if (mask) {
+        PX_TRY(ws.mask.reserve(f->d_rows));
+        PX_HIP(hipMemcpyAsync(ws.mask.p, mask, f->d_rows, hipMemcpyHostToDevice, s));
+        d_mask = ws.mask.as<uint8_t>();
+    }
+    PX_TRY(ws.out_ids.reserve(sizeof(int64_t) * nq * k));
+    PX_TRY(ws.out_d.reserve(sizeof(float) * nq * k));
+    PX_TRY(flat_run(f, ws.q.as<float>(), nq, k, d_mask, ws.out_ids.as<int64_t>(),
+                    ws.out_d.as<float>(), raw_keys));
+    PX_HIP(hipMemcpyAsync(out_ids, ws.out_ids.p, sizeof(int64_t) * nq * k, hipMemcpyDeviceToHost, s));
+    PX_HIP(hipMemcpyAsync(out_d, ws.out_d.p, sizeof(float) * nq * k, hipMemcpyDeviceToHost, s));
+    PX_HIP(hipStreamSynchronize(s));
+    return PX_OK;
+}
+
+// ---- PQ ----------------------------------------------------------------------------
+int pq_bind(px_pq* p) {
+    PX_TRY(bind_device(p->dev));
+    if (!p->stream) PX_HIP(hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking));
+    return PX_OK;
+}
+
+int pq_sync(px_pq* p) {
+    PX_TRY(pq_bind(p));
+    if (!p->books_on_device) {
+        if (!p->d_books) PX_HIP(hipMalloc(&p->d_books, sizeof(float) * p->codebooks.size()));
+        PX_HIP(hipMemcpyAsync(p->d_books, p->codebooks.data(), sizeof(float) * p->codebooks.size(),
+                              hipMemcpyHostToDevice, p->stream));
+        PX_HIP(hipStreamSynchronize(p->stream));
+        p->books_on_device = true;
+    }
+    const int64_t add = p->n - p->d_rows;
+    if (add <= 0) return PX_OK;
+    if (p->n > p->d_cap) {
+        const int64_t cap = std::max<int64_t>({p->n, p->d_cap * 2, 4096});
+        uint8_t* nc = nullptr;
+        PX_HIP(hipMalloc(&nc, (size_t)(cap * p->m)));
+        if (p->d_rows)
+            PX_HIP(hipMemcpyAsync(nc, p->d_codes, (size_t)(p->d_rows * p->m),
+                                  hipMemcpyDeviceToDevice, p->stream));
+        PX_HIP(hipStreamSynchronize(p->stream));
+        if (p->d_codes) (void)hipFree(p->d_codes);
+        p->d_codes = nc;
+        p->d_cap = cap;
+    }
+    PX_HIP(hipMemcpyAsync(p->d_codes + p->d_rows * p->m, p->codes.data() + p->d_rows * p->m,
+                          (size_t)(add * p->m), hipMemcpyHostToDevice, p->stream));
+    PX_HIP(hipStreamSynchronize(p->stream));
+    p->d_rows = p->n;
+    return PX_OK;
+}
+
+int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
+           int64_t* d_ids, float* d_out) {
+    Workspace& ws = p->ws;
+    hipStream_t s = p->stream;
+    int64_t n_eff = p->d_rows;
+    const int* rowidx = nullptr;
+    if (d_mask) PX_TRY(compact_mask(ws, d_mask, p->d_rows, s, &n_eff, &rowidx));
+
+    const int kl = (int)k;
+    const int lists = px::pq_lists_per_split();
+    const int64_t qpb = px::pq_queries_per_block((int)p->m, (int)p->ks);
+    const int64_t groups = (nq + qpb - 1) / qpb;
+    int splits = choose_splits(n_eff, groups, lists, kl, p->dev.cus, 4096);
+    int64_t rps = (n_eff + splits - 1) / splits;
+    rps = std::max<int64_t>((rps + 255) / 256 * 256, 256);
+    splits = (int)std::max<int64_t>(1, (n_eff + rps - 1) / rps);
+    const int64_t width = (int64_t)splits * lists * kl;
+
+    PX_TRY(ws.part_k.reserve(sizeof(float) * nq * width));
+    PX_TRY(ws.part_i.reserve(sizeof(int) * nq * width));
+    PX_TRY(p->timing.ensure());
+    if (p->timing.enabled) PX_HIP(hipEventRecord(p->timing.ev[0], s));
+    px::PqScanArgs a{};
+    a.codes = p->d_codes;
+    a.codebooks = p->d_books;
+    a.queries = d_q;
+    a.rowidx = rowidx;
+    a.n_eff = n_eff;
+    a.rows_per_split = rps;
+    a.dim = (int)p->dim;
+    a.m = (int)p->m;
+    a.ks = (int)p->ks;
+    a.dsub = (int)p->dsub;
+    a.nq = (int)nq;
+    a.kl = kl;
+    a.splits = splits;
+    a.metric = p->metric;
+    a.part_keys = ws.part_k.as<float>();
+    a.part_ids = ws.part_i.as<int>();
+    if (n_eff > 0) PX_HIP(px::launch_pq_scan(a, s));
+    if (p->timing.enabled) PX_HIP(hipEventRecord(p->timing.ev[1], s));
+
+    px::MergeArgs mg{};
+    mg.part_keys = a.part_keys;
+    mg.part_ids = a.part_ids;
+    mg.rowidx = rowidx;
+    mg.width = n_eff > 0 ? (int)width : 0;
+    mg.nq = (int)nq;
+    mg.kl = kl;
+    mg.k = (int)k;
+    mg.metric = p->metric;
+    mg.corpus = nullptr;  // ADC keys are already the reference's
+    mg.out_ids = d_ids;
+    mg.out_dists = d_out;
+    mg.raw_keys = 0;
+    PX_HIP(px::launch_merge(mg, s));
+    if (p->timing.enabled) PX_HIP(hipEventRecord(p->timing.ev[2], s));
+    PX_HIP(hipStreamSynchronize(s));
+    if (p->timing.enabled) {
+        PX_HIP(hipEventElapsedTime(&p->timing.scan_ms, p->timing.ev[0], p->timing.ev[1]));
+        PX_HIP(hipEventElapsedTime(&p->timing.total_ms, p->timing.ev[0], p->timing.ev[2]));
+        p->timing.splits = splits;
+        p->timing.blocks = (int)(groups * splits);
+    }
+    return PX_OK;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------------------
+extern "C" {
+
+const char* px_last_error(void) { return g_err.c_str(); }
+const char* px_version(void) { return "0.1.0"; }
+
+int px_flat_create(int metric, int64_t dim, px_flat** out) {
+    if (!out) return fail(PX_ERR_ARG, "null output handle pointer");
+    *out = nullptr;
+    if (metric != 0 && metric != 1) return fail(PX_ERR_ARG, "metric must be 0 (L2) or 1 (InnerProduct)");
+    if (dim <= 0) return fail(PX_ERR_DIM, "dim must be > 0");
+    px_flat* f = new (std::nothrow) px_flat();
+    if (!f) return fail(PX_ERR_ARG, "out of host memory");
+    f->metric = metric;
+    f->dim = dim;
+    f->dp = px::padded_dim(dim);
+    *out = f;
+    return PX_OK;
+}
+
+void px_flat_destroy(px_flat* f) {
+    if (!f) return;
+    if (f->dev.device >= 0) {
+        (void)hipSetDevice(f->dev.device);
+        if (f->stream) (void)hipStreamSynchronize(f->stream);
+        if (f->d_x) (void)hipFree(f->d_x);
+        if (f->d_norm) (void)hipFree(f->d_norm);
+        f->ws.release();
+        f->timing.destroy();
+        if (f->stream) (void)hipStreamDestroy(f->stream);
+    }
+    delete f;
+}
+
+int px_flat_add(px_flat* f, const float* vectors, int64_t n) {
+    if (!f) return fail(PX_ERR_ARG, "null index handle");
+    if (n < 0 || (n > 0 && !vectors)) return fail(PX_ERR_ARG, "bad vectors pointer or count");
+    if (n == 0) return PX_OK;
+    if (!all_finite(vectors, n * f->dim))
+        return fail(PX_ERR_NONFINITE, "vectors must not contain NaN or infinite values");
+    if (f->n + n > (int64_t)INT32_MAX - 1)
+        return fail(PX_ERR_ARG, "index would exceed 2^31 - 2 rows");
+    std::lock_guard<std::mutex> lock(f->mu);
+    f->pending.insert(f->pending.end(), vectors, vectors + n * f->dim);
+    f->n += n;
+    if (px_device_count() > 0) PX_TRY(flat_sync(f));
+    return PX_OK;
+}
+
+int px_flat_search(const px_flat* cf, const float* queries, int64_t nq, int64_t k,
+                   const uint8_t* mask, int64_t* out_ids, float* out_dists) {
+    PX_TRY(check_search_args(cf, queries, nq, k, out_ids, out_dists));
+    if (k == 0 || nq == 0) return PX_OK;
+    return flat_search_host(const_cast<px_flat*>(cf), queries, nq, k, mask, out_ids, out_dists, 0);
+}
+
+int px_flat_search_device(const px_flat* cf, const float* d_queries, int64_t nq, int64_t k,
+                          const uint8_t* d_mask, int64_t* d_ids, float* d_dists) {
+    PX_TRY(check_search_args(cf, d_queries, nq, k, d_ids, d_dists));
+    if (k == 0 || nq == 0) return PX_OK;
+    px_flat* f = const_cast<px_flat*>(cf);
+    std::lock_guard<std::mutex> lock(f->mu);
+    PX_TRY(flat_bind(f));
+    PX_TRY(flat_sync(f));
+    const float* q = d_queries;
+    if (f->dp != f->dim) {
+        PX_TRY(f->ws.q.reserve(sizeof(float) * nq * f->dp));
+        PX_HIP(px::launch_pad_rows(d_queries, nq, (int)f->dim, (int)f->dp, f->ws.q.as<float>(), f->stream));
+        q = f->ws.q.as<float>();
+    }
+    return flat_run(f, q, nq, k, f->d_rows ? d_mask : nullptr, d_ids, d_dists, 0);
+}
+
+int px_flat_get_vectors(const px_flat* cf, int64_t first, int64_t n, float* out) {
+    if (!cf || (n > 0 && !out)) return fail(PX_ERR_ARG, "null argument");
+    if (first < 0 || n < 0 || first + n > cf->n) return fail(PX_ERR_ARG, "row range out of bounds");
+    if (n == 0) return PX_OK;
+    px_flat* f = const_cast<px_flat*>(cf);
+    std::lock_guard<std::mutex> lock(f->mu);
+    // rows [0, d_rows) live in HBM (padded pitch), the rest in the host pending buffer
+    const int64_t dev_hi = std::min(first + n, f->d_rows);
+    if (first < dev_hi) {
+        PX_TRY(flat_bind(f));
+        PX_HIP(hipMemcpy2DAsync(out, sizeof(float) * f->dim, f->d_x + first * f->dp,
+                                sizeof(float) * f->dp, sizeof(float) * f->dim, dev_hi - first,
+                                hipMemcpyDeviceToHost, f->stream));
+        PX_HIP(hipStreamSynchronize(f->stream));
+    }
+    for (int64_t r = std::max(first, f->d_rows); r < first + n; ++r)
+        std::memcpy(out + (r - first) * f->dim, f->pending.data() + (r - f->d_rows) * f->dim,
+                    sizeof(float) * f->dim);
+    return PX_OK;
+}
+
+int64_t px_flat_size(const px_flat* f) { return f ? f->n : 0; }
+int64_t px_flat_dim(const px_flat* f) { return f ? f->dim : 0; }
+int px_flat_metric(const px_flat* f) { return f ? f->metric : -1; }
+int64_t px_flat_memory_bytes(const px_flat* f) {
+    return f ? f->n * f->dim * (int64_t)sizeof(float) : 0;
+}
+
+int px_flat_set_timing(px_flat* f, int enable) {
+    if (!f) return fail(PX_ERR_ARG, "null index handle");
+    f->timing.enabled = enable != 0;
+    return PX_OK;
+}
+
+int px_flat_last_timing(const px_flat* f, float* scan_ms, float* total_ms, int* splits,
+                        int* blocks) {
+    if (!f) return fail(PX_ERR_ARG, "null index handle");
+    if (scan_ms) *scan_ms = f->timing.scan_ms;
+    if (total_ms) *total_ms = f->timing.total_ms;
+    if (splits) *splits = f->timing.splits;
+    if (blocks) *blocks = f->timing.blocks;
+    return PX_OK;
+}
+
+// ---- reference GPU seam (gpu.rs:10-15) ------------------------------------------------
+PxGpuIndex* knn_gpu_create(const float* base, int n, int dim) {
+    if (!base || n < 0 || dim <= 0) return nullptr;
+    PxGpuIndex* g = new (std::nothrow) PxGpuIndex();
+    if (!g) return nullptr;
+    for (int metric = 0; metric < 2; ++metric) {
+        if (px_flat_create(metric, dim, &g->flat[metric]) != PX_OK ||
+            px_flat_add(g->flat[metric], base, n) != PX_OK) {
+            knn_gpu_free(g);
+            return nullptr;
+        }
+    }
+    return g;
+}
+
+int knn_gpu_search(const PxGpuIndex* g, const float* queries, int nq, int k, int metric,
+                   long long* out_ids, float* out_keys) {
+    if (!g) return fail(PX_ERR_ARG, "null index handle");
+    if (k < 1 || k > PX_MAX_K) return fail(PX_ERR_BAD_K, "k out of range");  // knn.cu:145
+    if (nq <= 0) return PX_OK;
+    px_flat* f = g->flat[metric == 0 ? 0 : 1];
+    PX_TRY(check_search_args(f, queries, nq, k, out_ids, out_keys));
+    return flat_search_host(f, queries, nq, k, nullptr, reinterpret_cast<int64_t*>(out_ids),
+                            out_keys, 1);
+}
+
+void knn_gpu_free(PxGpuIndex* g) {
+    if (!g) return;
+    px_flat_destroy(g->flat[0]);
+    px_flat_destroy(g->flat[1]);
+    delete g;
+}
+
+// ---- PQ ------------------------------------------------------------------------------
+int px_pq_create(int metric, int64_t dim, int64_t m, int64_t nbits, px_pq** out) {
+    if (!out) return fail(PX_ERR_ARG, "null output handle pointer");
+    *out = nullptr;
+    if (metric != 0 && metric != 1) return fail(PX_ERR_ARG, "metric must be 0 (L2) or 1 (InnerProduct)");
+    if (m < 1) return fail(PX_ERR_ARG, "m must be >= 1");
+    if (dim <= 0 || dim % m != 0) return fail(PX_ERR_DIM, "dim must be > 0 and divisible by m");
+    if (nbits < 1 || nbits > 8) return fail(PX_ERR_ARG, "nbits must be in 1..=8");
+    px_pq* p = new (std::nothrow) px_pq();
+    if (!p) return fail(PX_ERR_ARG, "out of host memory");
+    p->metric = metric;
+    p->dim = dim;
+    p->m = m;
+    p->nbits = nbits;
+    p->ks = (int64_t)1 << nbits;
+    p->dsub = dim / m;
+    *out = p;
+    return PX_OK;
+}
+
+void px_pq_destroy(px_pq* p) {
+    if (!p) return;
+    if (p->dev.device >= 0) {
+        (void)hipSetDevice(p->dev.device);
+        if (p->stream) (void)hipStreamSynchronize(p->stream);
+        if (p->d_books) (void)hipFree(p->d_books);
+        if (p->d_codes) (void)hipFree(p->d_codes);
+        p->ws.release();
+        p->timing.destroy();
+        if (p->stream) (void)hipStreamDestroy(p->stream);
+    }
+    delete p;
+}
+
+int px_pq_train(px_pq* p, const float* training, int64_t n, int64_t train_iters,
+                int64_t train_sample, uint64_t seed) {
+    if (!p) return fail(PX_ERR_ARG, "null index handle");
+    if (n < 0 || (n > 0 && !training) || train_iters < 0 || train_sample < 0)
+        return fail(PX_ERR_ARG, "bad training arguments");
+    if (n < p->ks)
+        return fail(PX_ERR_ARG, "training set too small: need at least " + std::to_string(p->ks) +
+                                    " rows for nbits=" + std::to_string(p->nbits) + ", got " +
+                                    std::to_string(n));
+    if (!all_finite(training, n * p->dim))
+        return fail(PX_ERR_NONFINITE, "training data must not contain NaN or infinite values");
+    std::vector<float> books((size_t)(p->m * p->ks * p->dsub));
+    px::pq_train_host(training, n, p->dim, p->m, p->nbits, train_iters, train_sample, seed,
+                      books.data());
+    std::lock_guard<std::mutex> lock(p->mu);
+    p->codebooks.swap(books);
+    p->trained = true;
+    p->books_on_device = false;
+    p->codes.clear();  // PqIndex::train builds a fresh index (pq.rs:226-229)
+    p->n = 0;
+    p->d_rows = 0;
+    return PX_OK;
+}
+
+int px_pq_set_codebooks(px_pq* p, const float* codebooks) {
+    if (!p || !codebooks) return fail(PX_ERR_ARG, "null argument");
+    const size_t len = (size_t)(p->m * p->ks * p->dsub);
+    if (!all_finite(codebooks, (int64_t)len))
+        return fail(PX_ERR_NONFINITE, "codebooks must not contain NaN or infinite values");
+    std::lock_guard<std::mutex> lock(p->mu);
+    p->codebooks.assign(codebooks, codebooks + len);
+    p->trained = true;
+    p->books_on_device = false;
+    return PX_OK;
+}
+
+int px_pq_get_codebooks(const px_pq* p, float* out) {
+    if (!p || !out) return fail(PX_ERR_ARG, "null argument");
+    if (!p->trained) return fail(PX_ERR_UNTRAINED, "index is not trained");
+    std::memcpy(out, p->codebooks.data(), sizeof(float) * p->codebooks.size());
+    return PX_OK;
+}
+
+int px_pq_add(px_pq* p, const float* vectors, int64_t n) {
+    if (!p) return fail(PX_ERR_ARG, "null index handle");
+    if (!p->trained) return fail(PX_ERR_UNTRAINED, "index is not trained; call train() first");
+    if (n < 0 || (n > 0 && !vectors)) return fail(PX_ERR_ARG, "bad vectors pointer or count");
+    if (n == 0) return PX_OK;
+    if (!all_finite(vectors, n * p->dim))
+        return fail(PX_ERR_NONFINITE, "vectors must not contain NaN or infinite values");
+    std::vector<uint8_t> codes((size_t)(n * p->m));
+    px::pq_encode_host(p->codebooks.data(), p->dim, p->m, p->nbits, vectors, n, codes.data());
+    return px_pq_add_codes(p, codes.data(), n);
+}
+
+int px_pq_add_codes(px_pq* p, const uint8_t* codes, int64_t n) {
+    if (!p) return fail(PX_ERR_ARG, "null index handle");
+    if (!p->trained) return fail(PX_ERR_UNTRAINED, "index is not trained; call train() first");
+    if (n < 0 || (n > 0 && !codes)) return fail(PX_ERR_ARG, "bad codes pointer or count");
+    if (n == 0) return PX_OK;
+    if (p->n + n > (int64_t)INT32_MAX - 1) return fail(PX_ERR_ARG, "index would exceed 2^31 - 2 rows");
+    for (int64_t i = 0; i < n * p->m; ++i)
+        if (codes[i] >= p->ks) return fail(PX_ERR_ARG, "code value out of range for nbits");
+    std::lock_guard<std::mutex> lock(p->mu);
+    p->codes.insert(p->codes.end(), codes, codes + n * p->m);
+    p->n += n;
+    if (px_device_count() > 0) PX_TRY(pq_sync(p));
+    return PX_OK;
+}
+
+int px_pq_get_codes(const px_pq* p, int64_t first, int64_t n, uint8_t* out) {
+    if (!p || (n > 0 && !out)) return fail(PX_ERR_ARG, "null argument");
+    if (first < 0 || n < 0 || first + n > p->n) return fail(PX_ERR_ARG, "code range out of bounds");
+    std::memcpy(out, p->codes.data() + first * p->m, (size_t)(n * p->m));
+    return PX_OK;
+}
+
+int px_pq_search(const px_pq* cp, const float* queries, int64_t nq, int64_t k,
+                 const uint8_t* mask, int64_t* out_ids, float* out_dists) {
+    PX_TRY(check_search_args(cp, queries, nq, k, out_ids, out_dists));
+    px_pq* p = const_cast<px_pq*>(cp);
+    if (!p->trained) return fail(PX_ERR_UNTRAINED, "index is not trained");
+    if (k == 0 || nq == 0) return PX_OK;
+    if (!all_finite(queries, nq * p->dim))
+        return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
+    std::lock_guard<std::mutex> lock(p->mu);
+    if (p->n == 0) {
+        host_padding(p->metric, nq, k, out_ids, out_dists, 0);
+        return PX_OK;
+    }
+    PX_TRY(pq_sync(p));
+    Workspace& ws = p->ws;
+    hipStream_t s = p->stream;
+    PX_TRY(ws.q.reserve(sizeof(float) * nq * p->dim));
+    PX_HIP(hipMemcpyAsync(ws.q.p, queries, sizeof(float) * nq * p->dim, hipMemcpyHostToDevice, s));
+    const uint8_t* d_mask = nullptr;
+    if (mask) {
+        PX_TRY(ws.mask.reserve(p->d_rows));
+        PX_HIP(hipMemcpyAsync(ws.mask.p, mask, p->d_rows, hipMemcpyHostToDevice, s));
+        d_mask = ws.mask.as<uint8_t>();
+    }
+    PX_TRY(ws.out_ids.reserve(sizeof(int64_t) * nq * k));
+    PX_TRY(ws.out_d.reserve(sizeof(float) * nq * k));
+    PX_TRY(pq_run(p, ws.q.as<float>(), nq, k, d_mask, ws.out_ids.as<int64_t>(), ws.out_d.as<float>()));
+    PX_HIP(hipMemcpyAsync(out_ids, ws.out_ids.p, sizeof(int64_t) * nq * k, hipMemcpyDeviceToHost, s));
+    PX_HIP(hipMemcpyAsync(out_dists, ws.out_d.p, sizeof(float) * nq * k, hipMemcpyDeviceToHost, s));
+    PX_HIP(hipStreamSynchronize(s));
+    return PX_OK;
+}
+
+int px_pq_search_device(const px_pq* cp, const float* d_queries, int64_t nq, int64_t k,
+                        const uint8_t* d_mask, int64_t* d_ids, float* d_dists) {
+    PX_TRY(check_search_args(cp, d_queries, nq, k, d_ids, d_dists));
+    px_pq* p = const_cast<px_pq*>(cp);
+    if (!p->trained) return fail(PX_ERR_UNTRAINED, "index is not trained");
+    if (k == 0 || nq == 0) return PX_OK;
+    std::lock_guard<std::mutex> lock(p->mu);
+    PX_TRY(pq_sync(p));
+    return pq_run(p, d_queries, nq, k, p->d_rows ? d_mask : nullptr, d_ids, d_dists);
+}
+
+int px_pq_is_trained(const px_pq* p) { return p && p->trained ? 1 : 0; }
+int64_t px_pq_size(const px_pq* p) { return p ? p->n : 0; }
+int64_t px_pq_dim(const px_pq* p) { return p ? p->dim : 0; }
+int64_t px_pq_m(const px_pq* p) { return p ? p->m : 0; }
+int64_t px_pq_nbits(const px_pq* p) { return p ? p->nbits : 0; }
+int px_pq_metric(const px_pq* p) { return p ? p->metric : -1; }
+int64_t px_pq_memory_bytes(const px_pq* p) {
+    if (!p || !p->trained) return 0;
+    return p->n * p->m + (int64_t)(p->codebooks.size() * sizeof(float));
+}
+int64_t px_pq_raw_bytes(const px_pq* p) {
+    return p && p->trained ? p->n * p->dim * (int64_t)sizeof(float) : 0;
+}
+
+int px_pq_set_timing(px_pq* p, int enable) {
+    if (!p) return fail(PX_ERR_ARG, "null index handle");
+    p->timing.enabled = enable != 0;
+    return PX_OK;
+}
+
+int px_pq_last_timing(const px_pq* p, float* scan_ms, float* total_ms, int* splits, int* blocks) {
+    if (!p) return fail(PX_ERR_ARG, "null index handle");
+    if (scan_ms) *scan_ms = p->timing.scan_ms;
+    if (total_ms) *total_ms = p->timing.total_ms;
+    if (splits) *splits = p->timing.splits;
+    if (blocks) *blocks = p->timing.blocks;
+    return PX_OK;
+}
+
+// ---- device info and plumbing ---------------------------------------------------------
+int px_device_count(void) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess) return 0;
+    return count;
+}
+
+int px_device_info(int device, char* name, size_t name_len, int* cu_count, int64_t* hbm_bytes,
+                   int* clock_khz, char* arch, size_t arch_len) {
+    if (px_device_count() <= device || device < 0)
+        return fail(PX_ERR_DEVICE, "no such HIP device");
+    hipDeviceProp_t prop;
+    PX_HIP(hipGetDeviceProperties(&prop, device));
+    if (name && name_len) {
+        std::strncpy(name, prop.name, name_len - 1);
+        name[name_len - 1] = 0;
+    }
+    if (arch && arch_len) {
+        std::strncpy(arch, prop.gcnArchName, arch_len - 1);
+        arch[arch_len - 1] = 0;
+    }
+    if (cu_count) *cu_count = prop.multiProcessorCount;
+    if (hbm_bytes) *hbm_bytes = (int64_t)prop.totalGlobalMem;
+    if (clock_khz) *clock_khz = prop.clockRate;
+    return PX_OK;
+}
+
+int px_dev_alloc(void** ptr, size_t bytes) {
+    if (!ptr) return fail(PX_ERR_ARG, "null pointer");
+    PX_HIP(hipMalloc(ptr, bytes));
+    return PX_OK;
+}
+int px_dev_free(void* ptr) {
+    PX_HIP(hipFree(ptr));
+    return PX_OK;
+}
+int px_dev_upload(void* dst, const void* src, size_t bytes) {
+    PX_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return PX_OK;
+}
+int px_dev_download(void* dst, const void* src, size_t bytes) {
+    PX_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return PX_OK;
+}
+int px_dev_copy_kernel(void* dst, const void* src, size_t bytes, float* ms) {
+    if (bytes % 16) return fail(PX_ERR_ARG, "bytes must be a multiple of 16");
+    hipEvent_t e0, e1;
+    PX_HIP(hipEventCreate(&e0));
+    PX_HIP(hipEventCreate(&e1));
+    PX_HIP(hipEventRecord(e0, nullptr));
+    PX_HIP(px::launch_copy(static_cast<const float4*>(src), static_cast<float4*>(dst),
+                           (int64_t)(bytes / 16), nullptr));
+    PX_HIP(hipEventRecord(e1, nullptr));
+    PX_HIP(hipEventSynchronize(e1));
+    float t = 0.f;
+    PX_HIP(hipEventElapsedTime(&t, e0, e1));
+    if (ms) *ms = t;
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return PX_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,175 @@
+// px_pq.hip -- PqIndex ADC scan for gfx950.
+//
+// Replaces crates/core/src/pq.rs:299-347 (per query: build the m x 2^nbits LUT, sum m
+// LUT entries per code row, heap top-k). A workgroup holds the LUTs of QPB queries in
+// LDS (built in the reference's exact arithmetic, pq.rs:123-136), streams code rows with
+// one coalesced 16-byte load per row (m = 16), and sums each row's m lookups in
+// subspace order starting from +0.0 -- the reference's order (pq.rs:320-323), so the keys
+// are bit-identical to the CPU's. Each wave keeps per-query sorted lists in LDS; the
+// per-wave lists are merged and finished by flat_merge_kernel (no re-rank: exact keys).
+// Work is bounded by code bytes and LUT gathers, not flops: no MFMA here.
+#include "px_device.h"
+#include "px_kernels.h"
+
+namespace px {
+
+constexpr int kPqWaves = 4;
+constexpr int kPqThreads = kPqWaves * 64;
+
+int pq_list_capacity(int kl) {
+    if (kl <= 16) return 16;
+    if (kl <= 32) return 32;
+    if (kl <= 64) return 64;
+    return 128;
+}
+int pq_lists_per_split() { return kPqWaves; }
+
+// Queries per workgroup: as many LUTs as fit in 64 KB of LDS, at most 4.
+int pq_queries_per_block(int m, int ks) {
+    const int lut_bytes = m * ks * 4;
+    int qpb = 65536 / (lut_bytes > 0 ? lut_bytes : 1);
+    if (qpb >= 4) return 4;
+    if (qpb >= 2) return 2;
+    return 1;
+}
+
+// One code row; aligned so that m = 16 loads as a single dwordx4 and m = 8 as a dwordx2.
+template <int M>
+struct alignas(M % 16 == 0 ? 16 : (M % 8 == 0 ? 8 : 1)) CodeRow {
+    uint8_t c[M];
+};
+
+// M > 0: compile-time subspace count with a vector code load; M == 0: runtime m.
+template <int QPB, int KP, int M>
+__global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float lut[];  // [QPB][m * ks]
+    __shared__ float lkeys[kPqWaves][QPB][KP];
+    __shared__ int lids[kPqWaves][QPB][KP];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int m = M > 0 ? M : a.m;
+    const int lut_len = m * a.ks;
+    const int qg = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+    const int q0 = qg * QPB;
+    const float kInf = __int_as_float(0x7f800000);
+
+    // LUT[qq][sub][c] = l2_sqr(q_sub, centroid) | -inner_product(q_sub, centroid)
+    for (int x = tid; x < QPB * lut_len; x += kPqThreads) {
+        const int qq = x / lut_len;
+        const int rest = x - qq * lut_len;
+        const int sub = rest / a.ks;
+        const int c = rest - sub * a.ks;
+        float v = 0.f;
+        if (q0 + qq < a.nq) {
+            const float* qs = a.queries + (int64_t)(q0 + qq) * a.dim + sub * a.dsub;
+            const float* cen = a.codebooks + ((int64_t)sub * a.ks + c) * a.dsub;
+            v = a.metric == 0 ? ref_l2_sqr(qs, cen, a.dsub) : -ref_inner_product(qs, cen, a.dsub);
+        }
+        lut[x] = v;
+    }
+    for (int x = lane; x < QPB * KP; x += 64) {
+        lkeys[wave][x / KP][x % KP] = kInf;
+        lids[wave][x / KP][x % KP] = kIdNone;
+    }
+    __syncthreads();
+
+    float tau_k[QPB];
+    int tau_i[QPB];
+#pragma unroll
+    for (int qq = 0; qq < QPB; ++qq) {
+        tau_k[qq] = kInf;
+        tau_i[qq] = kIdNone;
+    }
+    bool qok[QPB];
+#pragma unroll
+    for (int qq = 0; qq < QPB; ++qq) qok[qq] = q0 + qq < a.nq;
+
+    const int64_t row0 = (int64_t)split * a.rows_per_split;
+    const int64_t row1 = min(a.n_eff, row0 + a.rows_per_split);
+    for (int64_t base = row0 + wave * 64; base < row1; base += kPqThreads) {
+        const int64_t pos = base + lane;
+        const bool valid = pos < row1;
+        float key[QPB];
+#pragma unroll
+        for (int qq = 0; qq < QPB; ++qq) key[qq] = 0.0f;
+        if (valid) {
+            const int64_t row = a.rowidx ? (int64_t)a.rowidx[pos] : pos;
+            if (M > 0) {
+                const CodeRow<(M > 0 ? M : 1)> cr =
+                    *reinterpret_cast<const CodeRow<(M > 0 ? M : 1)>*>(a.codes + row * M);
+#pragma unroll
+                for (int sub = 0; sub < (M > 0 ? M : 1); ++sub) {
+                    const int off = sub * a.ks + cr.c[sub];
+#pragma unroll
+                    for (int qq = 0; qq < QPB; ++qq) key[qq] = key[qq] + lut[qq * lut_len + off];
+                }
+            } else {
+                const uint8_t* cp = a.codes + row * m;
+                for (int sub = 0; sub < m; ++sub) {
+                    const int off = sub * a.ks + cp[sub];
+#pragma unroll
+                    for (int qq = 0; qq < QPB; ++qq) key[qq] = key[qq] + lut[qq * lut_len + off];
+                }
+            }
+        }
+#pragma unroll
+        for (int qq = 0; qq < QPB; ++qq) {
+            unsigned long long msk = __ballot(valid && qok[qq] && key[qq] <= tau_k[qq]);
+            while (msk) {
+                const int src = __builtin_ctzll(msk);
+                msk &= msk - 1;
+                const float ck = readlane_f(key[qq], src);
+                const int cid = (int)(base + src);
+                if (!cand_less(ck, cid, tau_k[qq], tau_i[qq])) continue;
+                list_insert<KP>(&lkeys[wave][qq][0], &lids[wave][qq][0], a.kl, ck, cid, tau_k[qq],
+                                tau_i[qq]);
+            }
+        }
+    }
+
+    // part[q][split * waves + wave][0..kl)
+    const int width = a.splits * kPqWaves;
+#pragma unroll
+    for (int qq = 0; qq < QPB; ++qq) {
+        if (q0 + qq >= a.nq) break;
+        const int64_t off = ((int64_t)(q0 + qq) * width + split * kPqWaves + wave) * a.kl;
+        for (int s = lane; s < a.kl; s += 64) {
+            a.part_keys[off + s] = lkeys[wave][qq][s];
+            a.part_ids[off + s] = lids[wave][qq][s];
+        }
+    }
+}
+
+template <int QPB, int KP>
+static hipError_t launch_pq_q(const PqScanArgs& a, hipStream_t s) {
+    const int64_t groups = (a.nq + QPB - 1) / QPB;
+    const dim3 grid((unsigned)(groups * a.splits));
+    const size_t lds = (size_t)QPB * a.m * a.ks * sizeof(float);
+    if (a.m == 16)
+        hipLaunchKernelGGL((pq_scan_kernel<QPB, KP, 16>), grid, dim3(kPqThreads), lds, s, a);
+    else if (a.m == 8)
+        hipLaunchKernelGGL((pq_scan_kernel<QPB, KP, 8>), grid, dim3(kPqThreads), lds, s, a);
+    else
+        hipLaunchKernelGGL((pq_scan_kernel<QPB, KP, 0>), grid, dim3(kPqThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int KP>
+static hipError_t launch_pq_k(const PqScanArgs& a, hipStream_t s) {
+    switch (pq_queries_per_block(a.m, a.ks)) {
+        case 4: return launch_pq_q<4, KP>(a, s);
+        case 2: return launch_pq_q<2, KP>(a, s);
+        default: return launch_pq_q<1, KP>(a, s);
+    }
+}
+
+hipError_t launch_pq_scan(const PqScanArgs& a, hipStream_t s) {
+    switch (pq_list_capacity(a.kl)) {
+        case 16: return launch_pq_k<16>(a, s);
+        case 32: return launch_pq_k<32>(a, s);
+        case 64: return launch_pq_k<64>(a, s);
+        default: return launch_pq_k<128>(a, s);
+    }
+}
+
+}  // namespace px
