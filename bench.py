@@ -247,6 +247,30 @@ def bench_pq(args, dev):
     return result
 
 
+def bench_copy(args, dev):
+    """Plain streaming copy of a known byte count: the HBM reference for traffic counters
+    (FETCH_SIZE / WRITE_SIZE of this kernel divided by its known bytes gives the scale)."""
+    nbytes = args.copy_mib << 20
+    src = dev.empty(nbytes)
+    dst = dev.empty(nbytes)
+    ms = ctypes.c_float()
+    times = []
+    for i in range(args.warmup + args.steps):
+        if dev.lib.px_dev_copy_kernel(dst, src, nbytes, ctypes.byref(ms)):
+            raise RuntimeError(_lib.last_error())
+        if i >= args.warmup:
+            times.append(ms.value)
+    gbs = 2 * nbytes / (np.mean(times) * 1e-3) / 1e9
+    return {"metric": "streaming copy bandwidth (read + write)", "value": gbs, "unit": "GB/s",
+            "ms_per_step": float(np.mean(times)), "dtype": "f32",
+            "config": {"workload": f"copy kernel, {args.copy_mib} MiB read + {args.copy_mib} MiB "
+                                   "written per launch", "bytes_read": nbytes,
+                       "bytes_written": nbytes},
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS, "traffic": 2 * nbytes,
+                         "kernel": "copy_kernel", "kernel_ms": float(np.mean(times))}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,7 +279,8 @@ def main():
     ap.add_argument("--k", type=int, default=10)
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nq", type=int, default=10_000)
-    ap.add_argument("--workload", choices=["flat", "pq"], default="flat")
+    ap.add_argument("--workload", choices=["flat", "pq", "copy"], default="flat")
+    ap.add_argument("--copy-mib", type=int, default=1024, help="copy: MiB per launch")
     ap.add_argument("--mask", action="store_true", help="pq: 50%% filter bitmask")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="CPU oracle budget for the baseline (0 disables)")
@@ -270,7 +295,8 @@ def main():
         sys.exit(1)
     dev = Dev()
     try:
-        res = bench_flat(args, dev) if args.workload == "flat" else bench_pq(args, dev)
+        run = {"flat": bench_flat, "pq": bench_pq, "copy": bench_copy}[args.workload]
+        res = run(args, dev)
     finally:
         dev.free()
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
