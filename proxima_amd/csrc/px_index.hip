@@ -535,6 +535,9 @@ int px_flat_add(px_flat* f, const float* vectors, int64_t n) {
 int px_flat_search(const px_flat* cf, const float* queries, int64_t nq, int64_t k,
                    const uint8_t* mask, int64_t* out_ids, float* out_dists) {
     PX_TRY(check_search_args(cf, queries, nq, k, out_ids, out_dists));
+    // crates/py/src/lib.rs:127-128 validates the queries before the k == 0 early return
+    if (queries && !all_finite(queries, nq * cf->dim))
+        return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
     if (k == 0 || nq == 0) return PX_OK;
     return flat_search_host(const_cast<px_flat*>(cf), queries, nq, k, mask, out_ids, out_dists, 0);
 }
@@ -605,9 +608,11 @@ PxGpuIndex* knn_gpu_create(const float* base, int n, int dim) {
     if (!base || n < 0 || dim <= 0) return nullptr;
     PxGpuIndex* g = new (std::nothrow) PxGpuIndex();
     if (!g) return nullptr;
+    // knn.cu:123-141: the corpus is on the device when create returns, else NULL
     for (int metric = 0; metric < 2; ++metric) {
         if (px_flat_create(metric, dim, &g->flat[metric]) != PX_OK ||
-            px_flat_add(g->flat[metric], base, n) != PX_OK) {
+            px_flat_add(g->flat[metric], base, n) != PX_OK || flat_bind(g->flat[metric]) != PX_OK ||
+            flat_sync(g->flat[metric]) != PX_OK) {
             knn_gpu_free(g);
             return nullptr;
         }
@@ -749,9 +754,9 @@ int px_pq_search(const px_pq* cp, const float* queries, int64_t nq, int64_t k,
     PX_TRY(check_search_args(cp, queries, nq, k, out_ids, out_dists));
     px_pq* p = const_cast<px_pq*>(cp);
     if (!p->trained) return fail(PX_ERR_UNTRAINED, "index is not trained");
-    if (k == 0 || nq == 0) return PX_OK;
-    if (!all_finite(queries, nq * p->dim))
+    if (queries && !all_finite(queries, nq * p->dim))
         return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
+    if (k == 0 || nq == 0) return PX_OK;
     std::lock_guard<std::mutex> lock(p->mu);
     if (p->n == 0) {
         host_padding(p->metric, nq, k, out_ids, out_dists, 0);
