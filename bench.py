@@ -106,15 +106,17 @@ def cpu_baseline(data, queries, k, metric, gpu_ids, gpu_d, budget_s, mask=None, 
                                            "max_rel_dist_err": max_rel}
 
 
-def read_traffic(name: str):
+def read_traffic(name: str, default_workload: bool):
+    """HBM bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE) from the committed rocprofv3
+    summary of this workload; None when the run is not that workload or no summary exists."""
     path = os.path.join(ROOT, "profiles", name)
-    if not os.path.exists(path):
+    if not default_workload or not os.path.exists(path):
         return None
-    try:
-        with open(path) as fh:
-            return json.load(fh).get("hbm_bytes_per_launch")
-    except (OSError, ValueError):
-        return None
+    with open(path) as fh:
+        for line in fh:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
 
 
 def bench_flat(args, dev):
@@ -168,7 +170,8 @@ def bench_flat(args, dev):
                    "queries_resident_in_hbm": True},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
-                     "traffic": read_traffic("flat_scan_l2_1Mx128_traffic.json"),
+                     "traffic": read_traffic("flat_scan_kernel_l2_1Mx128_q10k_k10.md",
+                                             (n, nq, k) == (1_000_000, 10_000, 10)),
                      "kernel": "flat_scan_kernel", "kernel_ms": float(np.mean(scan_ms)),
                      "algorithmic_flop_per_launch": flops},
         "pipeline_ms": float(np.mean(total_ms)),
@@ -233,7 +236,8 @@ def bench_pq(args, dev):
                    "n": n, "m": m, "nq": nq, "k": k},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": read_traffic("pq_scan_1Mx16_traffic.json"),
+                     "traffic": read_traffic("pq_scan_kernel_l2_1Mx16_q10k_k10.md",
+                                             (n, nq, k, mask) == (1_000_000, 10_000, 10, None)),
                      "kernel": "pq_scan_kernel", "kernel_ms": float(np.mean(scan_ms)),
                      "algorithmic_bytes_per_launch": algo_bytes},
     }

@@ -17,7 +17,7 @@
  * Results: ids ascending by (key, id) with equal keys going to the lower row id; keys are
  * recomputed for the returned rows in the reference's arithmetic (distance.rs:3-39), so
  * distances are the reference's. Short results are padded with id -1 and FLT_MAX (L2)
- * or -FLT_MAX (IP), as flat.rs:234-237.
+ * or -FLT_MAX (IP), as flat.rs:144-147.
  */
 #ifndef PROXIMA_PX_H
 #define PROXIMA_PX_H
@@ -32,8 +32,8 @@ extern "C" {
 #define PX_OK 0
 #define PX_ERR_BAD_K (-1)      /* k outside what the kernels support (knn.cu:145) */
 #define PX_ERR_SHMEM (-2)      /* reserved: knn.cu:147's shared-memory code; never returned */
-#define PX_ERR_DIM (-3)        /* dim == 0, or a length not a multiple of dim (flat.rs:163-168) */
-#define PX_ERR_NONFINITE (-4)  /* NaN or infinite input (flat.rs:169-172, 204-207) */
+#define PX_ERR_DIM (-3)        /* dim == 0, or a length not a multiple of dim (flat.rs:73-78, 162-167) */
+#define PX_ERR_NONFINITE (-4)  /* NaN or infinite input (flat.rs:79-82, 114-117) */
 #define PX_ERR_ARG (-5)        /* null handle/pointer, negative size, bad metric or params */
 #define PX_ERR_UNTRAINED (-6)  /* PQ index used before train (crates/py/src/lib.rs:492-504) */
 #define PX_ERR_DEVICE (-7)     /* no usable gfx950 device */
@@ -68,23 +68,23 @@ int knn_gpu_search(const PxGpuIndex* idx, const float* queries, int nq, int k, i
 void knn_gpu_free(PxGpuIndex* idx);
 
 /* ------------------------------------------------------------------------------------
- * FlatIndex (crates/core/src/flat.rs:124-321), the path a `hip` feature of
+ * FlatIndex (crates/core/src/flat.rs:34-231), the path a `hip` feature of
  * crates/core would bind behind FlatIndex::{new, add, search*, len, dim, metric,
  * memory_bytes}.
  * ---------------------------------------------------------------------------------- */
 typedef struct px_flat px_flat;
 
-/* FlatIndex::new, flat.rs:133-136 */
+/* FlatIndex::new, flat.rs:43-46 */
 int px_flat_create(int metric, int64_t dim, px_flat** out);
 /* Drop */
 void px_flat_destroy(px_flat* idx);
-/* FlatIndex::add, flat.rs:162-175: append n rows (row-major n x dim). */
+/* FlatIndex::add, flat.rs:72-85: append n rows (row-major n x dim). */
 int px_flat_add(px_flat* idx, const float* vectors, int64_t n);
 
 /*
- * FlatIndex::search_batch / search_batch_filtered, flat.rs:240-320 (search and
+ * FlatIndex::search_batch / search_batch_filtered, flat.rs:150-230 (search and
  * search_filtered are nq = 1). Host pointers. mask is NULL or px_flat_size() bytes,
- * nonzero = keep (flat.rs:215-219). Outputs nq * k each. k == 0 or nq == 0 is a no-op.
+ * nonzero = keep (flat.rs:125-129). Outputs nq * k each. k == 0 or nq == 0 is a no-op.
  */
 int px_flat_search(const px_flat* idx, const float* queries, int64_t nq, int64_t k,
                    const uint8_t* mask, int64_t* out_ids, float* out_dists);
@@ -98,13 +98,13 @@ int px_flat_search_device(const px_flat* idx, const float* d_queries, int64_t nq
                           const uint8_t* d_mask, int64_t* d_ids, float* d_dists);
 
 /* Copy rows [first, first + n) out as row-major n x dim floats (FlatIndex::save needs the
- * data, flat.rs:154-156 -> lib.rs:19-30). */
+ * data, flat.rs:64-66 -> lib.rs:19-30). */
 int px_flat_get_vectors(const px_flat* idx, int64_t first, int64_t n, float* out);
 
-int64_t px_flat_size(const px_flat* idx);         /* FlatIndex::len, flat.rs:141-143 */
-int64_t px_flat_dim(const px_flat* idx);          /* FlatIndex::dim, flat.rs:138-140 */
-int px_flat_metric(const px_flat* idx);           /* FlatIndex::metric, flat.rs:147-149 */
-int64_t px_flat_memory_bytes(const px_flat* idx); /* FlatIndex::memory_bytes, flat.rs:150-152 */
+int64_t px_flat_size(const px_flat* idx);         /* FlatIndex::len, flat.rs:51-53 */
+int64_t px_flat_dim(const px_flat* idx);          /* FlatIndex::dim, flat.rs:48-50 */
+int px_flat_metric(const px_flat* idx);           /* FlatIndex::metric, flat.rs:57-59 */
+int64_t px_flat_memory_bytes(const px_flat* idx); /* FlatIndex::memory_bytes, flat.rs:60-62 */
 
 /* ------------------------------------------------------------------------------------
  * PqIndex (crates/core/src/pq.rs:217-397).

@@ -2,7 +2,7 @@
 
 The checker, never the product: only tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg import this package. It wraps oracle/libpx_oracle.so, a C restatement of
-crates/core/src/distance.rs:3-39, flat.rs:106-320 and pq.rs:25-396 (see px_oracle.h for
+crates/core/src/distance.rs:3-39, flat.rs:106-230 and pq.rs:25-396 (see px_oracle.h for
 the line-by-line map and the canonical (key, id) tie order).
 
 Parity status of every function: pinned (tests/test_oracle.py) by the reference's known

@@ -91,7 +91,7 @@ static uint64_t splitmix_below(uint64_t* state, uint64_t n) {
 
 /* ---------------------------------------------------------------------------
  * Top-k selection: flat.rs:11-32 (Cand ordered by f32::total_cmp) and
- * flat.rs:213-237 (heap of the k best, into_sorted_vec, finish, pad).
+ * flat.rs:123-147 (heap of the k best, into_sorted_vec, finish, pad).
  * The heap is ordered on (total-order key, id); see px_oracle.h.
  * ------------------------------------------------------------------------- */
 typedef struct {
@@ -137,7 +137,7 @@ static void heap_sift_up(cand_t* h, int64_t i) {
     }
 }
 
-/* offer (key, id) to a max-heap of capacity k holding *len entries (flat.rs:221-226) */
+/* offer (key, id) to a max-heap of capacity k holding *len entries (flat.rs:131-136) */
 static inline void heap_offer(cand_t* h, int64_t* len, int64_t k, float key, int64_t id) {
     cand_t c;
     c.tk = total_key(key);
@@ -161,7 +161,7 @@ static int cand_cmp(const void* pa, const void* pb) {
     return 0;
 }
 
-/* flat.rs:229-237 / pq.rs:332-346: ascending order, finish, pad */
+/* flat.rs:139-147 / pq.rs:332-346: ascending order, finish, pad */
 static void heap_finish(cand_t* h, int64_t len, int64_t k, int l2, int64_t* ids, float* dists,
                         float* keys) {
     qsort(h, (size_t)len, sizeof(cand_t), cand_cmp);
@@ -177,7 +177,7 @@ static void heap_finish(cand_t* h, int64_t len, int64_t k, int l2, int64_t* ids,
     }
 }
 
-/* flat.rs:106-148 for one query, batch over queries as flat.rs:240-320 */
+/* flat.rs:106-148 for one query, batch over queries as flat.rs:150-230 */
 int px_or_flat_search(const float* data, int64_t n, int64_t dim, int metric,
                       const float* queries, int64_t nq, int64_t k, const uint8_t* mask,
                       int64_t* out_ids, float* out_dists, float* out_keys, int nthreads) {
@@ -195,7 +195,7 @@ int px_or_flat_search(const float* data, int64_t n, int64_t dim, int metric,
             const float* q = queries + qi * dim;
             int64_t len = 0;
             for (int64_t i = 0; i < n; ++i) {
-                if (mask && !mask[i]) continue; /* flat.rs:215-219: skip before the distance */
+                if (mask && !mask[i]) continue; /* flat.rs:125-129: skip before the distance */
                 const float* v = data + i * dim;
                 float key = l2 ? px_or_l2_sqr(q, v, dim) : -px_or_inner_product(q, v, dim);
                 heap_offer(heap, &len, k, key, i);

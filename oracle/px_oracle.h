@@ -16,7 +16,7 @@
  *   px_or_pq_search         crates/core/src/pq.rs:299-347 (scan), 361-396 (batch)
  *
  * Canonical order: the reference keeps the first k rows and then replaces the heap
- * maximum only when a new key is strictly smaller under f32::total_cmp (flat.rs:221-226).
+ * maximum only when a new key is strictly smaller under f32::total_cmp (flat.rs:131-136).
  * Which of several equal maxima Rust's BinaryHeap evicts, and the order
  * into_sorted_vec gives equal keys, are std-library details. The oracle resolves
  * both by ordering candidates on (key total-order, row id): equal keys go to the

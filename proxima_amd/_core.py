@@ -243,7 +243,7 @@ class FlatIndex:
         _check(self._lib.px_flat_get_vectors(self._h, 0, n, _lib.f32p(out)))
         return out
 
-    # lib.rs:219-226 over flat.rs:34-40: dim u64, metric u32, n u64, data (u64 len, f32...)
+    # lib.rs:219-226 (save, load) over flat.rs:34-40: dim u64, metric u32, n u64, data (u64 len, f32...)
     def save(self, path) -> None:
         data = self.vectors()
         head = struct.pack("<QIQQ", self._dim, int(self._metric), data.shape[0], data.size)
@@ -448,7 +448,7 @@ class PqIndex:
             raise ValueError("codes must have shape (n, m)")
         _check(self._lib.px_pq_add_codes(self._h, _lib.u8p(c), c.shape[0]))
 
-    # lib.rs:665-671 over pq.rs:217-223 / 39-46: metric u32; pq {dim, m, dsub, k: u64,
+    # lib.rs:662-678 over pq.rs:217-223 / 39-46: metric u32; pq {dim, m, dsub, k: u64,
     # codebooks (u64 len, f32...)}; codes (u64 len, u8...); n u64
     def save(self, path) -> None:
         self._trained()

@@ -134,7 +134,7 @@ def test_k_larger_than_n_pads(gpu):
 
 
 def test_reference_padding_known_answer(gpu):
-    # crates/core/src/flat.rs:413-428
+    # crates/core/src/flat.rs:323-338
     idx = FlatIndex(4, Metric.L2)
     idx.add(np.array([[0, 0, 0, 0], [1, 1, 1, 1]], dtype=np.float32))
     ids, d = idx.search(np.zeros(4, dtype=np.float32), k=5)
@@ -144,7 +144,7 @@ def test_reference_padding_known_answer(gpu):
 
 
 def test_reference_filtered_padding_known_answer(gpu):
-    # crates/core/src/flat.rs:460-473
+    # crates/core/src/flat.rs:370-383
     idx = FlatIndex(4, Metric.L2)
     idx.add(np.array([[0] * 4, [1] * 4, [2] * 4], dtype=np.float32))
     ids, d = idx.search_filtered(np.zeros(4, dtype=np.float32),
@@ -154,7 +154,7 @@ def test_reference_filtered_padding_known_answer(gpu):
 
 
 def test_self_is_nearest_reference(gpu):
-    # crates/core/src/flat.rs:342-357 (200 x 16, SplitMix seed 42, uniform [-1, 1])
+    # crates/core/src/flat.rs:252-267 (200 x 16, SplitMix seed 42, uniform [-1, 1])
     data = datagen.uniform_pm1(200, 16, 42)
     idx = FlatIndex(16, Metric.L2)
     idx.add(data)
@@ -165,7 +165,7 @@ def test_self_is_nearest_reference(gpu):
 
 
 def test_batch_matches_single_reference(gpu):
-    # crates/core/src/flat.rs:384-411 (500 x 12 IP, 33 queries, k=5)
+    # crates/core/src/flat.rs:294-321 (500 x 12 IP, 33 queries, k=5)
     data = datagen.uniform_pm1(500, 12, 3)
     q = datagen.uniform_pm1(33, 12, 88)
     idx = FlatIndex(12, Metric.InnerProduct)
