@@ -35,23 +35,51 @@ __device__ __forceinline__ f32x16 mfma4(float4 a, float4 b, f32x16 c) {
 }
 
 int flat_list_capacity(int kl) {
-    if (kl <= 16) return 16;
     if (kl <= 32) return 32;
     if (kl <= 64) return 64;
     return 128;
 }
-int flat_waves(int kp) { return kp >= 128 ? 2 : 4; }
+// Waves per workgroup: all waves share one double-buffered corpus stage (67.6 KB of LDS);
+// the per-wave candidate lists take 32 * KP * 8 bytes each, kept within 64 KB.
+int flat_waves(int kp) { return kp <= 32 ? 8 : (kp <= 64 ? 4 : 2); }
 int flat_queries_per_block(int kp) { return 32 * flat_waves(kp); }
 
-// One workgroup = WAVES waves = 32*WAVES queries x one corpus split.
+// Total-order int of a key (flat.rs:30's f32::total_cmp) and back; the mapping is its own
+// inverse. Shared thresholds are published as these ints with atomicMin.
+__device__ __forceinline__ float from_total_key(int t) {
+    return __int_as_float(t ^ (int)(((unsigned)(t >> 31)) >> 1));
+}
+
+// One workgroup = WAVES waves = 32 * WAVES queries x one corpus split of rows_per_split rows.
+//
 // MFMA operands: A = corpus rows (M), B = queries (N), K = dims. For the 4 sub-steps e of
 // dim group g, lane (i, h) feeds A[i][h] = x[row i][8g + 4h + e] and lane (j, h) feeds
 // B[h][j] = q[j][8g + 4h + e]: both sides agree on the dim of every K slot.
-template <int KP, int WAVES>
+//
+// Pipeline: the corpus streams through LDS in stages of 64 rows x 128 dims (one tile is
+// ceil(dp / 128) stages; MULTI when that is more than one). While the waves run the MFMAs
+// of stage s out of one LDS buffer, every thread holds the global loads of stage s + 1 in
+// registers (and, with MULTI, each wave the next query chunk) and writes them to the other
+// buffer afterwards: one barrier per stage. Every load is issued in a fixed order on a
+// static path, so waiting for one never waits for the prefetch behind it (vector loads
+// retire in order). FILT scans the compacted row ids of a filter; the ids of the next
+// tile are loaded one stage ahead of the rows themselves.
+//
+// Selection: each wave keeps, per query, a sorted list of the best kl (key, position)
+// candidates of its split in LDS. A candidate must beat the list's last entry (tau) and
+// the query's shared threshold gtau, the smallest list tail any split has published so far
+// (a valid bound: that split already holds kl rows at or below it). Equal keys pass only
+// where they can still matter for the lower-id tie rule: at the shared bound, or when the
+// list's tail came from the current tile (earlier tiles hold smaller positions).
+template <int KP, int WAVES, bool L2, bool MULTI, bool FILT>
 __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     constexpr int NT = WAVES * 64;
-    __shared__ __attribute__((aligned(16))) float tile[kTileRows * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float tnorm[kTileRows];
+    constexpr int kF4PerRow = kChunk / 4;                  // 32 float4 per staged row
+    constexpr int kRowStep = NT / kF4PerRow;               // rows between a thread's loads
+    constexpr int kPF = kTileRows / kRowStep;              // float4 per thread per stage
+    static_assert(NT % kF4PerRow == 0 && kTileRows % kRowStep == 0, "uneven stage split");
+    __shared__ __attribute__((aligned(16))) float tile[2][kTileRows * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float tnorm[2][kTileRows];
     __shared__ float lkeys[WAVES][32][KP];
     __shared__ int lids[WAVES][32][KP];
 
@@ -60,119 +88,198 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     const int qt = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
     const int q = qt * (WAVES * 32) + wave * 32 + j;
     const bool qvalid = q < a.nq;
-    const bool l2 = a.metric == 0;
     const int64_t row0 = (int64_t)split * a.rows_per_split;
     const int64_t row1 = min(a.n_eff, row0 + a.rows_per_split);
     const float kInf = __int_as_float(0x7f800000);
-    const float kNaN = __int_as_float(0x7fc00000);
+    const int nch = MULTI ? (a.dp + kChunk - 1) / kChunk : 1;
+    const int64_t ntiles = (row1 - row0 + kTileRows - 1) / kTileRows;
+    const int64_t nstages = ntiles * nch;
+    const int cc = tid % kF4PerRow;                        // this thread's float4 column
+    const int rr0 = tid / kF4PerRow;                       // its first row in a stage
 
     for (int x = lane; x < 32 * KP; x += 64) {
         lkeys[wave][x / KP][x % KP] = kInf;
         lids[wave][x / KP][x % KP] = kIdNone;
     }
-    float tau_k = kInf;   // threshold of query j: its list's slot kl-1
+    float tau_k = kInf;   // this wave's list tail for query j (slot kl-1)
     int tau_i = kIdNone;
-    const float qn = (l2 && qvalid) ? a.qnorms[q] : 0.f;
-
-    const int nchunks = (a.dp + kChunk - 1) / kChunk;
+    int published = 0x7fffffff;
     const float* qrow = a.queries + (int64_t)(qvalid ? q : 0) * a.dp;
-    float4 b[16];
-    auto load_b = [&](int c) {
+    int* gtau = a.gtau + (qvalid ? q : 0);
+
+    // Every load below is unconditional (clamped to a valid address) so that the number of
+    // loads in flight is known statically; values are zeroed where they are consumed, not
+    // where they are loaded, so that no select waits for a load.
+    auto zero_unless = [](bool keep, float4 v) {
+        v.x = keep ? v.x : 0.f;
+        v.y = keep ? v.y : 0.f;
+        v.z = keep ? v.z : 0.f;
+        v.w = keep ? v.w : 0.f;
+        return v;
+    };
+    // raw query chunk c (dims past the chunk's end are loaded clamped, zeroed by b_valid)
+    auto load_b = [&](int c, float4 (&bb)[16]) {
         const int dc = min(kChunk, a.dp - c * kChunk);
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
-            const int d = g * 8 + h * 4;
-            b[g] = (qvalid && d < dc) ? *reinterpret_cast<const float4*>(qrow + c * kChunk + d)
-                                      : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int g = 0; g < 16; ++g)
+            bb[g] = *reinterpret_cast<const float4*>(qrow + c * kChunk + min(g * 8 + h * 4, dc - 4));
+    };
+    auto b_valid = [&](int c, int g) {
+        return qvalid && g * 8 + h * 4 < min(kChunk, a.dp - c * kChunk);
+    };
+    // Row ids (-1 past the split's end) of the rows this thread stages for tile t, and of
+    // row t0 + tid whose norm it stages.
+    int rid[kPF], pid;
+    auto tile_ids = [&](int64_t t) {
+        const int64_t t0 = row0 + t * kTileRows;
+#pragma unroll
+        for (int u = 0; u < kPF; ++u) {
+            const int64_t pos = t0 + rr0 + u * kRowStep;
+            const int v = FILT ? a.rowidx[min(pos, row1 - 1)] : (int)pos;
+            rid[u] = pos < row1 ? v : -1;
+        }
+        const int64_t pos = t0 + tid;
+        const int v = FILT ? a.rowidx[min(pos, row1 - 1)] : (int)pos;
+        pid = (tid < kTileRows && pos < row1) ? v : -1;
+    };
+    float4 pf[kPF];
+    float pn = 0.f;
+    unsigned pvalid = 0;  // bit u: pf[u] is a real row's data; bit kPF: pn is a real norm
+    auto fetch = [&](int64_t s) {
+        const int c = MULTI ? (int)(s % nch) : 0;
+        const int f4r = min(kChunk, a.dp - c * kChunk) >> 2;
+        pvalid = 0;
+#pragma unroll
+        for (int u = 0; u < kPF; ++u) {
+            pf[u] = *reinterpret_cast<const float4*>(
+                a.corpus + (int64_t)max(rid[u], 0) * a.dp + c * kChunk + min(cc, f4r - 1) * 4);
+            pvalid |= (rid[u] >= 0 && cc < f4r) ? 1u << u : 0u;
+        }
+        if (L2) {
+            pn = a.norms[max(pid, 0)];
+            pvalid |= pid >= 0 ? 1u << kPF : 0u;
         }
     };
-    if (nchunks == 1) load_b(0);
-
-    for (int64_t t0 = row0; t0 < row1; t0 += kTileRows) {
-        f32x16 acc0 = {0.f}, acc1 = {0.f};
-        for (int c = 0; c < nchunks; ++c) {
-            const int dc = min(kChunk, a.dp - c * kChunk);
-            const int f4_per_row = dc >> 2;
-            __syncthreads();  // previous tile (and its norms) fully consumed
-            for (int f = tid; f < kTileRows * f4_per_row; f += NT) {
-                const int rr = f / f4_per_row, cc = f - rr * f4_per_row;
-                const int64_t pos = t0 + rr;
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (pos < row1) {
-                    const int64_t row = a.rowidx ? (int64_t)a.rowidx[pos] : pos;
-                    v = *reinterpret_cast<const float4*>(a.corpus + row * a.dp + c * kChunk + cc * 4);
-                }
-                *reinterpret_cast<float4*>(tile + rr * kLdsStride + cc * 4) = v;
-            }
-            if (c == 0 && tid < kTileRows) {
-                const int64_t pos = t0 + tid;
-                float nv = 0.f;
-                if (l2 && pos < row1) nv = a.norms[a.rowidx ? (int64_t)a.rowidx[pos] : pos];
-                tnorm[tid] = nv;
-            }
-            __syncthreads();
-            if (nchunks > 1) load_b(c);
-            const int ng = dc >> 3;
-            const float* ta0 = tile + j * kLdsStride + h * 4;
-            const float* ta1 = tile + (32 + j) * kLdsStride + h * 4;
+    auto commit = [&](int64_t s) {
+        float* tb = tile[s & 1];
 #pragma unroll
-            for (int g = 0; g < 16; ++g) {
-                if (g < ng) {
-                    const float4 a0 = *reinterpret_cast<const float4*>(ta0 + g * 8);
-                    const float4 a1 = *reinterpret_cast<const float4*>(ta1 + g * 8);
-                    acc0 = mfma4(a0, b[g], acc0);
-                    acc1 = mfma4(a1, b[g], acc1);
-                }
+        for (int u = 0; u < kPF; ++u)
+            *reinterpret_cast<float4*>(tb + (rr0 + u * kRowStep) * kLdsStride + cc * 4) =
+                zero_unless((pvalid >> u) & 1u, pf[u]);
+        const int c = MULTI ? (int)(s % nch) : 0;
+        if (L2 && c == 0 && tid < kTileRows)
+            tnorm[(s / nch) & 1][tid] = (pvalid >> kPF) & 1u ? pn : 0.f;
+    };
+
+    float4 b[16], bn[MULTI ? 16 : 1];
+    load_b(0, b);
+#pragma unroll
+    for (int g = 0; g < 16; ++g) b[g] = zero_unless(b_valid(0, g), b[g]);
+    if (nstages > 0) {
+        tile_ids(0);
+        fetch(0);
+        commit(0);
+        tile_ids(nch > 1 ? 0 : 1);  // ids for the tile of stage 1
+    }
+    __syncthreads();
+
+    f32x16 acc0 = {0.f}, acc1 = {0.f};
+    for (int64_t s = 0; s < nstages; ++s) {
+        const int c = MULTI ? (int)(s % nch) : 0;
+        const int64_t t0 = row0 + (s / nch) * kTileRows;
+        const int gt_raw = __hip_atomic_load(gtau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if constexpr (MULTI) load_b((c + 1) % nch, bn);
+        fetch(s + 1);  // past the last stage every row is -1: harmless clamped loads
+        tile_ids((s + 2) / nch);  // ids for the tile of stage s + 2
+        if (c == 0) {
+            acc0 = (f32x16){0.f};
+            acc1 = (f32x16){0.f};
+        }
+        const int ng = min(kChunk, a.dp - c * kChunk) >> 3;
+        const float* ta0 = tile[s & 1] + j * kLdsStride + h * 4;
+        const float* ta1 = tile[s & 1] + (32 + j) * kLdsStride + h * 4;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            if (g < ng) {
+                const float4 a0 = *reinterpret_cast<const float4*>(ta0 + g * 8);
+                const float4 a1 = *reinterpret_cast<const float4*>(ta1 + g * 8);
+                acc0 = mfma4(a0, b[g], acc0);
+                acc1 = mfma4(a1, b[g], acc1);
             }
         }
 
-        // Epilogue: keys for the 32 rows this lane holds for query j.
-        float key[32];
-        float kmin = kNaN;
+        if (c == nch - 1) {
+            // Epilogue, branch-free: keys of the 32 rows this lane holds for query j.
+            // L2 drops the per-query constant ||q||^2 (it does not change a query's order;
+            // the merge re-ranks exactly), so key = ||x||^2 - 2 q.x; IP key = -q.x.
+            const float* tn = tnorm[(s / nch) & 1];
+            float key[32];
+            float kmin = kInf;
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) {
+            for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) {
-                const int lr = rb * 32 + 8 * r4 + 4 * h;  // rows lr .. lr+3
-                const float4 nv = *reinterpret_cast<const float4*>(tnorm + lr);
-                const float nn[4] = {nv.x, nv.y, nv.z, nv.w};
+                for (int r4 = 0; r4 < 4; ++r4) {
+                    const int lr = rb * 32 + 8 * r4 + 4 * h;  // rows lr .. lr+3
+                    float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (L2) nv = *reinterpret_cast<const float4*>(tn + lr);
+                    const float nn[4] = {nv.x, nv.y, nv.z, nv.w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * r4 + e;
-                    const float dot = rb == 0 ? acc0[r] : acc1[r];
-                    float kv = l2 ? fmaxf(__builtin_fmaf(-2.0f, dot, nn[e] + qn), 0.0f) : -dot;
-                    if (!qvalid || t0 + lr + e >= row1) kv = kNaN;  // never selected
-                    key[rb * 16 + r] = kv;
-                    kmin = fminf(kmin, kv);
-                }
-            }
-        }
-
-        // Slow path: some lane holds a candidate at or below its query's threshold.
-        if (__ballot(kmin <= tau_k)) {
-#pragma unroll
-            for (int x = 0; x < 32; ++x) {
-                const int rb = x >> 4, r = x & 15;
-                unsigned long long m = __ballot(key[x] <= tau_k);
-                while (m) {
-                    const int src = __builtin_ctzll(m);
-                    m &= m - 1;
-                    const float ck = readlane_f(key[x], src);
-                    const int cid = (int)(t0 + rb * 32 + mfma_row(r, src >> 5));
-                    const float tk = readlane_f(tau_k, src);
-                    const int ti = readlane_i(tau_i, src);
-                    if (!cand_less(ck, cid, tk, ti)) continue;
-                    const int ql = src & 31;
-                    float nk;
-                    int ni;
-                    list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], a.kl, ck, cid, nk, ni);
-                    if (j == ql) {
-                        tau_k = nk;
-                        tau_i = ni;
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * r4 + e;
+                        const float dot = rb == 0 ? acc0[r] : acc1[r];
+                        const float kv = L2 ? __builtin_fmaf(-2.0f, dot, nn[e]) : -dot;
+                        key[rb * 16 + r] = kv;
+                        kmin = fminf(kmin, kv);
                     }
                 }
             }
+            // Padding queries get a threshold nothing passes; rows past the split's end
+            // (last tile only) are excluded in the slow path below.
+            const float thr = qvalid ? fminf(tau_k, from_total_key(gt_raw)) : -kInf;
+            if (__ballot(kmin <= thr)) {
+                const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
+                const bool eq_ok = thr < tau_k || tau_i >= t0;
+#pragma unroll
+                for (int x = 0; x < 32; ++x) {
+                    const int rb = x >> 4, r = x & 15;
+                    const int off = rb * 32 + mfma_row(r, h);
+                    unsigned long long m = __ballot(
+                        off < rem && (key[x] < thr || (key[x] == thr && eq_ok)));
+                    while (m) {
+                        const int src = __builtin_ctzll(m);
+                        m &= m - 1;
+                        const float ck = readlane_f(key[x], src);
+                        const int cid = (int)(t0 + rb * 32 + mfma_row(r, src >> 5));
+                        const float tk = readlane_f(tau_k, src);
+                        const int ti = readlane_i(tau_i, src);
+                        if (!cand_less(ck, cid, tk, ti)) continue;
+                        const int ql = src & 31;
+                        float nk;
+                        int ni;
+                        list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], a.kl, ck, cid,
+                                        nk, ni);
+                        if (j == ql) {
+                            tau_k = nk;
+                            tau_i = ni;
+                        }
+                    }
+                }
+                // publish a tightened list tail as the query's shared bound
+                const int tk = total_key(tau_k);
+                if (h == 0 && qvalid && tau_i != kIdNone && tk < published) {
+                    atomicMin(gtau, tk);
+                    published = tk;
+                }
+            }
         }
+
+        commit(s + 1);
+        if constexpr (MULTI) {
+            const int cn = (c + 1) % nch;
+#pragma unroll
+            for (int g = 0; g < 16; ++g) b[g] = zero_unless(b_valid(cn, g), bn[g]);
+        }
+        __syncthreads();
     }
 
     // Write this split's lists: part[q][split][0..kl)
@@ -189,23 +296,49 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     }
 }
 
+template <int KP, int WAVES, bool L2, bool MULTI>
+static void launch_scan_f(const FlatScanArgs& a, dim3 grid, hipStream_t s) {
+    if (a.rowidx)
+        hipLaunchKernelGGL((flat_scan_kernel<KP, WAVES, L2, MULTI, true>), grid, dim3(WAVES * 64),
+                           0, s, a);
+    else
+        hipLaunchKernelGGL((flat_scan_kernel<KP, WAVES, L2, MULTI, false>), grid, dim3(WAVES * 64),
+                           0, s, a);
+}
+
 template <int KP, int WAVES>
 static hipError_t launch_scan_t(const FlatScanArgs& a, hipStream_t s) {
     const int qpb = 32 * WAVES;
     const int64_t qtiles = (a.nq + qpb - 1) / qpb;
-    const int64_t blocks = qtiles * a.splits;
-    hipLaunchKernelGGL((flat_scan_kernel<KP, WAVES>), dim3((unsigned)blocks), dim3(WAVES * 64), 0,
-                       s, a);
+    const dim3 grid((unsigned)(qtiles * a.splits));
+    const bool multi = a.dp > kChunk;
+    if (a.metric == 0) {
+        if (multi) launch_scan_f<KP, WAVES, true, true>(a, grid, s);
+        else launch_scan_f<KP, WAVES, true, false>(a, grid, s);
+    } else {
+        if (multi) launch_scan_f<KP, WAVES, false, true>(a, grid, s);
+        else launch_scan_f<KP, WAVES, false, false>(a, grid, s);
+    }
     return hipGetLastError();
 }
 
 hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s) {
     switch (flat_list_capacity(a.kl)) {
-        case 16: return launch_scan_t<16, 4>(a, s);
-        case 32: return launch_scan_t<32, 4>(a, s);
+        case 32: return launch_scan_t<32, 8>(a, s);
         case 64: return launch_scan_t<64, 4>(a, s);
         default: return launch_scan_t<128, 2>(a, s);
     }
+}
+
+__global__ void fill_int_kernel(int* p, int64_t n, int v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+hipError_t launch_fill_int(int* p, int64_t n, int v, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_int_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, n, v);
+    return hipGetLastError();
 }
 
 // In-LDS bitonic sort (ascending by (key total-order, id)) of p = 2^x entries.

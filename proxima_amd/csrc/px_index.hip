@@ -117,14 +117,15 @@ struct Timing {
 
 // Scratch shared by both index kinds for one search.
 struct Workspace {
-    DevBuf q, qn, mask, rowidx, scratch, count, part_k, part_i, out_ids, out_d;
+    DevBuf q, qn, mask, rowidx, scratch, count, part_k, part_i, out_ids, out_d, gtau;
     int* h_count = nullptr;  // pinned
     int ensure_pinned() {
         if (!h_count) PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_count), sizeof(int)));
         return PX_OK;
     }
     void release() {
-        for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids, &out_d})
+        for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids,
+                          &out_d, &gtau})
             b->release();
         if (h_count) (void)hipHostFree(h_count);
         h_count = nullptr;
@@ -157,6 +158,30 @@ int choose_splits(int64_t n_eff, int64_t groups, int lists_per_split, int kl, in
     s = std::min<int64_t>(s, px::kMaxMerge / std::max(1, lists_per_split * kl));
     if (s >= 8) s = s / 8 * 8;  // consecutive blocks share a query tile; 8 XCDs
     return (int)std::max<int64_t>(s, 1);
+}
+
+// Corpus splits for the flat scan. Its workgroups fill a CU each (133 KB of LDS), so the
+// grid is sized in whole rounds of `cus` workgroups: the smallest multiple of 8 splits
+// (each XCD then sees a fixed subset of splits across query tiles) giving at least four
+// rounds with at most 5% idle in the last, else the best-filled choice. Splits keep at
+// least 256 rows and their lists fit the merge (splits * kl <= kMaxMerge).
+int choose_flat_splits(int64_t n_eff, int64_t groups, int kl, int cus) {
+    cus = std::max(cus, 1);
+    const int64_t max_s = std::max<int64_t>(
+        1, std::min<int64_t>(n_eff / 256, px::kMaxMerge / std::max(kl, 1)));
+    int best = 1;
+    double best_eff = -1.0;
+    for (int64_t s = 1; s <= std::min<int64_t>(max_s, 256); s = s < 8 ? s * 2 : s + 8) {
+        const int64_t blocks = groups * s;
+        const int64_t rounds = (blocks + cus - 1) / cus;
+        const double eff = (double)blocks / (double)(rounds * cus);
+        if (rounds >= 4 && eff >= 0.95) return (int)s;
+        if (eff > best_eff + 1e-9 || (rounds < 4 && eff >= best_eff - 1e-9)) {
+            best = (int)s;
+            best_eff = eff;
+        }
+    }
+    return best;
 }
 
 }  // namespace
@@ -262,17 +287,15 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     const int kp = px::flat_list_capacity(kl);
     const int64_t qpb = px::flat_queries_per_block(kp);
     const int64_t groups = (nq + qpb - 1) / qpb;
-    int splits = choose_splits(n_eff, groups, 1, kl, f->dev.cus, 256);
+    int splits = choose_flat_splits(n_eff, groups, kl, f->dev.cus);
     int64_t rps = (n_eff + splits - 1) / splits;
     rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
     splits = (int)std::max<int64_t>(1, (n_eff + rps - 1) / rps);
 
     PX_TRY(ws.part_k.reserve(sizeof(float) * nq * splits * kl));
     PX_TRY(ws.part_i.reserve(sizeof(int) * nq * splits * kl));
-    if (f->metric == 0) {
-        PX_TRY(ws.qn.reserve(sizeof(float) * nq));
-        PX_HIP(px::launch_row_norms(d_q, nq, (int)f->dp, ws.qn.as<float>(), s));
-    }
+    PX_TRY(ws.gtau.reserve(sizeof(int) * nq));
+    PX_HIP(px::launch_fill_int(ws.gtau.as<int>(), nq, px::kTotalKeyInf, s));
     PX_TRY(f->timing.ensure());
     if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[0], s));
 
@@ -280,7 +303,6 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     a.corpus = f->d_x;
     a.norms = f->d_norm;
     a.queries = d_q;
-    a.qnorms = ws.qn.as<float>();
     a.rowidx = rowidx;
     a.n_eff = n_eff;
     a.rows_per_split = rps;
@@ -291,6 +313,7 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     a.metric = f->metric;
     a.part_keys = ws.part_k.as<float>();
     a.part_ids = ws.part_i.as<int>();
+    a.gtau = ws.gtau.as<int>();
     if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
     if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[1], s));
 

@@ -20,7 +20,6 @@ struct FlatScanArgs {
     const float* corpus;   // [n][dp] row-major, zero pad columns
     const float* norms;    // [n] squared norms (L2 only)
     const float* queries;  // [nq][dp] row-major, zero pad columns
-    const float* qnorms;   // [nq] squared norms (L2 only)
     const int* rowidx;     // optional: ascending row ids of the rows to scan (filter)
     int64_t n_eff;         // rows to scan (rowidx length when filtered)
     int64_t rows_per_split;
@@ -31,6 +30,7 @@ struct FlatScanArgs {
     int metric;            // 0 = L2, 1 = inner product
     float* part_keys;      // [nq][splits][kl]
     int* part_ids;         // compacted positions (row ids when unfiltered)
+    int* gtau;             // [nq] shared per-query bound, total-order ints; starts at +inf
 };
 
 // Waves per workgroup and list capacity used for a list length kl.
@@ -38,6 +38,9 @@ int flat_list_capacity(int kl);
 int flat_waves(int kp);
 int flat_queries_per_block(int kp);
 hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s);
+// Total-order int of +inf: the starting value of FlatScanArgs::gtau.
+constexpr int kTotalKeyInf = 0x7f800000;
+hipError_t launch_fill_int(int* p, int64_t n, int v, hipStream_t s);
 
 struct MergeArgs {
     const float* part_keys;  // [nq][width] candidates (key, id/position)
