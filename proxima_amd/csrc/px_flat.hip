@@ -50,6 +50,59 @@ __device__ __forceinline__ float from_total_key(int t) {
     return __int_as_float(t ^ (int)(((unsigned)(t >> 31)) >> 1));
 }
 
+// Bulk list fill for the first tile of a split (k' <= 32), whose lists start empty: rather
+// than inserting the tile's candidates one by one (shifting the list each time), take them
+// in ascending (key, row) order, kl rounds of "smallest remaining", so each is appended.
+// key[x] is this lane's key of tile row 32 (x / 16) + mfma_row(x % 16, h) for query j;
+// lanes l and l ^ 32 hold the two halves of the same query's 64 rows, and within a lane
+// rows ascend with x. Rows past the split's end (and padding queries) never qualify.
+// Writes slots 0..kl-1 of the query's list (unfilled slots stay (+inf, none)) and returns
+// its tail.
+__device__ __forceinline__ void first_tile_lists(const float (&key)[32], int64_t t0,
+                                                 int64_t row1, bool qvalid, int kl, float* lk,
+                                                 int* li, float& tau_k, int& tau_i) {
+    constexpr int kNoKey = 0x7fffffff;  // sorts after every real key's total-order int
+    const int h = lane_id() >> 5;
+    const int rem = (int)min<int64_t>(row1 - t0, (int64_t)64);
+    int tk[32];
+#pragma unroll
+    for (int x = 0; x < 32; ++x) {
+        const int off = (x >> 4) * 32 + mfma_row(x & 15, h);
+        tk[x] = (qvalid && off < rem) ? total_key(key[x]) : kNoKey;
+    }
+    int last_t = kNoKey, last_i = kIdNone;
+    for (int r = 0; r < kl; ++r) {
+        // this lane's smallest remaining (strict < keeps the lowest row among equal keys)
+        int bt = kNoKey, bx = 0;
+#pragma unroll
+        for (int x = 0; x < 32; ++x) {
+            const bool lt = tk[x] < bt;
+            bt = lt ? tk[x] : bt;
+            bx = lt ? x : bx;
+        }
+        const int bi = bt == kNoKey ? kIdNone
+                                    : (int)(t0 + (bx >> 4) * 32 + mfma_row(bx & 15, h));
+        const int pt = __shfl_xor(bt, 32), pi = __shfl_xor(bi, 32);
+        const bool mine = bt < pt || (bt == pt && bi < pi);
+        const int wt = mine ? bt : pt, wi = mine ? bi : pi;
+        if (__ballot(wt != kNoKey) == 0) break;  // fewer than kl rows qualify anywhere
+#pragma unroll
+        for (int x = 0; x < 32; ++x) tk[x] = (mine && x == bx) ? kNoKey : tk[x];
+        if (h == 0 && wt != kNoKey) {
+            lk[r] = __int_as_float(wt ^ (int)(((unsigned)(wt >> 31)) >> 1));
+            li[r] = wi;
+        }
+        last_t = wt;
+        last_i = wi;
+        if (r != kl - 1) last_i = kIdNone;
+    }
+    // the tail is slot kl-1: a real entry only when kl rows qualified
+    const bool full = last_i != kIdNone;
+    tau_k = full ? __int_as_float(last_t ^ (int)(((unsigned)(last_t >> 31)) >> 1))
+                 : __int_as_float(0x7f800000);
+    tau_i = full ? last_i : kIdNone;
+}
+
 // One workgroup = WAVES waves = 32 * WAVES queries x one corpus split of rows_per_split rows.
 //
 // MFMA operands: A = corpus rows (M), B = queries (N), K = dims. For the 4 sub-steps e of
@@ -236,7 +289,19 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             // Padding queries get a threshold nothing passes; rows past the split's end
             // (last tile only) are excluded in the slow path below.
             const float thr = qvalid ? fminf(tau_k, from_total_key(gt_raw)) : -kInf;
-            if (__ballot(kmin <= thr)) {
+            if (KP <= 32 && t0 == row0) {
+                // First tile of the split: the lists are empty, so instead of inserting the
+                // tile's candidates one by one, sort them. Each lane sorts its 32 (key, row)
+                // pairs, merges them with its partner lane's (same query, other 32 rows)
+                // and the pair writes the query's best kl as its list.
+                first_tile_lists(key, t0, row1, qvalid, a.kl, &lkeys[wave][j][0],
+                                 &lids[wave][j][0], tau_k, tau_i);
+                const int tk = total_key(tau_k);
+                if (h == 0 && qvalid && tau_i != kIdNone && tk < published) {
+                    atomicMin(gtau, tk);
+                    published = tk;
+                }
+            } else if (__ballot(kmin <= thr)) {
                 const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
                 const bool eq_ok = thr < tau_k || tau_i >= t0;
 #pragma unroll
