@@ -103,6 +103,51 @@ __device__ __forceinline__ void first_tile_lists(const float (&key)[32], int64_t
     tau_i = full ? last_i : kIdNone;
 }
 
+// rank-th smallest (1-based, rank <= 32) of the 32 ints held as v[0..15] by this lane and
+// by lane ^ 32; both lanes return it. Bitonic: sort 16 in registers, split the union into
+// its 16 smallest and 16 largest with the partner's list reversed, sort those halves.
+__device__ __forceinline__ int kth_smallest32(int (&v)[16], int rank) {
+#pragma unroll
+    for (int k = 2; k <= 16; k <<= 1)
+#pragma unroll
+        for (int s = k >> 1; s > 0; s >>= 1)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int l = i ^ s;
+                if (l > i) {
+                    const int mn = min(v[i], v[l]), mx = max(v[i], v[l]);
+                    const bool up = (i & k) == 0;
+                    v[i] = up ? mn : mx;
+                    v[l] = up ? mx : mn;
+                }
+            }
+    int lo[16], hi[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int p = __shfl_xor(v[15 - i], 32);
+        lo[i] = min(v[i], p);
+        hi[i] = max(v[i], p);
+    }
+#pragma unroll
+    for (int s = 8; s > 0; s >>= 1)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int l = i ^ s;
+            if (l > i) {
+                const int a0 = min(lo[i], lo[l]), a1 = max(lo[i], lo[l]);
+                const int b0 = min(hi[i], hi[l]), b1 = max(hi[i], hi[l]);
+                lo[i] = a0; lo[l] = a1; hi[i] = b0; hi[l] = b1;
+            }
+        }
+    int r = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        r = i == rank - 1 ? lo[i] : r;
+        r = i == rank - 17 ? hi[i] : r;
+    }
+    return r;
+}
+
 // One workgroup = WAVES waves = 32 * WAVES queries x one corpus split of rows_per_split rows.
 //
 // MFMA operands: A = corpus rows (M), B = queries (N), K = dims. For the 4 sub-steps e of
@@ -121,7 +166,12 @@ __device__ __forceinline__ void first_tile_lists(const float (&key)[32], int64_t
 // Selection: each wave keeps, per query, a sorted list of the best kl (key, position)
 // candidates of its split in LDS. A candidate must beat the list's last entry (tau) and
 // the query's shared threshold gtau, the smallest list tail any split has published so far
-// (a valid bound: that split already holds kl rows at or below it). Equal keys pass only
+// (a valid bound: that split already holds kl rows at or below it), and a second bound
+// gbound: every split publishes the key in its list slot m - 1 (m = ceil(kl / 32)) to slot
+// (split % 32) of the query's gbest row, so m rows of that split sit at or below it; the
+// ceil(kl / m)-th smallest of the 32 published keys then covers kl rows. gbound is
+// recomputed on a geometric schedule of tiles (most of its tightening happens early),
+// which cuts list insertions by an order of magnitude over gtau alone. Equal keys pass only
 // where they can still matter for the lower-id tie rule: at the shared bound, or when the
 // list's tail came from the current tile (earlier tiles hold smaller positions).
 template <int KP, int WAVES, bool L2, bool MULTI, bool FILT>
@@ -157,8 +207,14 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     float tau_k = kInf;   // this wave's list tail for query j (slot kl-1)
     int tau_i = kIdNone;
     int published = 0x7fffffff;
+    const int pub_m = (a.kl + 31) / 32;                     // list slot published is pub_m - 1
+    const int pub_rank = (a.kl + pub_m - 1) / pub_m;        // rank of the bound among 32
+    int published_best = kTotalKeyInf;
+    float gbound = kInf;
+    int64_t next_refresh = 1;                                // tile index of the next refresh
     const float* qrow = a.queries + (int64_t)(qvalid ? q : 0) * a.dp;
     int* gtau = a.gtau + (qvalid ? q : 0);
+    int* gbest = a.gbest + (int64_t)(qvalid ? q : 0) * 32;
 
     // Every load below is unconditional (clamped to a valid address) so that the number of
     // loads in flight is known statically; values are zeroed where they are consumed, not
@@ -241,6 +297,15 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         const int c = MULTI ? (int)(s % nch) : 0;
         const int64_t t0 = row0 + (s / nch) * kTileRows;
         const int gt_raw = __hip_atomic_load(gtau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int64_t ti = s / nch;
+        const bool refresh = c == nch - 1 && ti == next_refresh;
+        long long gb[8];
+        if (refresh) {
+            const long long* src = reinterpret_cast<const long long*>(gbest + h * 16);
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                gb[u] = __hip_atomic_load(src + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         if constexpr (MULTI) load_b((c + 1) % nch, bn);
         fetch(s + 1);  // past the last stage every row is -1: harmless clamped loads
         tile_ids((s + 2) / nch);  // ids for the tile of stage s + 2
@@ -288,7 +353,18 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             }
             // Padding queries get a threshold nothing passes; rows past the split's end
             // (last tile only) are excluded in the slow path below.
-            const float thr = qvalid ? fminf(tau_k, from_total_key(gt_raw)) : -kInf;
+            if (refresh) {
+                int v[16];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    v[2 * u] = (int)(gb[u] & 0xffffffffll);
+                    v[2 * u + 1] = (int)(gb[u] >> 32);
+                }
+                gbound = fminf(gbound, from_total_key(kth_smallest32(v, pub_rank)));
+                next_refresh = ti + max<int64_t>(1, ti >> 2);
+            }
+            const float thr =
+                qvalid ? fminf(fminf(tau_k, from_total_key(gt_raw)), gbound) : -kInf;
             if (KP <= 32 && t0 == row0) {
                 // First tile of the split: the lists are empty, so instead of inserting the
                 // tile's candidates one by one, sort them. Each lane sorts its 32 (key, row)
@@ -300,6 +376,11 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                 if (h == 0 && qvalid && tau_i != kIdNone && tk < published) {
                     atomicMin(gtau, tk);
                     published = tk;
+                }
+                const int bk = total_key(lkeys[wave][j][pub_m - 1]);
+                if (h == 0 && qvalid && bk < published_best) {
+                    gbest[split & 31] = bk;
+                    published_best = bk;
                 }
             } else if (__ballot(kmin <= thr)) {
                 const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
@@ -334,6 +415,11 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                 if (h == 0 && qvalid && tau_i != kIdNone && tk < published) {
                     atomicMin(gtau, tk);
                     published = tk;
+                }
+                const int bk = total_key(lkeys[wave][j][pub_m - 1]);
+                if (h == 0 && qvalid && bk < published_best) {
+                    gbest[split & 31] = bk;
+                    published_best = bk;
                 }
             }
         }

@@ -117,7 +117,7 @@ struct Timing {
 
 // Scratch shared by both index kinds for one search.
 struct Workspace {
-    DevBuf q, qn, mask, rowidx, scratch, count, part_k, part_i, out_ids, out_d, gtau;
+    DevBuf q, qn, mask, rowidx, scratch, count, part_k, part_i, out_ids, out_d, gtau, gbest;
     int* h_count = nullptr;  // pinned
     int ensure_pinned() {
         if (!h_count) PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_count), sizeof(int)));
@@ -125,7 +125,7 @@ struct Workspace {
     }
     void release() {
         for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids,
-                          &out_d, &gtau})
+                          &out_d, &gtau, &gbest})
             b->release();
         if (h_count) (void)hipHostFree(h_count);
         h_count = nullptr;
@@ -296,6 +296,8 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     PX_TRY(ws.part_i.reserve(sizeof(int) * nq * splits * kl));
     PX_TRY(ws.gtau.reserve(sizeof(int) * nq));
     PX_HIP(px::launch_fill_int(ws.gtau.as<int>(), nq, px::kTotalKeyInf, s));
+    PX_TRY(ws.gbest.reserve(sizeof(int) * nq * 32));
+    PX_HIP(px::launch_fill_int(ws.gbest.as<int>(), nq * 32, px::kTotalKeyInf, s));
     PX_TRY(f->timing.ensure());
     if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[0], s));
 
@@ -314,6 +316,7 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     a.part_keys = ws.part_k.as<float>();
     a.part_ids = ws.part_i.as<int>();
     a.gtau = ws.gtau.as<int>();
+    a.gbest = ws.gbest.as<int>();
     if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
     if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[1], s));
 

@@ -31,6 +31,7 @@ struct FlatScanArgs {
     float* part_keys;      // [nq][splits][kl]
     int* part_ids;         // compacted positions (row ids when unfiltered)
     int* gtau;             // [nq] shared per-query bound, total-order ints; starts at +inf
+    int* gbest;            // [nq][32] per-split published list keys, total-order ints; +inf
 };
 
 // Waves per workgroup and list capacity used for a list length kl.
