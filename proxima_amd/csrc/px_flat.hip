@@ -121,12 +121,12 @@ __device__ __forceinline__ int kth_smallest32(int (&v)[16], int rank) {
                     v[l] = up ? mx : mn;
                 }
             }
-    int lo[16], hi[16];
+    // only the half holding the answer is kept (rank is uniform across the wave)
+    const bool low = rank <= 16;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int p = __shfl_xor(v[15 - i], 32);
-        lo[i] = min(v[i], p);
-        hi[i] = max(v[i], p);
+        v[i] = low ? min(v[i], p) : max(v[i], p);
     }
 #pragma unroll
     for (int s = 8; s > 0; s >>= 1)
@@ -134,17 +134,15 @@ __device__ __forceinline__ int kth_smallest32(int (&v)[16], int rank) {
         for (int i = 0; i < 16; ++i) {
             const int l = i ^ s;
             if (l > i) {
-                const int a0 = min(lo[i], lo[l]), a1 = max(lo[i], lo[l]);
-                const int b0 = min(hi[i], hi[l]), b1 = max(hi[i], hi[l]);
-                lo[i] = a0; lo[l] = a1; hi[i] = b0; hi[l] = b1;
+                const int mn = min(v[i], v[l]), mx = max(v[i], v[l]);
+                v[i] = mn;
+                v[l] = mx;
             }
         }
+    const int want = low ? rank - 1 : rank - 17;
     int r = 0x7fffffff;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        r = i == rank - 1 ? lo[i] : r;
-        r = i == rank - 17 ? hi[i] : r;
-    }
+    for (int i = 0; i < 16; ++i) r = i == want ? v[i] : r;
     return r;
 }
 
@@ -298,14 +296,6 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         const int64_t t0 = row0 + (s / nch) * kTileRows;
         const int gt_raw = __hip_atomic_load(gtau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int64_t ti = s / nch;
-        const bool refresh = c == nch - 1 && ti == next_refresh;
-        long long gb[8];
-        if (refresh) {
-            const long long* src = reinterpret_cast<const long long*>(gbest + h * 16);
-#pragma unroll
-            for (int u = 0; u < 8; ++u)
-                gb[u] = __hip_atomic_load(src + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
         if constexpr (MULTI) load_b((c + 1) % nch, bn);
         fetch(s + 1);  // past the last stage every row is -1: harmless clamped loads
         tile_ids((s + 2) / nch);  // ids for the tile of stage s + 2
@@ -353,12 +343,17 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             }
             // Padding queries get a threshold nothing passes; rows past the split's end
             // (last tile only) are excluded in the slow path below.
-            if (refresh) {
+            if (ti == next_refresh) {
+                // loaded here rather than ahead: refreshes are rare, and holding 16 more
+                // registers across the MFMAs would spill
+                const long long* src = reinterpret_cast<const long long*>(gbest + h * 16);
                 int v[16];
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    v[2 * u] = (int)(gb[u] & 0xffffffffll);
-                    v[2 * u + 1] = (int)(gb[u] >> 32);
+                    const long long w =
+                        __hip_atomic_load(src + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    v[2 * u] = (int)(w & 0xffffffffll);
+                    v[2 * u + 1] = (int)(w >> 32);
                 }
                 gbound = fminf(gbound, from_total_key(kth_smallest32(v, pub_rank)));
                 next_refresh = ti + max<int64_t>(1, ti >> 2);
