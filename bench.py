@@ -11,7 +11,8 @@ every timed launch. cpu_baseline times the CPU oracle (a C restatement of the re
 per-query scan, flat.rs:106-148 with distance.rs:3-39) on a bounded query sample on the
 host's cores, and the same sample checks parity of the GPU results.
 
-  python bench.py [--steps K] [--warmup W] [--k 10] [--workload flat|pq] [--gpus 1]
+  python bench.py [--steps K] [--warmup W] [--workload flat|pq|copy] [--config 1|2|3|5]
+                  [--k K] [--n N] [--nq NQ] [--mask] [--cpu-seconds S] [--gpus 1]
 """
 from __future__ import annotations
 
@@ -119,22 +120,38 @@ def read_traffic(name: str, default_workload: bool):
     return None
 
 
+HEADLINE_METRIC = "exact kNN QPS (1M\u00d7128 fp32, k=10, 10k-query batch); % fp32 MFMA / HBM peak"
+
+
 def bench_flat(args, dev):
-    n, dim, nq, k = args.n, 128, args.nq, args.k
-    log(f"[bench] generating corpus {n} x {dim} SIFT-like and {nq} queries")
-    data = datagen.sift_like(n, dim, 3001)
-    queries = datagen.sift_like(nq, dim, 3002)
-    idx = FlatIndex(dim, Metric.L2)
+    """FlatIndex search_batch on one of the flat workloads (datagen.CONFIGS 1, 2, 3, 5);
+    workload 3 (1M x 128 SIFT-like integers, L2, 10k queries, k=10) is the headline."""
+    c = args.config
+    cfg = datagen.CONFIGS[c]
+    if cfg["kind"] != "flat":
+        raise SystemExit(f"workload {c} is not a FlatIndex workload")
+    n = args.n or cfg["n"]
+    nq = args.nq or cfg["nq"]
+    k = args.k or cfg["k"][0]
+    dim = cfg["dim"]
+    l2 = cfg["metric"] == "L2"
+    log(f"[bench] workload {c}: generating corpus {n} x {dim} ({cfg['dist']}) and {nq} queries")
+    data = datagen.corpus(c, rows=n)
+    queries = datagen.queries(c, rows=nq)
+    mask = datagen.config_mask(c, n) if cfg["mask"] is not None else None
+    n_eff = int(mask.sum()) if mask is not None else n
+    idx = FlatIndex(dim, Metric.L2 if l2 else Metric.InnerProduct)
     t0 = time.perf_counter()
     idx.add(data)
     log(f"[bench] add + upload {time.perf_counter() - t0:.2f} s")
     lib = dev.lib
     dq = dev.put(queries)
+    dm = dev.put(mask.view(np.uint8)) if mask is not None else None
     di = dev.empty(nq * k * 8)
     dd = dev.empty(nq * k * 4)
 
     def step():
-        rc = lib.px_flat_search_device(idx._h, dq, nq, k, None, di, dd)
+        rc = lib.px_flat_search_device(idx._h, dq, nq, k, dm, di, dd)
         if rc:
             raise RuntimeError(_lib.last_error())
 
@@ -156,22 +173,24 @@ def bench_flat(args, dev):
     ids = dev.get(di, np.empty((nq, k), dtype=np.int64))
     dists = dev.get(dd, np.empty((nq, k), dtype=np.float32))
 
-    flops = 2.0 * nq * n * dim
+    flops = 2.0 * nq * n_eff * dim
     achieved = flops / (np.mean(scan_ms) * 1e-3) / 1e12
+    headline = (c, n, nq, k) == (3, 1_000_000, 10_000, 10)
+    desc = (f"FlatIndex exact {'L2' if l2 else 'inner product'}, corpus {n} x {dim} fp32 "
+            f"{ {'gaussian': 'N(0,1)', 'unit': 'unit-normalised Gaussian', 'sift': 'SIFT-like integers in [0,255]'}[cfg['dist']] }, "
+            f"{nq}-query batch, k={k}" + (f", {cfg['mask']:.0%}-density filter" if mask is not None else ""))
     result = {
-        "metric": "exact kNN QPS (1M x 128 fp32, k=10, 10k-query batch); % fp32 MFMA peak",
+        "metric": HEADLINE_METRIC if headline else f"exact kNN QPS ({desc}); % fp32 MFMA peak",
         "value": nq * args.steps / elapsed,
         "unit": "queries/s",
         "ms_per_step": elapsed / args.steps * 1e3,
         "dtype": "f32",
-        "config": {"workload": f"FlatIndex exact L2, corpus {n} x {dim} fp32 SIFT-like "
-                               f"integers in [0,255], {nq}-query batch, k={k}",
-                   "n": n, "dim": dim, "nq": nq, "k": k, "metric": "L2",
-                   "queries_resident_in_hbm": True},
+        "config": {"workload": desc, "n": n, "dim": dim, "nq": nq, "k": k,
+                   "metric": "L2" if l2 else "IP", "mask_density": cfg["mask"],
+                   "n_eff": n_eff, "queries_resident_in_hbm": True},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
-                     "traffic": read_traffic("flat_scan_kernel_l2_1Mx128_q10k_k10.md",
-                                             (n, nq, k) == (1_000_000, 10_000, 10)),
+                     "traffic": read_traffic("flat_scan_kernel_l2_1Mx128_q10k_k10.md", headline),
                      "kernel": "flat_scan_kernel", "kernel_ms": float(np.mean(scan_ms)),
                      "algorithmic_flop_per_launch": flops},
         "pipeline_ms": float(np.mean(total_ms)),
@@ -180,14 +199,16 @@ def bench_flat(args, dev):
         log("[bench] CPU oracle baseline + parity sample")
         import oracle
 
-        cb, par = cpu_baseline(data, queries, k, oracle.L2, ids, dists, args.cpu_seconds)
+        cb, par = cpu_baseline(data, queries, k, oracle.L2 if l2 else oracle.IP, ids, dists,
+                               args.cpu_seconds, mask=mask)
         result["cpu_baseline"] = cb
         result["parity_sample"] = par
     return result
 
 
 def bench_pq(args, dev):
-    n, dim, nq, k, m = args.n, 128, args.nq, args.k, 16
+    n, dim, m = args.n or 1_000_000, 128, 16
+    nq, k = args.nq or 10_000, args.k or 10
     log(f"[bench] generating PQ corpus {n} x {dim} N(0,1), training m={m}")
     data = datagen.gaussian(n, dim, 4001)
     queries = datagen.gaussian(nq, dim, 4002)
@@ -280,10 +301,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--k", type=int, default=10)
-    ap.add_argument("--n", type=int, default=1_000_000)
-    ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--workload", choices=["flat", "pq", "copy"], default="flat")
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 5],
+                    help="flat: which FlatIndex workload (3, the headline, by default)")
+    ap.add_argument("--k", type=int, default=None, help="override the workload's k")
+    ap.add_argument("--n", type=int, default=None, help="override the corpus rows")
+    ap.add_argument("--nq", type=int, default=None, help="override the query count")
     ap.add_argument("--copy-mib", type=int, default=1024, help="copy: MiB per launch")
     ap.add_argument("--mask", action="store_true", help="pq: 50%% filter bitmask")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,

@@ -32,16 +32,29 @@ __device__ __forceinline__ int readlane_i(int v, int lane) {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 
+// List slot ids: int positions, or (for the larger list capacities, to fit more waves in
+// LDS) 16-bit offsets from the split's first position with 0xffff as the empty sentinel.
+template <typename IdT>
+__device__ __forceinline__ int id_load(IdT v, int base) {
+    if constexpr (sizeof(IdT) == 2) return v == 0xffff ? kIdNone : base + (int)v;
+    else return (int)v;
+}
+template <typename IdT>
+__device__ __forceinline__ IdT id_store(int id, int base) {
+    if constexpr (sizeof(IdT) == 2) return (IdT)(id == kIdNone ? 0xffff : id - base);
+    else return (IdT)id;
+}
+
 // Wave-cooperative insertion of (ck, cid) into a sorted list of `kl` live slots
-// (capacity KP, a multiple of 64 or <= 64) held in LDS at lk/li. Lane s owns slots
-// s, s+64, ... The caller guarantees (ck, cid) is smaller than slot kl-1, so the new
-// element lands at some pos < kl and the old slot kl-1 falls off the end.
-// Returns the new last live slot (the list threshold) in every lane.
-template <int KP>
-__device__ __forceinline__ void list_insert(float* lk, int* li, int kl, float ck, int cid,
-                                            float& tau_k, int& tau_i) {
+// (capacity KP) held in LDS at lk/li. Lane s owns slots s, s+64, ... The caller guarantees
+// (ck, cid) is smaller than slot kl-1, so the new element lands at some pos < kl and the
+// old slot kl-1 falls off the end. Returns the new last live slot (the list threshold) in
+// every lane.
+template <int KP, typename IdT>
+__device__ __forceinline__ void list_insert(float* lk, IdT* li, int base, int kl, float ck,
+                                            int cid, float& tau_k, int& tau_i) {
     const int s = lane_id();
-    constexpr int U = KP > 64 ? KP / 64 : 1;
+    constexpr int U = (KP + 63) / 64;
     float okey[U], pkey[U];
     int oid[U], pid[U];
     unsigned long long after[U];
@@ -50,9 +63,9 @@ __device__ __forceinline__ void list_insert(float* lk, int* li, int kl, float ck
         const int slot = s + 64 * u;
         const bool live = slot < kl;
         okey[u] = live ? lk[slot] : __int_as_float(0x7f800000);
-        oid[u] = live ? li[slot] : kIdNone;
+        oid[u] = live ? id_load(li[slot], base) : kIdNone;
         pkey[u] = (live && slot > 0) ? lk[slot - 1] : 0.f;
-        pid[u] = (live && slot > 0) ? li[slot - 1] : 0;
+        pid[u] = (live && slot > 0) ? id_load(li[slot - 1], base) : 0;
         after[u] = __ballot(live && cand_less(ck, cid, okey[u], oid[u]));
     }
     int pos = kl;
@@ -65,10 +78,10 @@ __device__ __forceinline__ void list_insert(float* lk, int* li, int kl, float ck
         if (slot < kl) {
             if (slot > pos) {
                 lk[slot] = pkey[u];
-                li[slot] = pid[u];
+                li[slot] = id_store<IdT>(pid[u], base);
             } else if (slot == pos) {
                 lk[slot] = ck;
-                li[slot] = cid;
+                li[slot] = id_store<IdT>(cid, base);
             }
         }
     }

@@ -14,6 +14,8 @@
 
 #include <float.h>
 
+#include <type_traits>
+
 namespace px {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -34,14 +36,22 @@ __device__ __forceinline__ f32x16 mfma4(float4 a, float4 b, f32x16 c) {
     return c;
 }
 
+// List capacities: 32 (int ids), 56 and 120 (16-bit offsets, so that 8 and 4 waves fit),
+// and 128 (int ids, 2 waves) for the last few k.
 int flat_list_capacity(int kl) {
     if (kl <= 32) return 32;
-    if (kl <= 64) return 64;
+    if (kl <= 56) return 56;
+    if (kl <= 120) return 120;
     return 128;
 }
-// Waves per workgroup: all waves share one double-buffered corpus stage (67.6 KB of LDS);
-// the per-wave candidate lists take 32 * KP * 8 bytes each, kept within 64 KB.
-int flat_waves(int kp) { return kp <= 32 ? 8 : (kp <= 64 ? 4 : 2); }
+bool flat_list_narrow_ids(int kp) { return kp == 56 || kp == 120; }
+// Waves per workgroup: the waves share one double-buffered corpus stage (67.6 KB of LDS);
+// the per-wave candidate lists take 32 * KP * (4 + id bytes) each.
+constexpr int flat_waves(int kp) { return kp <= 56 ? 8 : (kp <= 120 ? 4 : 2); }
+template <int KP>
+struct ListId {
+    using type = typename std::conditional<KP == 56 || KP == 120, unsigned short, int>::type;
+};
 int flat_queries_per_block(int kp) { return 32 * flat_waves(kp); }
 
 // Total-order int of a key (flat.rs:30's f32::total_cmp) and back; the mapping is its own
@@ -50,17 +60,18 @@ __device__ __forceinline__ float from_total_key(int t) {
     return __int_as_float(t ^ (int)(((unsigned)(t >> 31)) >> 1));
 }
 
-// Bulk list fill for the first tile of a split (k' <= 32), whose lists start empty: rather
+// Bulk list fill for the first tile of a split, whose lists start empty: rather
 // than inserting the tile's candidates one by one (shifting the list each time), take them
 // in ascending (key, row) order, kl rounds of "smallest remaining", so each is appended.
 // key[x] is this lane's key of tile row 32 (x / 16) + mfma_row(x % 16, h) for query j;
 // lanes l and l ^ 32 hold the two halves of the same query's 64 rows, and within a lane
 // rows ascend with x. Rows past the split's end (and padding queries) never qualify.
-// Writes slots 0..kl-1 of the query's list (unfilled slots stay (+inf, none)) and returns
-// its tail.
+// Writes slots 0..min(kl, 64)-1 of the query's list (unfilled slots stay (+inf, none))
+// and returns its tail (+inf until kl rows qualified).
+template <typename IdT>
 __device__ __forceinline__ void first_tile_lists(const float (&key)[32], int64_t t0,
                                                  int64_t row1, bool qvalid, int kl, float* lk,
-                                                 int* li, float& tau_k, int& tau_i) {
+                                                 IdT* li, int base, float& tau_k, int& tau_i) {
     constexpr int kNoKey = 0x7fffffff;  // sorts after every real key's total-order int
     const int h = lane_id() >> 5;
     const int rem = (int)min<int64_t>(row1 - t0, (int64_t)64);
@@ -90,7 +101,7 @@ __device__ __forceinline__ void first_tile_lists(const float (&key)[32], int64_t
         for (int x = 0; x < 32; ++x) tk[x] = (mine && x == bx) ? kNoKey : tk[x];
         if (h == 0 && wt != kNoKey) {
             lk[r] = __int_as_float(wt ^ (int)(((unsigned)(wt >> 31)) >> 1));
-            li[r] = wi;
+            li[r] = id_store<IdT>(wi, base);
         }
         last_t = wt;
         last_i = wi;
@@ -182,7 +193,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     __shared__ __attribute__((aligned(16))) float tile[2][kTileRows * kLdsStride];
     __shared__ __attribute__((aligned(16))) float tnorm[2][kTileRows];
     __shared__ float lkeys[WAVES][32][KP];
-    __shared__ int lids[WAVES][32][KP];
+    using IdT = typename ListId<KP>::type;
+    __shared__ IdT lids[WAVES][32][KP];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
@@ -200,7 +212,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
 
     for (int x = lane; x < 32 * KP; x += 64) {
         lkeys[wave][x / KP][x % KP] = kInf;
-        lids[wave][x / KP][x % KP] = kIdNone;
+        lids[wave][x / KP][x % KP] = id_store<IdT>(kIdNone, 0);
     }
     float tau_k = kInf;   // this wave's list tail for query j (slot kl-1)
     int tau_i = kIdNone;
@@ -360,13 +372,13 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             }
             const float thr =
                 qvalid ? fminf(fminf(tau_k, from_total_key(gt_raw)), gbound) : -kInf;
-            if (KP <= 32 && t0 == row0) {
+            if (t0 == row0) {
                 // First tile of the split: the lists are empty, so instead of inserting the
                 // tile's candidates one by one, sort them. Each lane sorts its 32 (key, row)
                 // pairs, merges them with its partner lane's (same query, other 32 rows)
                 // and the pair writes the query's best kl as its list.
                 first_tile_lists(key, t0, row1, qvalid, a.kl, &lkeys[wave][j][0],
-                                 &lids[wave][j][0], tau_k, tau_i);
+                                 &lids[wave][j][0], (int)row0, tau_k, tau_i);
                 const int tk = total_key(tau_k);
                 if (h == 0 && qvalid && tau_i != kIdNone && tk < published) {
                     atomicMin(gtau, tk);
@@ -397,8 +409,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                         const int ql = src & 31;
                         float nk;
                         int ni;
-                        list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], a.kl, ck, cid,
-                                        nk, ni);
+                        list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], (int)row0,
+                                        a.kl, ck, cid, nk, ni);
                         if (j == ql) {
                             tau_k = nk;
                             tau_i = ni;
@@ -437,7 +449,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         int* pi = a.part_ids + ((int64_t)qq * a.splits + split) * a.kl;
         for (int s = lane; s < a.kl; s += 64) {
             pk[s] = lkeys[wave][ql][s];
-            pi[s] = lids[wave][ql][s];
+            pi[s] = id_load(lids[wave][ql][s], (int)row0);
         }
     }
 }
@@ -470,9 +482,10 @@ static hipError_t launch_scan_t(const FlatScanArgs& a, hipStream_t s) {
 
 hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s) {
     switch (flat_list_capacity(a.kl)) {
-        case 32: return launch_scan_t<32, 8>(a, s);
-        case 64: return launch_scan_t<64, 4>(a, s);
-        default: return launch_scan_t<128, 2>(a, s);
+        case 32: return launch_scan_t<32, flat_waves(32)>(a, s);
+        case 56: return launch_scan_t<56, flat_waves(56)>(a, s);
+        case 120: return launch_scan_t<120, flat_waves(120)>(a, s);
+        default: return launch_scan_t<128, flat_waves(128)>(a, s);
     }
 }
 
@@ -576,6 +589,14 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {
     int p = 1;
     while (p < a.width) p <<= 1;
     const size_t lds = (size_t)p * 8 + (size_t)kMaxList * 8;
+    static bool big_lds = false;  // widths past 8k candidates need more than 64 KB of LDS
+    if (lds > 65536 && !big_lds) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(flat_merge_kernel),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)((size_t)kMaxMerge * 8 + kMaxList * 8));
+        if (e != hipSuccess) return e;
+        big_lds = true;
+    }
     hipLaunchKernelGGL(flat_merge_kernel, dim3((unsigned)a.nq), dim3(256), lds, s, a);
     return hipGetLastError();
 }

@@ -160,28 +160,38 @@ int choose_splits(int64_t n_eff, int64_t groups, int lists_per_split, int kl, in
     return (int)std::max<int64_t>(s, 1);
 }
 
-// Corpus splits for the flat scan. Its workgroups fill a CU each (133 KB of LDS), so the
-// grid is sized in whole rounds of `cus` workgroups: the smallest multiple of 8 splits
-// (each XCD then sees a fixed subset of splits across query tiles) giving at least four
-// rounds with at most 5% idle in the last, else the best-filled choice. Splits keep at
-// least 256 rows and their lists fit the merge (splits * kl <= kMaxMerge).
-int choose_flat_splits(int64_t n_eff, int64_t groups, int kl, int cus) {
+// Corpus splits for the flat scan. Its workgroups fill a CU each (134-160 KB of LDS), so
+// the grid is sized in whole rounds of `cus` workgroups. Splits are multiples of 8 where
+// possible (each XCD then sees a fixed subset of splits across query tiles), keep at least
+// 256 rows, fit the merge (splits * kl <= kMaxMerge) and, for lists with 16-bit positions,
+// at most kMaxNarrowSplitRows rows. Every split starts its own lists, and list insertions
+// grow with splits x kl, so small lists take the smallest split count giving four rounds
+// with at most 5% idle in the last, large lists the smallest giving one round at 90%.
+int choose_flat_splits(int64_t n_eff, int64_t groups, int kl, int cus, bool narrow_ids) {
     cus = std::max(cus, 1);
+    const int64_t min_s =
+        narrow_ids ? std::max<int64_t>(1, (n_eff + px::kMaxNarrowSplitRows - 1) /
+                                              px::kMaxNarrowSplitRows)
+                   : 1;
     const int64_t max_s = std::max<int64_t>(
-        1, std::min<int64_t>(n_eff / 256, px::kMaxMerge / std::max(kl, 1)));
-    int best = 1;
+        min_s, std::min<int64_t>(n_eff / 256, px::kMaxMerge / std::max(kl, 1)));
+    const bool large = kl > 32;
+    const int64_t want_rounds = large ? 1 : 4;
+    const double want_eff = large ? 0.90 : 0.95;
+    int64_t best = min_s;
     double best_eff = -1.0;
-    for (int64_t s = 1; s <= std::min<int64_t>(max_s, 256); s = s < 8 ? s * 2 : s + 8) {
+    for (int64_t s = 1; s <= std::min<int64_t>(max_s, 512); s = s < 8 ? s * 2 : s + 8) {
+        if (s < min_s) continue;
         const int64_t blocks = groups * s;
         const int64_t rounds = (blocks + cus - 1) / cus;
         const double eff = (double)blocks / (double)(rounds * cus);
-        if (rounds >= 4 && eff >= 0.95) return (int)s;
-        if (eff > best_eff + 1e-9 || (rounds < 4 && eff >= best_eff - 1e-9)) {
-            best = (int)s;
+        if (rounds >= want_rounds && eff >= want_eff) return (int)s;
+        if (eff > best_eff + 1e-9 || (rounds < want_rounds && eff >= best_eff - 1e-9)) {
+            best = s;
             best_eff = eff;
         }
     }
-    return best;
+    return (int)std::max<int64_t>(best, min_s);
 }
 
 }  // namespace
@@ -287,10 +297,15 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     const int kp = px::flat_list_capacity(kl);
     const int64_t qpb = px::flat_queries_per_block(kp);
     const int64_t groups = (nq + qpb - 1) / qpb;
-    int splits = choose_flat_splits(n_eff, groups, kl, f->dev.cus);
+    const bool narrow = px::flat_list_narrow_ids(kp);
+    int splits = choose_flat_splits(n_eff, groups, kl, f->dev.cus, narrow);
     int64_t rps = (n_eff + splits - 1) / splits;
     rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
+    if (narrow) rps = std::min<int64_t>(rps, px::kMaxNarrowSplitRows);
     splits = (int)std::max<int64_t>(1, (n_eff + rps - 1) / rps);
+    if ((int64_t)splits * kl > px::kMaxMerge)
+        return fail(PX_ERR_BAD_K, "k=" + std::to_string(k) + " over " + std::to_string(n_eff) +
+                                      " rows needs more split lists than the merge holds");
 
     PX_TRY(ws.part_k.reserve(sizeof(float) * nq * splits * kl));
     PX_TRY(ws.part_i.reserve(sizeof(int) * nq * splits * kl));

@@ -13,8 +13,11 @@ inline int64_t padded_dim(int64_t dim) { return (dim + 7) / 8 * 8; }
 
 // Longest candidate list the fused kernels keep per query (k' = k + margin <= 128).
 constexpr int kMaxList = 128;
-// Largest split-merge width: splits * k' candidates per query sorted in LDS.
-constexpr int kMaxMerge = 4096;
+// Largest split-merge width: splits * k' candidates per query sorted in LDS (128 KB).
+constexpr int kMaxMerge = 16384;
+// Longest split whose list positions fit 16-bit offsets (0xffff is the empty sentinel).
+constexpr int64_t kMaxNarrowSplitRows = 65472;
+bool flat_list_narrow_ids(int kp);
 
 struct FlatScanArgs {
     const float* corpus;   // [n][dp] row-major, zero pad columns
@@ -36,7 +39,6 @@ struct FlatScanArgs {
 
 // Waves per workgroup and list capacity used for a list length kl.
 int flat_list_capacity(int kl);
-int flat_waves(int kp);
 int flat_queries_per_block(int kp);
 hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s);
 // Total-order int of +inf: the starting value of FlatScanArgs::gtau.

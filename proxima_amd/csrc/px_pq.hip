@@ -121,8 +121,8 @@ __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
                 const float ck = readlane_f(key[qq], src);
                 const int cid = (int)(base + src);
                 if (!cand_less(ck, cid, tau_k[qq], tau_i[qq])) continue;
-                list_insert<KP>(&lkeys[wave][qq][0], &lids[wave][qq][0], a.kl, ck, cid, tau_k[qq],
-                                tau_i[qq]);
+                list_insert<KP>(&lkeys[wave][qq][0], &lids[wave][qq][0], 0, a.kl, ck, cid,
+                                tau_k[qq], tau_i[qq]);
             }
         }
     }
