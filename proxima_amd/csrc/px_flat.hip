@@ -176,9 +176,10 @@ __device__ __forceinline__ int kth_smallest32(int (&v)[16], int rank) {
 // candidates of its split in LDS. A candidate must beat the list's last entry (tau) and
 // the query's shared threshold gtau, the smallest list tail any split has published so far
 // (a valid bound: that split already holds kl rows at or below it), and a second bound
-// gbound: every split publishes the key in its list slot m - 1 (m = ceil(kl / 32)) to slot
-// (split % 32) of the query's gbest row, so m rows of that split sit at or below it; the
-// ceil(kl / m)-th smallest of the 32 published keys then covers kl rows. gbound is
+// gbound: every split publishes the key in its list slot m - 1 (m = ceil(kl / P), P =
+// min(splits, 32)) to slot (split % 32) of the query's gbest row, so m rows of that split
+// sit at or below it; the ceil(kl / m)-th smallest of the published keys (at most P are
+// needed) then covers kl rows. gbound is
 // recomputed on a geometric schedule of tiles (most of its tightening happens early),
 // which cuts list insertions by an order of magnitude over gtau alone. Equal keys pass only
 // where they can still matter for the lower-id tie rule: at the shared bound, or when the
@@ -217,8 +218,9 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     float tau_k = kInf;   // this wave's list tail for query j (slot kl-1)
     int tau_i = kIdNone;
     int published = 0x7fffffff;
-    const int pub_m = (a.kl + 31) / 32;                     // list slot published is pub_m - 1
-    const int pub_rank = (a.kl + pub_m - 1) / pub_m;        // rank of the bound among 32
+    // published list slot pub_m - 1, so that pub_rank <= min(splits, 32) publishers cover kl
+    const int pub_m = (a.kl + min(a.splits, 32) - 1) / min(a.splits, 32);
+    const int pub_rank = (a.kl + pub_m - 1) / pub_m;
     int published_best = kTotalKeyInf;
     float gbound = kInf;
     int64_t next_refresh = 1;                                // tile index of the next refresh
