@@ -2,12 +2,15 @@
 //
 // Replaces crates/core/src/pq.rs:299-347 (per query: build the m x 2^nbits LUT, sum m
 // LUT entries per code row, heap top-k). A workgroup holds the LUTs of QPB queries in
-// LDS (built in the reference's exact arithmetic, pq.rs:123-136), streams code rows with
-// one coalesced 16-byte load per row (m = 16), and sums each row's m lookups in
-// subspace order starting from +0.0 -- the reference's order (pq.rs:320-323), so the keys
-// are bit-identical to the CPU's. Each wave keeps per-query sorted lists in LDS; the
-// per-wave lists are merged and finished by flat_merge_kernel (no re-rank: exact keys).
-// Work is bounded by code bytes and LUT gathers, not flops: no MFMA here.
+// LDS (built in the reference's exact arithmetic, pq.rs:123-136), interleaved by query
+// (lut[sub][code][query]) so that one LDS read gathers the entry of every query for a
+// (row, subspace): a 16-byte read for four queries instead of four random 4-byte reads.
+// Code rows stream with one coalesced 16-byte load per row (m = 16), and each row's m
+// lookups are summed in subspace order starting from +0.0 -- the reference's order
+// (pq.rs:320-323), so the keys are bit-identical to the CPU's. Each wave keeps per-query
+// sorted lists in LDS; the per-wave lists are merged and finished by flat_merge_kernel
+// (no re-rank: exact keys). Work is bounded by code bytes and LUT gathers, not flops: no
+// MFMA here.
 #include "px_device.h"
 #include "px_kernels.h"
 
@@ -39,10 +42,28 @@ struct alignas(M % 16 == 0 ? 16 : (M % 8 == 0 ? 8 : 1)) CodeRow {
     uint8_t c[M];
 };
 
+// key[qq] += entry of query qq, for the QPB query-interleaved entries at e (one LDS read).
+template <int QPB>
+__device__ __forceinline__ void add_entries(float (&key)[QPB], const float* e) {
+    if constexpr (QPB == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(e);
+        key[0] = key[0] + v.x;
+        key[1] = key[1] + v.y;
+        key[2] = key[2] + v.z;
+        key[3] = key[3] + v.w;
+    } else if constexpr (QPB == 2) {
+        const float2 v = *reinterpret_cast<const float2*>(e);
+        key[0] = key[0] + v.x;
+        key[1] = key[1] + v.y;
+    } else {
+        key[0] = key[0] + e[0];
+    }
+}
+
 // M > 0: compile-time subspace count with a vector code load; M == 0: runtime m.
 template <int QPB, int KP, int M>
 __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
-    extern __shared__ __attribute__((aligned(16))) float lut[];  // [QPB][m * ks]
+    extern __shared__ __attribute__((aligned(16))) float lut[];  // [m * ks][QPB]
     __shared__ float lkeys[kPqWaves][QPB][KP];
     __shared__ int lids[kPqWaves][QPB][KP];
 
@@ -53,10 +74,10 @@ __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
     const int q0 = qg * QPB;
     const float kInf = __int_as_float(0x7f800000);
 
-    // LUT[qq][sub][c] = l2_sqr(q_sub, centroid) | -inner_product(q_sub, centroid)
+    // lut[(sub * ks + c) * QPB + qq] = l2_sqr(q_sub, centroid) | -inner_product(q_sub, centroid)
     for (int x = tid; x < QPB * lut_len; x += kPqThreads) {
-        const int qq = x / lut_len;
-        const int rest = x - qq * lut_len;
+        const int qq = x % QPB;
+        const int rest = x / QPB;
         const int sub = rest / a.ks;
         const int c = rest - sub * a.ks;
         float v = 0.f;
@@ -98,18 +119,12 @@ __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
                 const CodeRow<(M > 0 ? M : 1)> cr =
                     *reinterpret_cast<const CodeRow<(M > 0 ? M : 1)>*>(a.codes + row * M);
 #pragma unroll
-                for (int sub = 0; sub < (M > 0 ? M : 1); ++sub) {
-                    const int off = sub * a.ks + cr.c[sub];
-#pragma unroll
-                    for (int qq = 0; qq < QPB; ++qq) key[qq] = key[qq] + lut[qq * lut_len + off];
-                }
+                for (int sub = 0; sub < (M > 0 ? M : 1); ++sub)
+                    add_entries<QPB>(key, lut + (sub * a.ks + cr.c[sub]) * QPB);
             } else {
                 const uint8_t* cp = a.codes + row * m;
-                for (int sub = 0; sub < m; ++sub) {
-                    const int off = sub * a.ks + cp[sub];
-#pragma unroll
-                    for (int qq = 0; qq < QPB; ++qq) key[qq] = key[qq] + lut[qq * lut_len + off];
-                }
+                for (int sub = 0; sub < m; ++sub)
+                    add_entries<QPB>(key, lut + (sub * a.ks + cp[sub]) * QPB);
             }
         }
 #pragma unroll

@@ -260,3 +260,35 @@ def test_device_pointer_entry(gpu):
     finally:
         for p in ptrs:
             lib.px_dev_free(p)
+
+
+@pytest.mark.parametrize("k", [24, 25, 48, 49, 112, 113, 120])
+def test_list_capacity_boundaries(gpu, k):
+    # k' = k + 8 crosses the list classes (32 int ids | 56 and 120 with 16-bit offsets | 128)
+    data = datagen.sift_like(20_000, 40, 51)
+    q = datagen.sift_like(45, 40, 52)
+    for metric in (oracle.L2, oracle.IP):
+        ids, d, o_ids, o_d = _run(data, q, k, metric)
+        assert np.array_equal(ids, o_ids), (k, metric)
+        assert np.array_equal(d, o_d), (k, metric)
+
+
+def test_large_k_many_splits_16bit_offsets(gpu):
+    # 300k rows at k=100: at least five splits of <= 65,472 rows, positions stored as 16-bit
+    # offsets from each split's start
+    data = datagen.sift_like(300_000, 16, 61)
+    q = datagen.sift_like(40, 16, 62)
+    for metric in (oracle.L2, oracle.IP):
+        ids, d, o_ids, o_d = _run(data, q, 100, metric)
+        assert np.array_equal(ids, o_ids), metric
+        assert np.array_equal(d, o_d), metric
+
+
+def test_large_k_filtered_multichunk(gpu):
+    # dim 200 (two 128-dim query chunks), 30% filter, k=100 and k=40
+    data = datagen.gaussian(40_000, 200, 71)
+    q = datagen.gaussian(30, 200, 72)
+    mask = datagen.mask(40_000, 0.3, 73)
+    for k in (40, 100):
+        for metric in (oracle.L2, oracle.IP):
+            _check(data, q, k, metric, mask=mask)
