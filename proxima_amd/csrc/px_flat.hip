@@ -386,9 +386,11 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     atomicMin(gtau, tk);
                     published = tk;
                 }
+                // atomicMin, not a plain store: a plain store would stay in this XCD's L2,
+                // out of sight of the splits running on the other XCDs
                 const int bk = total_key(lkeys[wave][j][pub_m - 1]);
                 if (h == 0 && qvalid && bk < published_best) {
-                    gbest[split & 31] = bk;
+                    atomicMin(gbest + (split & 31), bk);
                     published_best = bk;
                 }
             } else if (__ballot(kmin <= thr)) {
@@ -425,9 +427,11 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     atomicMin(gtau, tk);
                     published = tk;
                 }
+                // atomicMin, not a plain store: a plain store would stay in this XCD's L2,
+                // out of sight of the splits running on the other XCDs
                 const int bk = total_key(lkeys[wave][j][pub_m - 1]);
                 if (h == 0 && qvalid && bk < published_best) {
-                    gbest[split & 31] = bk;
+                    atomicMin(gbest + (split & 31), bk);
                     published_best = bk;
                 }
             }
