@@ -39,7 +39,7 @@ extern "C" {
 #define PX_ERR_DEVICE (-7)     /* no usable gfx950 device */
 
 /* Largest k a search accepts. */
-#define PX_MAX_K 128
+#define PX_MAX_K 4096
 
 /* Message for the calling thread's last non-zero status (empty string if none). */
 const char* px_last_error(void);
@@ -53,7 +53,7 @@ const char* px_version(void);
  * build links this library in place of knn.cu and CudaKnn works unchanged.
  * Keys are raw (squared L2 or negated inner product); the caller finishes them
  * (gpu.rs:80-93). Padding: id -1, key FLT_MAX. k may be up to PX_MAX_K (the CUDA
- * kernel stopped at 46).
+ * kernel stopped at 46; the reference's FlatIndex takes any k).
  * ---------------------------------------------------------------------------------- */
 typedef struct PxGpuIndex PxGpuIndex;
 
@@ -159,6 +159,10 @@ int px_device_info(int device, char* name, size_t name_len, int* cu_count, int64
 int px_flat_set_timing(px_flat* idx, int enable);
 int px_flat_last_timing(const px_flat* idx, float* scan_ms, float* total_ms, int* splits,
                         int* blocks);
+/* Collect rounds of the handle's last search: 0 when k + 8 <= 128 (per-split candidate
+ * lists), else the rounds of the large-k threshold-collect path (1 when every query
+ * finished in the first). Diagnostic; no counterpart in the reference. */
+int px_flat_last_rounds(const px_flat* idx, int* rounds);
 int px_pq_set_timing(px_pq* idx, int enable);
 int px_pq_last_timing(const px_pq* idx, float* scan_ms, float* total_ms, int* splits,
                       int* blocks);

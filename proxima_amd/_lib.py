@@ -23,7 +23,7 @@ PX_ERR_NONFINITE = -4
 PX_ERR_ARG = -5
 PX_ERR_UNTRAINED = -6
 PX_ERR_DEVICE = -7
-PX_MAX_K = 128
+PX_MAX_K = 4096
 
 _f32p = POINTER(c_float)
 _i64p = POINTER(c_int64)
@@ -71,6 +71,7 @@ SIGNATURES = {
                                POINTER(c_int), POINTER(c_char), c_size_t]),
     "px_flat_set_timing": (c_int, [c_void_p, c_int]),
     "px_flat_last_timing": (c_int, [c_void_p, _f32p, _f32p, POINTER(c_int), POINTER(c_int)]),
+    "px_flat_last_rounds": (c_int, [c_void_p, POINTER(c_int)]),
     "px_pq_set_timing": (c_int, [c_void_p, c_int]),
     "px_pq_last_timing": (c_int, [c_void_p, _f32p, _f32p, POINTER(c_int), POINTER(c_int)]),
     "px_dev_alloc": (c_int, [POINTER(c_void_p), c_size_t]),

@@ -146,4 +146,58 @@ __device__ __forceinline__ float ref_inner_product(const float* a, const float* 
     return sum;
 }
 
+// Same arithmetic and order, for rows stored with a pitch that is a multiple of 8 floats
+// (32-byte aligned, readable up to the next multiple of 8): chunks of 8 are loaded as two
+// float4, four chunks per step so that the loads of a step are in flight together.
+__device__ __forceinline__ float ref_key_v(const float* a, const float* b, int n, bool l2) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const int chunks = n >> 3;
+    auto step = [&](const float4 (&x)[2], const float4 (&y)[2]) {
+        const float xs[8] = {x[0].x, x[0].y, x[0].z, x[0].w, x[1].x, x[1].y, x[1].z, x[1].w};
+        const float ys[8] = {y[0].x, y[0].y, y[0].z, y[0].w, y[1].x, y[1].y, y[1].z, y[1].w};
+#pragma unroll
+        for (int l = 0; l < 8; ++l) {
+            if (l2) {
+                const float d = xs[l] - ys[l];
+                acc[l] = acc[l] + d * d;
+            } else {
+                acc[l] = acc[l] + xs[l] * ys[l];
+            }
+        }
+    };
+    int c = 0;
+    for (; c + 4 <= chunks; c += 4) {
+        float4 x[4][2], y[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            x[u][0] = *reinterpret_cast<const float4*>(a + (c + u) * 8);
+            x[u][1] = *reinterpret_cast<const float4*>(a + (c + u) * 8 + 4);
+            y[u][0] = *reinterpret_cast<const float4*>(b + (c + u) * 8);
+            y[u][1] = *reinterpret_cast<const float4*>(b + (c + u) * 8 + 4);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) step(x[u], y[u]);
+    }
+    for (; c < chunks; ++c) {
+        float4 x[2], y[2];
+        x[0] = *reinterpret_cast<const float4*>(a + c * 8);
+        x[1] = *reinterpret_cast<const float4*>(a + c * 8 + 4);
+        y[0] = *reinterpret_cast<const float4*>(b + c * 8);
+        y[1] = *reinterpret_cast<const float4*>(b + c * 8 + 4);
+        step(x, y);
+    }
+    float sum = 0.f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) sum = sum + acc[l];
+    for (int i = chunks * 8; i < n; ++i) {
+        if (l2) {
+            const float d = a[i] - b[i];
+            sum = sum + d * d;
+        } else {
+            sum = sum + a[i] * b[i];
+        }
+    }
+    return sum;
+}
+
 }  // namespace px

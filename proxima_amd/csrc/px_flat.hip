@@ -184,7 +184,14 @@ __device__ __forceinline__ int kth_smallest32(int (&v)[16], int rank) {
 // which cuts list insertions by an order of magnitude over gtau alone. Equal keys pass only
 // where they can still matter for the lower-id tie rule: at the shared bound, or when the
 // list's tail came from the current tile (earlier tiles hold smaller positions).
-template <int KP, int WAVES, bool L2, bool MULTI, bool FILT>
+//
+// COLLECT replaces the lists: each query has a fixed threshold (key, position), and every
+// row at or below it is appended, unsorted, to one of two regions of its (query slot,
+// split) -- one per lane of the pair that holds the query, each with its own counter, so
+// appends need no cross-lane step; flat_collect_select_kernel takes it from there. The
+// threshold tests of a tile run during the next tile's MFMAs (both waves of a SIMD reach
+// the epilogue together, so an epilogue of its own would leave the matrix unit idle).
+template <int KP, int WAVES, bool L2, bool MULTI, bool FILT, bool COLLECT = false>
 __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     constexpr int NT = WAVES * 64;
     constexpr int kF4PerRow = kChunk / 4;                  // 32 float4 per staged row
@@ -200,8 +207,9 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
     const int qt = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
-    const int q = qt * (WAVES * 32) + wave * 32 + j;
-    const bool qvalid = q < a.nq;
+    const int slot = qt * (WAVES * 32) + wave * 32 + j;
+    const bool qvalid = slot < a.nq;
+    const int q = (COLLECT && a.qlist) ? a.qlist[qvalid ? slot : 0] : slot;
     const int64_t row0 = (int64_t)split * a.rows_per_split;
     const int64_t row1 = min(a.n_eff, row0 + a.rows_per_split);
     const float kInf = __int_as_float(0x7f800000);
@@ -211,9 +219,11 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     const int cc = tid % kF4PerRow;                        // this thread's float4 column
     const int rr0 = tid / kF4PerRow;                       // its first row in a stage
 
-    for (int x = lane; x < 32 * KP; x += 64) {
-        lkeys[wave][x / KP][x % KP] = kInf;
-        lids[wave][x / KP][x % KP] = id_store<IdT>(kIdNone, 0);
+    if constexpr (!COLLECT) {
+        for (int x = lane; x < 32 * KP; x += 64) {
+            lkeys[wave][x / KP][x % KP] = kInf;
+            lids[wave][x / KP][x % KP] = id_store<IdT>(kIdNone, 0);
+        }
     }
     float tau_k = kInf;   // this wave's list tail for query j (slot kl-1)
     int tau_i = kIdNone;
@@ -225,8 +235,36 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     float gbound = kInf;
     int64_t next_refresh = 1;                                // tile index of the next refresh
     const float* qrow = a.queries + (int64_t)(qvalid ? q : 0) * a.dp;
-    int* gtau = a.gtau + (qvalid ? q : 0);
-    int* gbest = a.gbest + (int64_t)(qvalid ? q : 0) * 32;
+    int* gtau = COLLECT ? nullptr : a.gtau + (qvalid ? q : 0);
+    int* gbest = COLLECT ? nullptr : a.gbest + (int64_t)(qvalid ? q : 0) * 32;
+    // collect mode: this query's threshold (nothing passes -inf) and region
+    float cthr = -kInf;
+    int cpos = -1, ccount = 0;
+    float pkey[COLLECT ? 32 : 1];  // keys of the previous tile, tested during this one
+    int pt0 = 0, prem = 0;         // its first position and row count
+    bool pend = false;             // some lane of the wave has a key at or below its threshold
+    auto collect_x = [&](int x) {
+        if constexpr (COLLECT) {
+            const int off = (x >> 4) * 32 + mfma_row(x & 15, h);
+            const float kv = pkey[x];
+            const bool p = off < prem && (kv < cthr || (kv == cthr && pt0 + off <= cpos));
+            if (p) {
+                if (ccount < a.cap) {
+                    const int64_t at =
+                        (((int64_t)slot * a.splits + split) * 2 + h) * a.cap + ccount;
+                    a.cand_keys[at] = kv;
+                    a.cand_pos[at] = pt0 + off;
+                }
+                ++ccount;
+            }
+        }
+    };
+    if constexpr (COLLECT) {
+        if (qvalid && !a.dense) {
+            cthr = from_total_key(a.thr_key[q]);
+            cpos = a.thr_pos[q];
+        }
+    }
 
     // Every load below is unconditional (clamped to a valid address) so that the number of
     // loads in flight is known statically; values are zeroed where they are consumed, not
@@ -308,7 +346,9 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     for (int64_t s = 0; s < nstages; ++s) {
         const int c = MULTI ? (int)(s % nch) : 0;
         const int64_t t0 = row0 + (s / nch) * kTileRows;
-        const int gt_raw = __hip_atomic_load(gtau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        int gt_raw = kTotalKeyInf;
+        if constexpr (!COLLECT)
+            gt_raw = __hip_atomic_load(gtau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int64_t ti = s / nch;
         if constexpr (MULTI) load_b((c + 1) % nch, bn);
         fetch(s + 1);  // past the last stage every row is -1: harmless clamped loads
@@ -328,7 +368,16 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                 acc0 = mfma4(a0, b[g], acc0);
                 acc1 = mfma4(a1, b[g], acc1);
             }
+            if constexpr (COLLECT) {
+                // one compare per row and one uniform branch per pair of rows; the exact
+                // test and the append only where some lane has a row at or below
+                if (pend && __ballot(pkey[2 * g] <= cthr || pkey[2 * g + 1] <= cthr)) {
+                    collect_x(2 * g);
+                    collect_x(2 * g + 1);
+                }
+            }
         }
+        if constexpr (COLLECT) pend = false;
 
         if (c == nch - 1) {
             // Epilogue, branch-free: keys of the 32 rows this lane holds for query j.
@@ -355,6 +404,36 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     }
                 }
             }
+            if constexpr (COLLECT) {
+                const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
+                if (a.dense) {
+                    // every key of the tile, +inf past the split's end: one 128-byte block
+                    // per lane, the wave's 64 blocks contiguous
+                    if (qvalid) {
+                        float* dst = a.cand_keys +
+                                     ((((int64_t)qt * WAVES + wave) * a.splits + split) *
+                                          (a.rows_per_split / kTileRows) + ti) * (64 * 32) +
+                                     lane * 32;
+#pragma unroll
+                        for (int m = 0; m < 8; ++m) {
+                            float v[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) {
+                                const int x = 4 * m + e;
+                                v[e] = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? key[x] : kInf;
+                            }
+                            *reinterpret_cast<float4*>(dst + 4 * m) = make_float4(v[0], v[1], v[2], v[3]);
+                        }
+                    }
+                } else {
+                // tested during the next tile's MFMAs (or after the last tile)
+#pragma unroll
+                for (int x = 0; x < 32; ++x) pkey[x] = key[x];
+                pt0 = (int)t0;
+                prem = rem;
+                pend = __ballot(kmin <= cthr) != 0;
+                }
+            } else {
             // Padding queries get a threshold nothing passes; rows past the split's end
             // (last tile only) are excluded in the slow path below.
             if (ti == next_refresh) {
@@ -435,6 +514,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     published_best = bk;
                 }
             }
+            }  // !COLLECT
         }
 
         commit(s + 1);
@@ -446,6 +526,14 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         __syncthreads();
     }
 
+    if constexpr (COLLECT) {
+        if (pend) {
+#pragma unroll
+            for (int x = 0; x < 32; ++x) collect_x(x);
+        }
+        if (qvalid && !a.dense) a.cand_count[((int64_t)slot * a.splits + split) * 2 + h] = ccount;
+        return;
+    }
     // Write this split's lists: part[q][split][0..kl)
     const int qbase = qt * (WAVES * 32) + wave * 32;
     for (int ql = 0; ql < 32; ++ql) {
@@ -493,6 +581,46 @@ hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s) {
         case 120: return launch_scan_t<120, flat_waves(120)>(a, s);
         default: return launch_scan_t<128, flat_waves(128)>(a, s);
     }
+}
+
+hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s) {
+    constexpr int kWaves = 8;
+    const int64_t qtiles = (a.nq + 32 * kWaves - 1) / (32 * kWaves);
+    const dim3 grid((unsigned)(qtiles * a.splits)), block(kWaves * 64);
+    const bool multi = a.dp > kChunk;
+    if (a.metric == 0) {
+        if (multi) {
+            if (a.rowidx) hipLaunchKernelGGL((flat_scan_kernel<1, kWaves, true, true, true, true>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((flat_scan_kernel<1, kWaves, true, true, false, true>), grid, block, 0, s, a);
+        } else {
+            if (a.rowidx) hipLaunchKernelGGL((flat_scan_kernel<1, kWaves, true, false, true, true>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((flat_scan_kernel<1, kWaves, true, false, false, true>), grid, block, 0, s, a);
+        }
+    } else {
+        if (multi) {
+            if (a.rowidx) hipLaunchKernelGGL((flat_scan_kernel<1, kWaves, false, true, true, true>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((flat_scan_kernel<1, kWaves, false, true, false, true>), grid, block, 0, s, a);
+        } else {
+            if (a.rowidx) hipLaunchKernelGGL((flat_scan_kernel<1, kWaves, false, false, true, true>), grid, block, 0, s, a);
+            else hipLaunchKernelGGL((flat_scan_kernel<1, kWaves, false, false, false, true>), grid, block, 0, s, a);
+        }
+    }
+    return hipGetLastError();
+}
+
+__global__ void sample_rows_kernel(const int* rowidx, int64_t count, int64_t stride, int* row) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= count) return;
+    const int64_t p = i * stride;
+    row[i] = rowidx ? rowidx[p] : (int)p;
+}
+
+hipError_t launch_sample_rows(const int* rowidx, int64_t count, int64_t stride, int* row,
+                              hipStream_t s) {
+    if (count <= 0) return hipSuccess;
+    hipLaunchKernelGGL(sample_rows_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s,
+                       rowidx, count, stride, row);
+    return hipGetLastError();
 }
 
 __global__ void fill_int_kernel(int* p, int64_t n, int v) {
@@ -567,7 +695,7 @@ __global__ __launch_bounds__(256) void flat_merge_kernel(MergeArgs a) {
             if (id != kIdNone && a.corpus) {
                 const float* qv = a.queries + (int64_t)q * a.dp;
                 const float* xv = a.corpus + (int64_t)id * a.dp;
-                kv = a.metric == 0 ? ref_l2_sqr(qv, xv, a.dim) : -ref_inner_product(qv, xv, a.dim);
+                kv = a.metric == 0 ? ref_key_v(qv, xv, a.dim, true) : -ref_key_v(qv, xv, a.dim, false);
             }
             if (id == kIdNone) kv = kInf;
         }
@@ -604,6 +732,262 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {
         big_lds = true;
     }
     hipLaunchKernelGGL(flat_merge_kernel, dim3((unsigned)a.nq), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+// One workgroup per query slot of a collect scan. With every candidate stored and at least
+// kk of them (or every row a candidate), it finishes the query as flat_merge_kernel does:
+// sort by (key, position), re-rank the best kk exactly, sort, emit k. Otherwise it sets the
+// query's next threshold and status 1:
+//   too few (fewer than kk rows at or below the threshold): the next, looser rung;
+//   too many (a region or the LDS overflowed): the kk-th smallest of the candidates it
+//   holds (at least kk + 1 of them: the threshold drops below at least one candidate, and
+//   at least kk rows stay at or below it).
+__global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelectArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char csmem[];
+    float* sk = reinterpret_cast<float*>(csmem);
+    int* si = reinterpret_cast<int*>(sk + a.lcap);
+    __shared__ int s_off[kMaxCollectRegions + 1];
+    __shared__ int s_total, s_over;
+
+    const int b = blockIdx.x;
+    const int q = a.qlist ? a.qlist[b] : b;
+    const int* cnt = a.cand_count + (int64_t)b * a.regions;
+    const float* rk = a.cand_keys + (int64_t)b * a.regions * a.cap;
+    const int* rp = a.cand_pos + (int64_t)b * a.regions * a.cap;
+    const float kInf = __int_as_float(0x7f800000);
+    // region offsets in LDS: each thread sums a run of regions, a block scan places them
+    __shared__ int s_wsum[16];
+    const int nt = blockDim.x, t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    if (t == 0) {
+        s_total = 0;
+        s_over = 0;
+    }
+    const int per = (a.regions + nt - 1) / nt;
+    const int rb0 = min(t * per, a.regions), rb1 = min(rb0 + per, a.regions);
+    int my_stored = 0, my_total = 0, my_over = 0;
+    for (int r = rb0; r < rb1; ++r) {
+        const int c = cnt[r];
+        my_total += c;
+        my_stored += min(c, a.cap);
+        my_over |= c > a.cap;
+    }
+    int incl = my_stored;
+    for (int off = 1; off < 64; off <<= 1) {
+        const int v = __shfl_up(incl, off);
+        if (lane >= off) incl += v;
+    }
+    if (lane == 63) s_wsum[wv] = incl;
+    __syncthreads();
+    int excl = incl - my_stored;
+    for (int w = 0; w < wv; ++w) excl += s_wsum[w];
+    for (int r = rb0; r < rb1; ++r) {
+        s_off[r] = min(excl, a.lcap);
+        excl += min(cnt[r], a.cap);
+    }
+    if (t == nt - 1) s_off[a.regions] = min(excl, a.lcap);
+    if (my_total) atomicAdd(&s_total, my_total);
+    if (my_over) atomicOr(&s_over, 1);
+    __syncthreads();
+    if (t == 0 && s_total > a.lcap) s_over = 1;
+    __syncthreads();
+    const int total = s_total;
+    const int held = s_off[a.regions];  // candidates loaded into LDS (all when !s_over)
+    const bool all_rows = a.thr_key[q] == kTotalKeyInf;
+    const bool finish = !s_over && (total >= a.kk || all_rows);
+    if (!s_over && !finish) {
+        // too few: next rung
+        if (threadIdx.x == 0) {
+            const int r = a.rung[q] + 1;
+            const bool more = r < kRungs;
+            a.thr_key[q] = more ? a.ladder_key[(int64_t)q * kRungs + r] : kTotalKeyInf;
+            a.thr_pos[q] = more ? a.ladder_pos[(int64_t)q * kRungs + r] : kIdNone;
+            a.rung[q] = min(r, kRungs);
+            a.status[q] = 1;
+        }
+        return;
+    }
+    if (s_over && held <= a.kk) {
+        // too many, but too few held to tighten: the caller collects again with a larger cap
+        if (threadIdx.x == 0) a.status[q] = 1;
+        return;
+    }
+
+    int p = 1;
+    while (p < held) p <<= 1;
+    for (int sp = 0; sp < a.regions; ++sp) {
+        const int o = s_off[sp], c = s_off[sp + 1] - o;
+        for (int x = threadIdx.x; x < c; x += blockDim.x) {
+            sk[o + x] = rk[(int64_t)sp * a.cap + x];
+            si[o + x] = rp[(int64_t)sp * a.cap + x];
+        }
+    }
+    for (int x = held + threadIdx.x; x < p; x += blockDim.x) {
+        sk[x] = kInf;
+        si[x] = kIdNone;
+    }
+    bitonic_sort(sk, si, p);
+
+    if (!finish) {
+        // too many: tighten to the kk-th smallest held candidate
+        if (threadIdx.x == 0) {
+            a.thr_key[q] = total_key(sk[a.kk - 1]);
+            a.thr_pos[q] = si[a.kk - 1];
+            a.status[q] = 1;
+        }
+        return;
+    }
+
+    const int keep = min(a.kk, held);
+    int p2 = 1;
+    while (p2 < keep) p2 <<= 1;
+    for (int x = threadIdx.x; x < p2; x += blockDim.x) {
+        float kv = kInf;
+        int id = kIdNone;
+        if (x < keep && si[x] != kIdNone) {
+            id = si[x];
+            if (a.rowidx) id = a.rowidx[id];
+            const float* qv = a.queries + (int64_t)q * a.dp;
+            const float* xv = a.corpus + (int64_t)id * a.dp;
+            kv = a.metric == 0 ? ref_key_v(qv, xv, a.dim, true) : -ref_key_v(qv, xv, a.dim, false);
+        }
+        sk[x] = kv;
+        si[x] = id;
+    }
+    bitonic_sort(sk, si, p2);
+    for (int x = threadIdx.x; x < a.k; x += blockDim.x) {
+        int64_t id = -1;
+        float d;
+        if (x < keep && si[x] != kIdNone) {
+            id = si[x];
+            const float kv = sk[x];
+            d = a.raw_keys ? kv : (a.metric == 0 ? sqrtf(kv) : -kv);
+        } else {
+            d = a.raw_keys ? FLT_MAX : (a.metric == 0 ? FLT_MAX : -FLT_MAX);
+        }
+        a.out_ids[(int64_t)q * a.k + x] = id;
+        a.out_dists[(int64_t)q * a.k + x] = d;
+    }
+    if (threadIdx.x == 0) a.status[q] = 0;
+}
+
+// One workgroup of 1024 threads per query: its sampled keys in registers (up to 24 per
+// thread), three 8-bit radix passes over the top 24 bits of the order-preserving unsigned
+// form of the total-order key, both ranks at once (LDS histograms of 256 bins each); the
+// 8 bits below are taken as ones, so each threshold is the top of the bin that holds its
+// rank. Query q's keys sit in the 64-key blocks of wave group q / 32, lanes q % 32 and + 32.
+__global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
+    constexpr int kPer = kMaxLadderEntries / 1024;
+    constexpr unsigned kNone = 0xffffffffu;
+    __shared__ unsigned hist[kRungs][256];
+    __shared__ unsigned s_prefix[kRungs], s_rank[kRungs];
+    const int q = blockIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+    const int total = a.blocks * 64;
+    const float* base = a.keys + (int64_t)(q >> 5) * a.blocks * (64 * 32) + (q & 31) * 32;
+    unsigned u[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int e = t + i * 1024;
+        const int b = e >> 6, hh = (e >> 5) & 1, x = e & 31;
+        const float kv = e < total ? base[(int64_t)b * (64 * 32) + hh * (32 * 32) + x]
+                                   : __int_as_float(0x7f800000);
+        // +inf (rows past a split's end) is left out
+        u[i] = kv < __int_as_float(0x7f800000) ? (unsigned)total_key(kv) ^ 0x80000000u : kNone;
+    }
+    if (t < kRungs) {
+        s_prefix[t] = 0;
+        s_rank[t] = (unsigned)a.ranks[t];
+    }
+    for (int pass = 0; pass < 3; ++pass) {
+        const int shift = 24 - 8 * pass;  // digit bits [shift, shift + 8)
+        for (int x = t; x < kRungs * 256; x += blockDim.x) (&hist[0][0])[x] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+            if (u[i] == kNone) continue;
+            const unsigned d = (u[i] >> shift) & 0xffu;
+#pragma unroll
+            for (int r = 0; r < kRungs; ++r) {
+                // keys whose higher digits match the rung's prefix so far
+                const bool match = pass == 0 || (u[i] >> (shift + 8)) == s_prefix[r];
+                if (match) atomicAdd(&hist[r][d], 1u);
+            }
+        }
+        __syncthreads();
+        if (wv < kRungs) {
+            // lane holds bins 4 lane .. 4 lane + 3; inclusive scan across the wave
+            unsigned c[4], sum = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                c[e] = hist[wv][4 * lane + e];
+                sum += c[e];
+            }
+            unsigned incl = sum;
+            for (int off = 1; off < 64; off <<= 1) {
+                const unsigned v = __shfl_up(incl, off);
+                if (lane >= off) incl += v;
+            }
+            const unsigned need = s_rank[wv];
+            unsigned before = incl - sum;
+            // the lane whose bins cross the rank picks the digit
+            int digit = -1;
+            unsigned below = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (digit < 0 && before + c[e] >= need) {
+                    digit = 4 * lane + e;
+                    below = before;
+                }
+                before += c[e];
+            }
+            const unsigned long long m = __ballot(digit >= 0);
+            const int src = m ? __builtin_ctzll(m) : 63;
+            const int dsel = __shfl(digit, src);
+            const unsigned bsel = __shfl(below, src);
+            if (lane == 0) {
+                // fewer keys than the rank (not for ranks <= the sample size): +inf
+                s_prefix[wv] = m ? (s_prefix[wv] << 8) | (unsigned)dsel : 0xffffffu;
+                s_rank[wv] = m ? need - bsel : 1u;
+            }
+        }
+        __syncthreads();
+    }
+    if (t < kRungs) {
+        const unsigned top = (s_prefix[t] << 8) | 0xffu;
+        int tk = (int)(top ^ 0x80000000u);
+        if (tk > kTotalKeyInf) tk = kTotalKeyInf;  // a bin reaching past +inf: every row passes
+        a.ladder_key[(int64_t)q * kRungs + t] = tk;
+        a.ladder_pos[(int64_t)q * kRungs + t] = kIdNone;
+        if (t == 0) {
+            a.thr_key[q] = tk;
+            a.thr_pos[q] = kIdNone;
+            a.rung[q] = 0;
+        }
+    }
+}
+
+hipError_t launch_ladder(const LadderArgs& a, hipStream_t s) {
+    if (a.nq <= 0) return hipSuccess;
+    if ((int64_t)a.blocks * 64 > kMaxLadderEntries) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(flat_ladder_kernel, dim3((unsigned)a.nq), dim3(1024), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_collect_select(const CollectSelectArgs& a, int slots, hipStream_t s) {
+    if (slots <= 0) return hipSuccess;
+    const size_t lds = (size_t)a.lcap * 8;
+    static bool big_lds = false;
+    if (lds > 65536 && !big_lds) {
+        const hipError_t e = hipFuncSetAttribute(
+            reinterpret_cast<const void*>(flat_collect_select_kernel),
+            hipFuncAttributeMaxDynamicSharedMemorySize, (int)((size_t)kMaxCollect * 8));
+        if (e != hipSuccess) return e;
+        big_lds = true;
+    }
+    // a quarter of the threads while the sorts are short
+    const int threads = a.lcap >= 8192 ? 1024 : 256;
+    hipLaunchKernelGGL(flat_collect_select_kernel, dim3((unsigned)slots), dim3(threads), lds, s, a);
     return hipGetLastError();
 }
 

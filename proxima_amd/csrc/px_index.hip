@@ -14,6 +14,7 @@
 #include <algorithm>
 #include <cfloat>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -118,6 +119,8 @@ struct Timing {
 // Scratch shared by both index kinds for one search.
 struct Workspace {
     DevBuf q, qn, mask, rowidx, scratch, count, part_k, part_i, out_ids, out_d, gtau, gbest;
+    // collect path (k' past the lists)
+    DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
     int* h_count = nullptr;  // pinned
     int ensure_pinned() {
         if (!h_count) PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_count), sizeof(int)));
@@ -125,7 +128,8 @@ struct Workspace {
     }
     void release() {
         for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids,
-                          &out_d, &gtau, &gbest})
+                          &out_d, &gtau, &gbest, &thr_k, &thr_p, &lad_k, &lad_p, &rung, &status,
+                          &cand_k, &cand_p, &cand_n, &samp_row, &qlist})
             b->release();
         if (h_count) (void)hipHostFree(h_count);
         h_count = nullptr;
@@ -211,6 +215,7 @@ struct px_flat {
     int64_t d_rows = 0, d_cap = 0;
     Workspace ws;
     Timing timing;
+    int last_rounds = 0;           // collect rounds of the last search (0: list path)
     std::mutex mu;
 };
 
@@ -284,6 +289,239 @@ int flat_sync(px_flat* f) {
     return PX_OK;
 }
 
+// Smallest k served by the threshold-collect path for batches of at least
+// kCollectMinQueries queries. Below it the per-split lists are faster (1M x 128, 10,000
+// queries: 24.0 ms a batch at k = 10 against 25.4); at k = 16 the two tie (25.3 / 25.5 ms)
+// and from there the collect path pulls ahead (28.1 / 25.5 ms at k = 24, 46.5 / 25.9 at
+// k = 64). Smaller batches keep the lists, which need no sample pass and no host round
+// trip. The PX_FLAT_COLLECT_FROM_K environment variable overrides the k (read once).
+constexpr int64_t kCollectMinQueries = 256;
+int64_t collect_from_k() {
+    static const int64_t v = [] {
+        const char* e = std::getenv("PX_FLAT_COLLECT_FROM_K");
+        return e && *e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)16;
+    }();
+    return v;
+}
+
+// Candidates beyond k whose keys are recomputed in the reference's arithmetic before the
+// final order is taken (the MFMA keys differ from it by rounding).
+constexpr int64_t kReRankMargin = 8;
+
+// Splits and list layout of a fused list scan over n_eff rows with lists of kl.
+struct ListPlan {
+    int splits = 1;
+    int64_t rps = 64, groups = 1;
+};
+int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int cus, ListPlan* out, int64_t k) {
+    const int kp = px::flat_list_capacity(kl);
+    const int64_t qpb = px::flat_queries_per_block(kp);
+    const int64_t groups = (nq + qpb - 1) / qpb;
+    const bool narrow = px::flat_list_narrow_ids(kp);
+    int splits = choose_flat_splits(n_eff, groups, kl, cus, narrow);
+    int64_t rps = (n_eff + splits - 1) / splits;
+    rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
+    if (narrow) rps = std::min<int64_t>(rps, px::kMaxNarrowSplitRows);
+    splits = (int)std::max<int64_t>(1, (n_eff + rps - 1) / rps);
+    if ((int64_t)splits * kl > px::kMaxMerge)
+        return fail(PX_ERR_BAD_K, "k=" + std::to_string(k) + " over " + std::to_string(n_eff) +
+                                      " rows needs more split lists than the merge holds");
+    out->splits = splits;
+    out->rps = rps;
+    out->groups = groups;
+    return PX_OK;
+}
+
+// Large k (k' = k + margin past the lists): the threshold-collect path.
+//  1. Thresholds from a strided sample of S rows: an all-pass collect scan over the sample
+//     and a radix select give each query the keys of (about) its r0-th and r1-th smallest
+//     sampled rows as a two-rung ladder. r0 is set so that the rows at or below it in the
+//     whole corpus are, with high probability, at least k' but not many more: about
+//     k' * S / n_eff sampled rows are expected below the true k'-th key, and r0 adds five
+//     standard deviations and 5; r1 = 2 r0 + 8 is the fallback.
+//  2. One collect scan appends every row at or below its query's threshold.
+//  3. The select finishes each query that has every candidate and at least k' of them;
+//     the others get a new threshold (next rung, or a tighter one from the candidates) and
+//     go round again, alone. Each round either finishes a query or strictly shrinks its
+//     candidate set, so the loop ends; nearly every query finishes in the first round.
+int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
+                     const int* rowidx, int64_t* d_ids, float* d_out, int raw_keys) {
+    Workspace& ws = f->ws;
+    hipStream_t s = f->stream;
+    const int64_t kk = k + kReRankMargin;
+    const int cus = std::max(f->dev.cus, 1);
+    PX_TRY(ws.thr_k.reserve(sizeof(int) * nq));
+    PX_TRY(ws.thr_p.reserve(sizeof(int) * nq));
+    PX_TRY(ws.lad_k.reserve(sizeof(int) * nq * px::kRungs));
+    PX_TRY(ws.lad_p.reserve(sizeof(int) * nq * px::kRungs));
+    PX_TRY(ws.rung.reserve(sizeof(int) * nq));
+    PX_TRY(ws.status.reserve(sizeof(int) * nq));
+    PX_TRY(f->timing.ensure());
+    if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[0], s));
+
+    // expected candidates per query in the first round
+    double expect = (double)n_eff;
+    if (n_eff <= kk) {
+        // every row is a candidate
+        PX_HIP(px::launch_fill_int(ws.thr_k.as<int>(), nq, px::kTotalKeyInf, s));
+        PX_HIP(px::launch_fill_int(ws.thr_p.as<int>(), nq, 0x7fffffff, s));
+        PX_HIP(px::launch_fill_int(ws.rung.as<int>(), nq, px::kRungs, s));
+    } else {
+        const int64_t S = std::max<int64_t>(
+            1, std::min<int64_t>({n_eff, (int64_t)16384, 80 * n_eff / kk}));
+        const int64_t stride = n_eff / S;
+        const double x = (double)kk * (double)S / (double)n_eff;
+        const int r0 = (int)std::min<int64_t>(S, (int64_t)std::ceil(x + 5.0 * std::sqrt(x) + 5.0));
+        const int r1 = (int)std::min<int64_t>(S, 2 * (int64_t)r0 + 8);
+        expect = std::min<double>((double)n_eff, (double)(r0 + 4) * (double)stride);
+        PX_TRY(ws.samp_row.reserve(sizeof(int) * S));
+        PX_HIP(px::launch_sample_rows(rowidx, S, stride, ws.samp_row.as<int>(), s));
+        // dense keys of the sample: [query tile][wave][split][tile][lane][32]
+        const int64_t groups = (nq + 255) / 256;
+        int64_t splits = choose_flat_splits(S, groups, 1, cus, false);
+        int64_t rps = (S + splits - 1) / splits;
+        rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
+        splits = std::max<int64_t>(1, (S + rps - 1) / rps);
+        const int64_t blocks = splits * (rps / 64);
+        if (blocks * 64 > px::kMaxLadderEntries)
+            return fail(PX_ERR_ARG, "internal: threshold sample too large for the ladder");
+        PX_TRY(ws.cand_k.reserve(sizeof(float) * groups * 256 * blocks * 64));
+        px::FlatScanArgs a{};
+        a.corpus = f->d_x;
+        a.norms = f->d_norm;
+        a.queries = d_q;
+        a.rowidx = ws.samp_row.as<int>();
+        a.n_eff = S;
+        a.rows_per_split = rps;
+        a.dp = (int)f->dp;
+        a.nq = (int)nq;
+        a.splits = (int)splits;
+        a.metric = f->metric;
+        a.cand_keys = ws.cand_k.as<float>();
+        a.dense = 1;
+        PX_HIP(px::launch_flat_collect(a, s));
+        px::LadderArgs la{};
+        la.keys = a.cand_keys;
+        la.blocks = (int)blocks;
+        la.nq = (int)nq;
+        la.ranks[0] = r0;
+        la.ranks[1] = r1;
+        la.ladder_key = ws.lad_k.as<int>();
+        la.ladder_pos = ws.lad_p.as<int>();
+        la.thr_key = ws.thr_k.as<int>();
+        la.thr_pos = ws.thr_p.as<int>();
+        la.rung = ws.rung.as<int>();
+        PX_HIP(px::launch_ladder(la, s));
+    }
+
+    std::vector<int> h_status((size_t)nq), failing;
+    int64_t slots = nq;
+    const int* qlist = nullptr;
+    for (int round = 0;; ++round) {
+        f->last_rounds = round + 1;
+        // splits: about four rounds of workgroups; regions sized for 3x the expected
+        // candidates (per split), and at least 2 k' + 1 after the first round
+        const int64_t groups = (slots + 255) / 256;
+        int64_t splits = std::min<int64_t>(choose_flat_splits(n_eff, groups, 1, cus, false),
+                                           px::kMaxCollectRegions / 2);
+        int64_t rps = (n_eff + splits - 1) / splits;
+        rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
+        splits = std::max<int64_t>(1, (n_eff + rps - 1) / rps);
+        // regions: two per split (one per lane of the pair holding a query)
+        int64_t cap = (int64_t)std::ceil(3.0 * expect / (double)(2 * splits));
+        if (round > 0) cap = std::max<int64_t>(cap, 2 * kk + 1);
+        cap = std::min<int64_t>((cap + 31) / 32 * 32, rps);
+        int64_t lcap = 1;
+        while (lcap < std::max<int64_t>(std::min<int64_t>(2 * splits * cap, px::kMaxCollect), 2 * kk + 1))
+            lcap <<= 1;
+        lcap = std::min<int64_t>(lcap, px::kMaxCollect);
+        PX_TRY(ws.cand_k.reserve(sizeof(float) * slots * splits * 2 * cap));
+        PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * splits * 2 * cap));
+        PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * splits * 2));
+
+        px::FlatScanArgs a{};
+        a.corpus = f->d_x;
+        a.norms = f->d_norm;
+        a.queries = d_q;
+        a.rowidx = rowidx;
+        a.n_eff = n_eff;
+        a.rows_per_split = rps;
+        a.dp = (int)f->dp;
+        a.nq = (int)slots;
+        a.splits = (int)splits;
+        a.metric = f->metric;
+        a.qlist = qlist;
+        a.thr_key = ws.thr_k.as<int>();
+        a.thr_pos = ws.thr_p.as<int>();
+        a.cand_keys = ws.cand_k.as<float>();
+        a.cand_pos = ws.cand_p.as<int>();
+        a.cand_count = ws.cand_n.as<int>();
+        a.cap = (int)cap;
+        PX_HIP(px::launch_flat_collect(a, s));
+        if (round == 0 && f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[1], s));
+
+        px::CollectSelectArgs c{};
+        c.cand_keys = a.cand_keys;
+        c.cand_pos = a.cand_pos;
+        c.cand_count = a.cand_count;
+        c.regions = (int)(2 * splits);
+        c.cap = (int)cap;
+        c.lcap = (int)lcap;
+        c.qlist = qlist;
+        c.rowidx = rowidx;
+        c.thr_key = ws.thr_k.as<int>();
+        c.thr_pos = ws.thr_p.as<int>();
+        c.ladder_key = ws.lad_k.as<int>();
+        c.ladder_pos = ws.lad_p.as<int>();
+        c.rung = ws.rung.as<int>();
+        c.status = ws.status.as<int>();
+        c.kk = (int)kk;
+        c.k = (int)k;
+        c.metric = f->metric;
+        c.corpus = f->d_x;
+        c.queries = d_q;
+        c.dim = (int)f->dim;
+        c.dp = (int)f->dp;
+        c.out_ids = d_ids;
+        c.out_dists = d_out;
+        c.raw_keys = raw_keys;
+        PX_HIP(px::launch_collect_select(c, (int)slots, s));
+        if (round == 0) {
+            f->timing.splits = (int)splits;
+            f->timing.blocks = (int)(groups * splits);
+        }
+        PX_HIP(hipMemcpyAsync(h_status.data(), ws.status.p, sizeof(int) * nq,
+                              hipMemcpyDeviceToHost, s));
+        PX_HIP(hipStreamSynchronize(s));
+        // queries of this round still open
+        std::vector<int> next;
+        if (qlist) {
+            for (int q : failing)
+                if (h_status[(size_t)q]) next.push_back(q);
+        } else {
+            for (int64_t q = 0; q < nq; ++q)
+                if (h_status[(size_t)q]) next.push_back((int)q);
+        }
+        if (next.empty()) break;
+        if (round >= 10000)
+            return fail(PX_ERR_ARG, "large-k selection did not converge");  // unreachable
+        failing.swap(next);
+        PX_TRY(ws.qlist.reserve(sizeof(int) * failing.size()));
+        PX_HIP(hipMemcpyAsync(ws.qlist.p, failing.data(), sizeof(int) * failing.size(),
+                              hipMemcpyHostToDevice, s));
+        qlist = ws.qlist.as<int>();
+        slots = (int64_t)failing.size();
+        expect = (double)(2 * kk + 1);
+    }
+    if (f->timing.enabled) {
+        PX_HIP(hipEventRecord(f->timing.ev[2], s));
+        PX_HIP(hipStreamSynchronize(s));
+        PX_HIP(hipEventElapsedTime(&f->timing.scan_ms, f->timing.ev[0], f->timing.ev[1]));
+        PX_HIP(hipEventElapsedTime(&f->timing.total_ms, f->timing.ev[0], f->timing.ev[2]));
+    }
+    return PX_OK;
+}
+
 // Runs the device pipeline. d_q: [nq][dp] on device. Outputs on device.
 int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
              int64_t* d_ids, float* d_out, int raw_keys) {
@@ -292,20 +530,17 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     int64_t n_eff = f->d_rows;
     const int* rowidx = nullptr;
     if (d_mask) PX_TRY(compact_mask(ws, d_mask, f->d_rows, s, &n_eff, &rowidx));
+    f->last_rounds = 0;
+    const bool collect = k + kReRankMargin > px::kMaxList ||
+                         (k >= collect_from_k() && nq >= kCollectMinQueries);
+    if (collect && n_eff > 0)
+        return flat_run_collect(f, d_q, nq, k, n_eff, rowidx, d_ids, d_out, raw_keys);
 
-    const int kl = (int)std::min<int64_t>(px::kMaxList, k + 8);
-    const int kp = px::flat_list_capacity(kl);
-    const int64_t qpb = px::flat_queries_per_block(kp);
-    const int64_t groups = (nq + qpb - 1) / qpb;
-    const bool narrow = px::flat_list_narrow_ids(kp);
-    int splits = choose_flat_splits(n_eff, groups, kl, f->dev.cus, narrow);
-    int64_t rps = (n_eff + splits - 1) / splits;
-    rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
-    if (narrow) rps = std::min<int64_t>(rps, px::kMaxNarrowSplitRows);
-    splits = (int)std::max<int64_t>(1, (n_eff + rps - 1) / rps);
-    if ((int64_t)splits * kl > px::kMaxMerge)
-        return fail(PX_ERR_BAD_K, "k=" + std::to_string(k) + " over " + std::to_string(n_eff) +
-                                      " rows needs more split lists than the merge holds");
+    const int kl = (int)std::min<int64_t>(px::kMaxList, k + kReRankMargin);
+    ListPlan lp;
+    PX_TRY(plan_list_scan(n_eff, nq, kl, f->dev.cus, &lp, k));
+    const int splits = lp.splits;
+    const int64_t rps = lp.rps, groups = lp.groups;
 
     PX_TRY(ws.part_k.reserve(sizeof(float) * nq * splits * kl));
     PX_TRY(ws.part_i.reserve(sizeof(int) * nq * splits * kl));
@@ -461,6 +696,8 @@ int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_m
     const int* rowidx = nullptr;
     if (d_mask) PX_TRY(compact_mask(ws, d_mask, p->d_rows, s, &n_eff, &rowidx));
 
+    if (k > px::kMaxList)
+        return fail(PX_ERR_BAD_K, "PqIndex searches take k <= " + std::to_string(px::kMaxList));
     const int kl = (int)k;
     const int lists = px::pq_lists_per_split();
     const int64_t qpb = px::pq_queries_per_block((int)p->m, (int)p->ks);
@@ -641,6 +878,12 @@ int px_flat_last_timing(const px_flat* f, float* scan_ms, float* total_ms, int* 
     if (total_ms) *total_ms = f->timing.total_ms;
     if (splits) *splits = f->timing.splits;
     if (blocks) *blocks = f->timing.blocks;
+    return PX_OK;
+}
+
+int px_flat_last_rounds(const px_flat* f, int* rounds) {
+    if (!f) return fail(PX_ERR_ARG, "null index handle");
+    if (rounds) *rounds = f->last_rounds;
     return PX_OK;
 }
 

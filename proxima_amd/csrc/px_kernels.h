@@ -35,6 +35,19 @@ struct FlatScanArgs {
     int* part_ids;         // compacted positions (row ids when unfiltered)
     int* gtau;             // [nq] shared per-query bound, total-order ints; starts at +inf
     int* gbest;            // [nq][32] per-split published list keys, total-order ints; +inf
+    // Collect mode (launch_flat_collect): no lists; every row whose (key, position) is at or
+    // below its query's threshold is appended to the region of (query slot, split).
+    const int* qlist;      // optional: query index of each of the nq slots
+    const int* thr_key;    // [queries] threshold keys as total-order ints (by query index)
+    const int* thr_pos;    // [queries] threshold positions (ties: position <= thr_pos passes)
+    float* cand_keys;      // [nq slots][splits][2][cap]: one region per lane of the query's pair
+    int* cand_pos;         // positions (indices into rowidx when filtered)
+    int* cand_count;       // [nq slots][splits][2] rows that passed; more than cap = overflow
+    int cap;
+    // dense != 0: no thresholds; every key goes to cand_keys as [query tile][wave][split]
+    // [tile of split][lane][32] (keys of rows past a split's end are +inf), cand_keys sized
+    // for whole query tiles of 32 * WAVES
+    int dense;
 };
 
 // Waves per workgroup and list capacity used for a list length kl.
@@ -43,6 +56,64 @@ int flat_queries_per_block(int kp);
 hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s);
 // Total-order int of +inf: the starting value of FlatScanArgs::gtau.
 constexpr int kTotalKeyInf = 0x7f800000;
+// Threshold-collect selection for k' past the lists (k' > kMaxList): thresholds from a
+// strided sample, one collect scan, per-query select; queries whose threshold proved too
+// tight or too loose go round again.
+hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s);
+// Threshold ladder rungs taken from the sample, loosest last; past the last rung a query's
+// threshold is +inf (every row passes).
+constexpr int kRungs = 2;
+// Most candidates one query's select holds in LDS (8 bytes each, 128 KB).
+constexpr int kMaxCollect = 16384;
+// Most candidate regions per query of a collect scan (two per split; the select walks
+// their counts).
+constexpr int kMaxCollectRegions = 1024;
+struct CollectSelectArgs {
+    const float* cand_keys;  // FlatScanArgs regions of the collect scan
+    const int* cand_pos;
+    const int* cand_count;
+    int regions, cap;        // regions per query slot (2 x splits), capacity of each
+    int lcap;                // candidates the launch's LDS holds (power of two <= kMaxCollect)
+    const int* qlist;        // optional: query index of each slot (one workgroup per slot)
+    const int* rowidx;       // optional: position -> row id
+    int* thr_key;            // [queries] in/out
+    int* thr_pos;
+    const int* ladder_key;   // [queries][kRungs]
+    const int* ladder_pos;
+    int* rung;               // [queries] current rung (kRungs once the threshold is +inf)
+    int* status;             // [queries] 0: outputs written; 1: collect again
+    int kk;                  // candidates re-ranked exactly (k + margin)
+    int k;
+    int metric;
+    const float* corpus;
+    const float* queries;
+    int dim, dp;
+    int64_t* out_ids;
+    float* out_dists;
+    int raw_keys;
+};
+hipError_t launch_collect_select(const CollectSelectArgs& a, int slots, hipStream_t s);
+// Threshold ladder from the dense keys of a collect scan over a row sample: per query,
+// rung i is a key value with at least ranks[i] sampled keys at or below it (the upper end
+// of the 2^-24-wide bin, in total order, that holds the ranks[i]-th smallest), position
+// limit kIdNone (every row with that key passes); rung 0 also goes to thr, rung = 0.
+struct LadderArgs {
+    const float* keys;       // FlatScanArgs::dense layout of the sample scan (8 waves)
+    int blocks;              // splits * tiles per split: 64-key blocks per query
+    int nq;
+    int ranks[kRungs];
+    int* ladder_key;         // [nq][kRungs]
+    int* ladder_pos;
+    int* thr_key;            // [nq]
+    int* thr_pos;
+    int* rung;
+};
+// Most sampled keys (64 per block) a ladder workgroup holds in registers.
+constexpr int kMaxLadderEntries = 24576;
+hipError_t launch_ladder(const LadderArgs& a, hipStream_t s);
+// Row sample of the collect path: row[i] = rowidx ? rowidx[i * stride] : i * stride.
+hipError_t launch_sample_rows(const int* rowidx, int64_t count, int64_t stride, int* row,
+                              hipStream_t s);
 hipError_t launch_fill_int(int* p, int64_t n, int v, hipStream_t s);
 
 struct MergeArgs {

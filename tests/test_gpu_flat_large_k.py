@@ -1,0 +1,204 @@
+"""GPU parity of the threshold-collect path of FlatIndex searches.
+
+The reference's FlatIndex takes any k (flat.rs:106-148 keeps a heap of k); the library
+serves k up to PX_MAX_K. For k + 8 > 128, and for k >= 16 in batches of at least 256
+queries, it samples a strided subset of the rows for per-query thresholds, appends every
+row at or below them in one collect scan, and finishes each query whose candidate set is
+complete and large enough; the others go round again with a looser or tighter threshold. These tests compare with the oracle at the
+parity rule, bit for bit on integer-valued data (exact in fp32), and force each kind of
+extra round with data laid out against the sample.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_parity
+from proxima_amd import FlatIndex, Metric, _lib, datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def _key_of(data, queries, metric):
+    def key_of(qi, row):
+        if metric == oracle.L2:
+            return float(oracle.l2_sqr(queries[qi], data[row]))
+        return float(-oracle.inner_product(queries[qi], data[row]))
+    return key_of
+
+
+def _rounds(idx) -> int:
+    r = ctypes.c_int(-1)
+    assert idx._lib.px_flat_last_rounds(idx._h, ctypes.byref(r)) == 0
+    return r.value
+
+
+def _search(data, queries, k, metric, mask=None):
+    idx = FlatIndex(data.shape[1], Metric.L2 if metric == oracle.L2 else Metric.InnerProduct)
+    idx.add(data)
+    if mask is None:
+        ids, d = idx.search_batch(queries, k=k)
+    else:
+        ids, d = idx.search_batch_filtered(queries, mask, k=k)
+    return idx, ids, d
+
+
+def _check(data, queries, k, metric, mask=None, exact=False):
+    print(f"case n={data.shape[0]} dim={data.shape[1]} nq={queries.shape[0]} k={k} "
+          f"metric={metric} mask={'yes' if mask is not None else 'no'}", flush=True)
+    idx, ids, d = _search(data, queries, k, metric, mask)
+    o_ids, o_d, _ = oracle.flat_search(data, queries, k, metric, mask=mask)
+    assert_parity(ids, d, o_ids, o_d, _key_of(data, queries, metric), allow_exempt=not exact)
+    if exact:
+        assert np.array_equal(ids, o_ids)
+        assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+    return _rounds(idx)
+
+
+def _sample_stride(n_eff: int, k: int) -> int:
+    """Stride of the threshold sample: S = min(n_eff, 16384, 80 * n_eff // k') rows taken
+    at positions 0, stride, 2 * stride, ... with stride = n_eff // S and k' = k + 8."""
+    kk = k + 8
+    s = max(1, min(n_eff, 16384, 80 * n_eff // kk))
+    return n_eff // s
+
+
+@pytest.mark.parametrize("k", [121, 300, 1000, 4096])
+def test_sift_like_exact(gpu, k):
+    data = datagen.sift_like(60_000, 128, 31)
+    q = datagen.sift_like(48, 128, 32)
+    rounds = _check(data, q, k, oracle.L2, exact=True)
+    assert rounds >= 1
+
+
+def test_first_k_past_the_lists_and_last_list_k(gpu):
+    # k = 120 is the last k on the per-split lists (k' = 128), k = 121 the first collected
+    data = datagen.sift_like(20_000, 96, 33)
+    q = datagen.sift_like(40, 96, 34)
+    for k in (120, 121):
+        idx, ids, d = _search(data, q, k, oracle.L2)
+        o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2)
+        assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d), k
+        assert (_rounds(idx) == 0) == (k == 120)
+
+
+def test_batch_routing_boundary(gpu):
+    # batches of >= 256 queries switch from the per-split lists to the collect path at k = 16
+    data = datagen.sift_like(30_000, 64, 49)
+    q = datagen.sift_like(300, 64, 50)
+    for k, collected in ((15, False), (16, True), (100, True)):
+        idx, ids, d = _search(data, q, k, oracle.L2)
+        o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2)
+        assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d), k
+        assert (_rounds(idx) > 0) == collected, k
+
+
+@pytest.mark.parametrize("metric", [oracle.L2, oracle.IP])
+@pytest.mark.parametrize("k", [16, 37, 100])
+def test_collect_moderate_k(gpu, metric, k):
+    data = datagen.gaussian(25_000, 72, 53)
+    q = datagen.gaussian(260, 72, 54)
+    _check(data, q, k, metric)
+
+
+def test_collect_filtered_two_chunks_config5_shape(gpu):
+    # the 10M x 384 unit-Gaussian IP workload's shape on 60,000 rows, 10% mask, k = 100
+    data = datagen.unit_gaussian(60_000, 384, 55)
+    q = datagen.unit_gaussian(300, 384, 56)
+    mask = datagen.mask(60_000, 0.1, 57)
+    _check(data, q, 100, oracle.IP, mask=mask)
+
+
+def test_ip_filtered_two_chunks(gpu):
+    # dim 200: two 128-dim query chunks; 30% of the rows kept
+    data = datagen.gaussian(40_000, 200, 35)
+    q = datagen.gaussian(32, 200, 36)
+    mask = datagen.mask(40_000, 0.3, 37)
+    _check(data, q, 500, oracle.IP, mask=mask)
+
+
+def test_l2_gaussian_unfiltered_odd_dim(gpu):
+    data = datagen.gaussian(30_000, 61, 38)
+    q = datagen.gaussian(300, 61, 39)
+    _check(data, q, 256, oracle.L2)
+
+
+def test_k_above_rows_pads(gpu):
+    # every row is a candidate: all 900 rows in order, then padding
+    data = datagen.sift_like(900, 32, 40)
+    q = datagen.sift_like(20, 32, 41)
+    _check(data, q, 2000, oracle.L2, exact=True)
+    mask = datagen.mask(900, 0.5, 42)
+    _check(data, q, 700, oracle.L2, mask=mask, exact=True)
+
+
+def test_exact_ties_lower_row_wins(gpu):
+    # 25 distinct rows repeated: thousands of exactly equal keys; ties go to the lower row
+    base = datagen.sift_like(25, 64, 43)
+    data = np.tile(base, (1200, 1))
+    q = datagen.sift_like(16, 64, 44)
+    _check(data, q, 700, oracle.L2, exact=True)
+
+
+def test_sample_far_overflow_round(gpu):
+    # The sampled rows are far from every query and the rest are near: the sample's
+    # threshold lets nearly every row through, the select overflows, and later rounds
+    # tighten the threshold from the candidates.
+    n, k = 40_000, 992
+    stride = _sample_stride(n, k)
+    rng = np.random.default_rng(45)
+    data = rng.integers(0, 4, size=(n, 48)).astype(np.float32)
+    data[::stride] = 255.0
+    q = rng.integers(0, 3, size=(12, 48)).astype(np.float32)
+    rounds = _check(data, q, k, oracle.L2, exact=True)
+    assert rounds >= 2
+
+
+def test_sample_near_underflow_rounds(gpu):
+    # The sampled rows are the near ones: the sample's thresholds admit too few rows, the
+    # ladder runs out, and the query finishes from an unbounded round.
+    n, k = 40_000, 992
+    stride = _sample_stride(n, k)
+    rng = np.random.default_rng(46)
+    data = rng.integers(200, 256, size=(n, 48)).astype(np.float32)
+    data[::stride] = rng.integers(0, 4, size=(data[::stride].shape[0], 48))
+    q = rng.integers(0, 3, size=(12, 48)).astype(np.float32)
+    rounds = _check(data, q, k, oracle.L2, exact=True)
+    assert rounds >= 3
+
+
+def test_sift_1m_subset(gpu):
+    # the 1M x 128 SIFT-like corpus, 16 of its queries, k = 1000
+    data = datagen.corpus(3)
+    q = datagen.queries(3)[:16]
+    _check(data, q, 1000, oracle.L2, exact=True)
+
+
+def test_knn_seam_raw_keys(gpu):
+    lib = _lib.load()
+    data = datagen.sift_like(5000, 40, 47)
+    q = datagen.sift_like(9, 40, 48)
+    k = 300
+    g = lib.knn_gpu_create(_lib.f32p(data), 5000, 40)
+    assert g
+    try:
+        ids = np.zeros((9, k), dtype=np.int64)
+        keys = np.zeros((9, k), dtype=np.float32)
+        rc = lib.knn_gpu_search(g, _lib.f32p(q), 9, k, 0, _lib.i64p(ids), _lib.f32p(keys))
+        assert rc == 0, _lib.last_error()
+    finally:
+        lib.knn_gpu_free(g)
+    o_ids, _, o_keys = oracle.flat_search(data, q, k, oracle.L2)
+    assert np.array_equal(ids, o_ids)
+    assert np.array_equal(keys, o_keys)
+
+
+def test_k_limit(gpu):
+    idx = FlatIndex(8, Metric.L2)
+    idx.add(np.zeros((10, 8), dtype=np.float32))
+    with pytest.raises(ValueError):
+        idx.search(np.zeros(8, dtype=np.float32), k=_lib.PX_MAX_K + 1)
+    ids, d = idx.search(np.zeros(8, dtype=np.float32), k=_lib.PX_MAX_K)
+    assert ids.shape == (_lib.PX_MAX_K,)
+    assert np.array_equal(ids[:10], np.arange(10)) and (ids[10:] == -1).all()
