@@ -163,6 +163,8 @@ int px_flat_last_timing(const px_flat* idx, float* scan_ms, float* total_ms, int
  * lists), else the rounds of the large-k threshold-collect path (1 when every query
  * finished in the first). Diagnostic; no counterpart in the reference. */
 int px_flat_last_rounds(const px_flat* idx, int* rounds);
+/* The same for PqIndex searches (k <= 128: per-wave lists; above: threshold-collect). */
+int px_pq_last_rounds(const px_pq* idx, int* rounds);
 int px_pq_set_timing(px_pq* idx, int enable);
 int px_pq_last_timing(const px_pq* idx, float* scan_ms, float* total_ms, int* splits,
                       int* blocks);

@@ -847,9 +847,13 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
         if (x < keep && si[x] != kIdNone) {
             id = si[x];
             if (a.rowidx) id = a.rowidx[id];
-            const float* qv = a.queries + (int64_t)q * a.dp;
-            const float* xv = a.corpus + (int64_t)id * a.dp;
-            kv = a.metric == 0 ? ref_key_v(qv, xv, a.dim, true) : -ref_key_v(qv, xv, a.dim, false);
+            kv = sk[x];
+            if (a.corpus) {
+                const float* qv = a.queries + (int64_t)q * a.dp;
+                const float* xv = a.corpus + (int64_t)id * a.dp;
+                kv = a.metric == 0 ? ref_key_v(qv, xv, a.dim, true)
+                                   : -ref_key_v(qv, xv, a.dim, false);
+            }
         }
         sk[x] = kv;
         si[x] = id;
@@ -883,15 +887,17 @@ __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
     __shared__ unsigned s_prefix[kRungs], s_rank[kRungs];
     const int q = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int total = a.blocks * 64;
-    const float* base = a.keys + (int64_t)(q >> 5) * a.blocks * (64 * 32) + (q & 31) * 32;
+    const int total = a.ld ? a.count : a.blocks * 64;
+    const float* base = a.ld ? a.keys + (int64_t)q * a.ld
+                             : a.keys + (int64_t)(q >> 5) * a.blocks * (64 * 32) + (q & 31) * 32;
     unsigned u[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const int e = t + i * 1024;
         const int b = e >> 6, hh = (e >> 5) & 1, x = e & 31;
-        const float kv = e < total ? base[(int64_t)b * (64 * 32) + hh * (32 * 32) + x]
-                                   : __int_as_float(0x7f800000);
+        const float kv = e >= total ? __int_as_float(0x7f800000)
+                         : a.ld    ? base[e]
+                                   : base[(int64_t)b * (64 * 32) + hh * (32 * 32) + x];
         // +inf (rows past a split's end) is left out
         u[i] = kv < __int_as_float(0x7f800000) ? (unsigned)total_key(kv) ^ 0x80000000u : kNone;
     }
@@ -969,7 +975,8 @@ __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
 
 hipError_t launch_ladder(const LadderArgs& a, hipStream_t s) {
     if (a.nq <= 0) return hipSuccess;
-    if ((int64_t)a.blocks * 64 > kMaxLadderEntries) return hipErrorInvalidValue;
+    if ((a.ld ? (int64_t)a.count : (int64_t)a.blocks * 64) > kMaxLadderEntries)
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(flat_ladder_kernel, dim3((unsigned)a.nq), dim3(1024), 0, s, a);
     return hipGetLastError();
 }

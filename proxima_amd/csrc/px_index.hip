@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -234,6 +235,7 @@ struct px_pq {
     int64_t d_rows = 0, d_cap = 0;
     Workspace ws;
     Timing timing;
+    int last_rounds = 0;           // collect rounds of the last search (0: list path)
     std::mutex mu;
 };
 
@@ -332,7 +334,8 @@ int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int cus, ListPlan* out, in
     return PX_OK;
 }
 
-// Large k (k' = k + margin past the lists): the threshold-collect path.
+// The threshold-collect path (large k, and moderate k on large batches), shared by the
+// flat and PQ scans.
 //  1. Thresholds from a strided sample of S rows: an all-pass collect scan over the sample
 //     and a radix select give each query the keys of (about) its r0-th and r1-th smallest
 //     sampled rows as a two-rung ladder. r0 is set so that the rows at or below it in the
@@ -344,20 +347,35 @@ int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int cus, ListPlan* out, in
 //     the others get a new threshold (next rung, or a tighter one from the candidates) and
 //     go round again, alone. Each round either finishes a query or strictly shrinks its
 //     candidate set, so the loop ends; nearly every query finishes in the first round.
-int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
-                     const int* rowidx, int64_t* d_ids, float* d_out, int raw_keys) {
-    Workspace& ws = f->ws;
-    hipStream_t s = f->stream;
-    const int64_t kk = k + kReRankMargin;
-    const int cus = std::max(f->dev.cus, 1);
+struct CollectJob {
+    Workspace* ws = nullptr;
+    hipStream_t stream = nullptr;
+    Timing* timing = nullptr;
+    int* last_rounds = nullptr;
+    int64_t nq = 0, kk = 0, n_eff = 0;
+    int cus = 1;
+    // keys of S rows sampled at the given stride -> ladder rungs r0, r1, thresholds, rung 0
+    std::function<int(int64_t S, int64_t stride, int r0, int r1)> sample;
+    // collect scan over `slots` query slots (qlist: their query indices, or null for all);
+    // returns the candidate regions per slot and their capacity
+    std::function<int(int64_t slots, const int* qlist, double expect, int round,
+                      int64_t* regions, int64_t* cap)>
+        scan;
+    px::CollectSelectArgs sel{};  // metric, corpus (null: no re-rank), dims, k, outputs
+};
+
+int run_collect(CollectJob& j) {
+    Workspace& ws = *j.ws;
+    hipStream_t s = j.stream;
+    const int64_t nq = j.nq, kk = j.kk, n_eff = j.n_eff;
     PX_TRY(ws.thr_k.reserve(sizeof(int) * nq));
     PX_TRY(ws.thr_p.reserve(sizeof(int) * nq));
     PX_TRY(ws.lad_k.reserve(sizeof(int) * nq * px::kRungs));
     PX_TRY(ws.lad_p.reserve(sizeof(int) * nq * px::kRungs));
     PX_TRY(ws.rung.reserve(sizeof(int) * nq));
     PX_TRY(ws.status.reserve(sizeof(int) * nq));
-    PX_TRY(f->timing.ensure());
-    if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[0], s));
+    PX_TRY(j.timing->ensure());
+    if (j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[0], s));
 
     // expected candidates per query in the first round
     double expect = (double)n_eff;
@@ -374,6 +392,95 @@ int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_
         const int r0 = (int)std::min<int64_t>(S, (int64_t)std::ceil(x + 5.0 * std::sqrt(x) + 5.0));
         const int r1 = (int)std::min<int64_t>(S, 2 * (int64_t)r0 + 8);
         expect = std::min<double>((double)n_eff, (double)(r0 + 4) * (double)stride);
+        PX_TRY(j.sample(S, stride, r0, r1));
+    }
+
+    std::vector<int> h_status((size_t)nq), failing;
+    int64_t slots = nq;
+    const int* qlist = nullptr;
+    for (int round = 0;; ++round) {
+        *j.last_rounds = round + 1;
+        int64_t regions = 0, cap = 0;
+        PX_TRY(j.scan(slots, qlist, expect, round, &regions, &cap));
+        if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[1], s));
+        int64_t lcap = 1;
+        while (lcap < std::max<int64_t>(std::min<int64_t>(regions * cap, px::kMaxCollect),
+                                        2 * kk + 1))
+            lcap <<= 1;
+        lcap = std::min<int64_t>(lcap, px::kMaxCollect);
+
+        px::CollectSelectArgs c = j.sel;
+        c.cand_keys = ws.cand_k.as<float>();
+        c.cand_pos = ws.cand_p.as<int>();
+        c.cand_count = ws.cand_n.as<int>();
+        c.regions = (int)regions;
+        c.cap = (int)cap;
+        c.lcap = (int)lcap;
+        c.qlist = qlist;
+        c.thr_key = ws.thr_k.as<int>();
+        c.thr_pos = ws.thr_p.as<int>();
+        c.ladder_key = ws.lad_k.as<int>();
+        c.ladder_pos = ws.lad_p.as<int>();
+        c.rung = ws.rung.as<int>();
+        c.status = ws.status.as<int>();
+        c.kk = (int)kk;
+        PX_HIP(px::launch_collect_select(c, (int)slots, s));
+        PX_HIP(hipMemcpyAsync(h_status.data(), ws.status.p, sizeof(int) * nq,
+                              hipMemcpyDeviceToHost, s));
+        PX_HIP(hipStreamSynchronize(s));
+        // queries of this round still open
+        std::vector<int> next;
+        if (qlist) {
+            for (int q : failing)
+                if (h_status[(size_t)q]) next.push_back(q);
+        } else {
+            for (int64_t q = 0; q < nq; ++q)
+                if (h_status[(size_t)q]) next.push_back((int)q);
+        }
+        if (next.empty()) break;
+        if (round >= 10000)
+            return fail(PX_ERR_ARG, "large-k selection did not converge");  // unreachable
+        failing.swap(next);
+        PX_TRY(ws.qlist.reserve(sizeof(int) * failing.size()));
+        PX_HIP(hipMemcpyAsync(ws.qlist.p, failing.data(), sizeof(int) * failing.size(),
+                              hipMemcpyHostToDevice, s));
+        qlist = ws.qlist.as<int>();
+        slots = (int64_t)failing.size();
+        expect = (double)(2 * kk + 1);
+    }
+    if (j.timing->enabled) {
+        PX_HIP(hipEventRecord(j.timing->ev[2], s));
+        PX_HIP(hipStreamSynchronize(s));
+        PX_HIP(hipEventElapsedTime(&j.timing->scan_ms, j.timing->ev[0], j.timing->ev[1]));
+        PX_HIP(hipEventElapsedTime(&j.timing->total_ms, j.timing->ev[0], j.timing->ev[2]));
+    }
+    return PX_OK;
+}
+
+// Region capacity of a collect round: 3x the expected candidates spread over the regions,
+// at least 2 k' + 1 after the first round (so an overflowing region holds enough to
+// tighten from), whole multiples of 32, never more than a region can receive.
+int64_t collect_cap(double expect, int64_t regions, int round, int64_t kk, int64_t most) {
+    int64_t cap = (int64_t)std::ceil(3.0 * expect / (double)regions);
+    if (round > 0) cap = std::max<int64_t>(cap, 2 * kk + 1);
+    return std::max<int64_t>(1, std::min<int64_t>((cap + 31) / 32 * 32, most));
+}
+
+int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
+                     const int* rowidx, int64_t* d_ids, float* d_out, int raw_keys) {
+    Workspace& ws = f->ws;
+    hipStream_t s = f->stream;
+    const int cus = std::max(f->dev.cus, 1);
+    CollectJob j;
+    j.ws = &ws;
+    j.stream = s;
+    j.timing = &f->timing;
+    j.last_rounds = &f->last_rounds;
+    j.nq = nq;
+    j.kk = k + kReRankMargin;
+    j.n_eff = n_eff;
+    j.cus = cus;
+    j.sample = [&](int64_t S, int64_t stride, int r0, int r1) -> int {
         PX_TRY(ws.samp_row.reserve(sizeof(int) * S));
         PX_HIP(px::launch_sample_rows(rowidx, S, stride, ws.samp_row.as<int>(), s));
         // dense keys of the sample: [query tile][wave][split][tile][lane][32]
@@ -412,33 +519,23 @@ int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_
         la.thr_pos = ws.thr_p.as<int>();
         la.rung = ws.rung.as<int>();
         PX_HIP(px::launch_ladder(la, s));
-    }
-
-    std::vector<int> h_status((size_t)nq), failing;
-    int64_t slots = nq;
-    const int* qlist = nullptr;
-    for (int round = 0;; ++round) {
-        f->last_rounds = round + 1;
-        // splits: about four rounds of workgroups; regions sized for 3x the expected
-        // candidates (per split), and at least 2 k' + 1 after the first round
+        return PX_OK;
+    };
+    j.scan = [&](int64_t slots, const int* qlist, double expect, int round, int64_t* regions,
+                 int64_t* cap) -> int {
         const int64_t groups = (slots + 255) / 256;
         int64_t splits = std::min<int64_t>(choose_flat_splits(n_eff, groups, 1, cus, false),
                                            px::kMaxCollectRegions / 2);
         int64_t rps = (n_eff + splits - 1) / splits;
         rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
         splits = std::max<int64_t>(1, (n_eff + rps - 1) / rps);
-        // regions: two per split (one per lane of the pair holding a query)
-        int64_t cap = (int64_t)std::ceil(3.0 * expect / (double)(2 * splits));
-        if (round > 0) cap = std::max<int64_t>(cap, 2 * kk + 1);
-        cap = std::min<int64_t>((cap + 31) / 32 * 32, rps);
-        int64_t lcap = 1;
-        while (lcap < std::max<int64_t>(std::min<int64_t>(2 * splits * cap, px::kMaxCollect), 2 * kk + 1))
-            lcap <<= 1;
-        lcap = std::min<int64_t>(lcap, px::kMaxCollect);
-        PX_TRY(ws.cand_k.reserve(sizeof(float) * slots * splits * 2 * cap));
-        PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * splits * 2 * cap));
-        PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * splits * 2));
-
+        // two regions per split (one per lane of the pair holding a query), each of which
+        // receives at most half the split's rows
+        *regions = 2 * splits;
+        *cap = collect_cap(expect, *regions, round, j.kk, rps / 2);
+        PX_TRY(ws.cand_k.reserve(sizeof(float) * slots * *regions * *cap));
+        PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * *regions * *cap));
+        PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * *regions));
         px::FlatScanArgs a{};
         a.corpus = f->d_x;
         a.norms = f->d_norm;
@@ -456,70 +553,25 @@ int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_
         a.cand_keys = ws.cand_k.as<float>();
         a.cand_pos = ws.cand_p.as<int>();
         a.cand_count = ws.cand_n.as<int>();
-        a.cap = (int)cap;
+        a.cap = (int)*cap;
         PX_HIP(px::launch_flat_collect(a, s));
-        if (round == 0 && f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[1], s));
-
-        px::CollectSelectArgs c{};
-        c.cand_keys = a.cand_keys;
-        c.cand_pos = a.cand_pos;
-        c.cand_count = a.cand_count;
-        c.regions = (int)(2 * splits);
-        c.cap = (int)cap;
-        c.lcap = (int)lcap;
-        c.qlist = qlist;
-        c.rowidx = rowidx;
-        c.thr_key = ws.thr_k.as<int>();
-        c.thr_pos = ws.thr_p.as<int>();
-        c.ladder_key = ws.lad_k.as<int>();
-        c.ladder_pos = ws.lad_p.as<int>();
-        c.rung = ws.rung.as<int>();
-        c.status = ws.status.as<int>();
-        c.kk = (int)kk;
-        c.k = (int)k;
-        c.metric = f->metric;
-        c.corpus = f->d_x;
-        c.queries = d_q;
-        c.dim = (int)f->dim;
-        c.dp = (int)f->dp;
-        c.out_ids = d_ids;
-        c.out_dists = d_out;
-        c.raw_keys = raw_keys;
-        PX_HIP(px::launch_collect_select(c, (int)slots, s));
         if (round == 0) {
             f->timing.splits = (int)splits;
             f->timing.blocks = (int)(groups * splits);
         }
-        PX_HIP(hipMemcpyAsync(h_status.data(), ws.status.p, sizeof(int) * nq,
-                              hipMemcpyDeviceToHost, s));
-        PX_HIP(hipStreamSynchronize(s));
-        // queries of this round still open
-        std::vector<int> next;
-        if (qlist) {
-            for (int q : failing)
-                if (h_status[(size_t)q]) next.push_back(q);
-        } else {
-            for (int64_t q = 0; q < nq; ++q)
-                if (h_status[(size_t)q]) next.push_back((int)q);
-        }
-        if (next.empty()) break;
-        if (round >= 10000)
-            return fail(PX_ERR_ARG, "large-k selection did not converge");  // unreachable
-        failing.swap(next);
-        PX_TRY(ws.qlist.reserve(sizeof(int) * failing.size()));
-        PX_HIP(hipMemcpyAsync(ws.qlist.p, failing.data(), sizeof(int) * failing.size(),
-                              hipMemcpyHostToDevice, s));
-        qlist = ws.qlist.as<int>();
-        slots = (int64_t)failing.size();
-        expect = (double)(2 * kk + 1);
-    }
-    if (f->timing.enabled) {
-        PX_HIP(hipEventRecord(f->timing.ev[2], s));
-        PX_HIP(hipStreamSynchronize(s));
-        PX_HIP(hipEventElapsedTime(&f->timing.scan_ms, f->timing.ev[0], f->timing.ev[1]));
-        PX_HIP(hipEventElapsedTime(&f->timing.total_ms, f->timing.ev[0], f->timing.ev[2]));
-    }
-    return PX_OK;
+        return PX_OK;
+    };
+    j.sel.rowidx = rowidx;
+    j.sel.k = (int)k;
+    j.sel.metric = f->metric;
+    j.sel.corpus = f->d_x;
+    j.sel.queries = d_q;
+    j.sel.dim = (int)f->dim;
+    j.sel.dp = (int)f->dp;
+    j.sel.out_ids = d_ids;
+    j.sel.out_dists = d_out;
+    j.sel.raw_keys = raw_keys;
+    return run_collect(j);
 }
 
 // Runs the device pipeline. d_q: [nq][dp] on device. Outputs on device.
@@ -688,6 +740,113 @@ int pq_sync(px_pq* p) {
     return PX_OK;
 }
 
+// k past the lists: the threshold-collect path with exact ADC keys (no re-rank, k' = k).
+int pq_run_collect(px_pq* p, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
+                   const int* rowidx, int64_t* d_ids, float* d_out) {
+    Workspace& ws = p->ws;
+    hipStream_t s = p->stream;
+    const int cus = std::max(p->dev.cus, 1);
+    const int waves = px::pq_lists_per_split();
+    const int64_t qpb = px::pq_queries_per_block((int)p->m, (int)p->ks);
+    auto base_args = [&]() {
+        px::PqScanArgs a{};
+        a.codes = p->d_codes;
+        a.codebooks = p->d_books;
+        a.queries = d_q;
+        a.dim = (int)p->dim;
+        a.m = (int)p->m;
+        a.ks = (int)p->ks;
+        a.dsub = (int)p->dsub;
+        a.metric = p->metric;
+        return a;
+    };
+    auto plan = [&](int64_t rows, int64_t slots, int64_t* splits, int64_t* rps) {
+        const int64_t groups = (slots + qpb - 1) / qpb;
+        *splits = std::min<int64_t>(choose_splits(rows, groups, waves, 1, cus, 4096),
+                                    px::kMaxCollectRegions / waves);
+        *rps = (rows + *splits - 1) / *splits;
+        *rps = std::max<int64_t>((*rps + 255) / 256 * 256, 256);
+        *splits = std::max<int64_t>(1, (rows + *rps - 1) / *rps);
+    };
+    CollectJob j;
+    j.ws = &ws;
+    j.stream = s;
+    j.timing = &p->timing;
+    j.last_rounds = &p->last_rounds;
+    j.nq = nq;
+    j.kk = k;
+    j.n_eff = n_eff;
+    j.cus = cus;
+    j.sample = [&](int64_t S, int64_t stride, int r0, int r1) -> int {
+        PX_TRY(ws.samp_row.reserve(sizeof(int) * S));
+        PX_HIP(px::launch_sample_rows(rowidx, S, stride, ws.samp_row.as<int>(), s));
+        PX_TRY(ws.cand_k.reserve(sizeof(float) * nq * S));
+        int64_t splits, rps;
+        plan(S, nq, &splits, &rps);
+        px::PqScanArgs a = base_args();
+        a.rowidx = ws.samp_row.as<int>();
+        a.n_eff = S;
+        a.rows_per_split = rps;
+        a.nq = (int)nq;
+        a.splits = (int)splits;
+        a.cand_keys = ws.cand_k.as<float>();
+        a.dense = 1;
+        PX_HIP(px::launch_pq_collect(a, s));
+        px::LadderArgs la{};
+        la.keys = a.cand_keys;
+        la.ld = S;
+        la.count = (int)S;
+        la.nq = (int)nq;
+        la.ranks[0] = r0;
+        la.ranks[1] = r1;
+        la.ladder_key = ws.lad_k.as<int>();
+        la.ladder_pos = ws.lad_p.as<int>();
+        la.thr_key = ws.thr_k.as<int>();
+        la.thr_pos = ws.thr_p.as<int>();
+        la.rung = ws.rung.as<int>();
+        PX_HIP(px::launch_ladder(la, s));
+        return PX_OK;
+    };
+    j.scan = [&](int64_t slots, const int* qlist, double expect, int round, int64_t* regions,
+                 int64_t* cap) -> int {
+        int64_t splits, rps;
+        plan(n_eff, slots, &splits, &rps);
+        // one region per wave of a split; a wave takes 64 of every 256 rows
+        *regions = splits * waves;
+        *cap = collect_cap(expect, *regions, round, j.kk, rps / waves);
+        PX_TRY(ws.cand_k.reserve(sizeof(float) * slots * *regions * *cap));
+        PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * *regions * *cap));
+        PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * *regions));
+        px::PqScanArgs a = base_args();
+        a.rowidx = rowidx;
+        a.n_eff = n_eff;
+        a.rows_per_split = rps;
+        a.nq = (int)slots;
+        a.splits = (int)splits;
+        a.qlist = qlist;
+        a.thr_key = ws.thr_k.as<int>();
+        a.thr_pos = ws.thr_p.as<int>();
+        a.cand_keys = ws.cand_k.as<float>();
+        a.cand_pos = ws.cand_p.as<int>();
+        a.cand_count = ws.cand_n.as<int>();
+        a.cap = (int)*cap;
+        PX_HIP(px::launch_pq_collect(a, s));
+        if (round == 0) {
+            p->timing.splits = (int)splits;
+            p->timing.blocks = (int)(((slots + qpb - 1) / qpb) * splits);
+        }
+        return PX_OK;
+    };
+    j.sel.rowidx = rowidx;
+    j.sel.k = (int)k;
+    j.sel.metric = p->metric;
+    j.sel.corpus = nullptr;  // ADC keys are the reference's already
+    j.sel.out_ids = d_ids;
+    j.sel.out_dists = d_out;
+    j.sel.raw_keys = 0;
+    return run_collect(j);
+}
+
 int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
            int64_t* d_ids, float* d_out) {
     Workspace& ws = p->ws;
@@ -696,9 +855,9 @@ int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_m
     const int* rowidx = nullptr;
     if (d_mask) PX_TRY(compact_mask(ws, d_mask, p->d_rows, s, &n_eff, &rowidx));
 
-    if (k > px::kMaxList)
-        return fail(PX_ERR_BAD_K, "PqIndex searches take k <= " + std::to_string(px::kMaxList));
-    const int kl = (int)k;
+    p->last_rounds = 0;
+    if (k > px::kMaxList && n_eff > 0) return pq_run_collect(p, d_q, nq, k, n_eff, rowidx, d_ids, d_out);
+    const int kl = (int)std::min<int64_t>(k, px::kMaxList);
     const int lists = px::pq_lists_per_split();
     const int64_t qpb = px::pq_queries_per_block((int)p->m, (int)p->ks);
     const int64_t groups = (nq + qpb - 1) / qpb;
@@ -884,6 +1043,12 @@ int px_flat_last_timing(const px_flat* f, float* scan_ms, float* total_ms, int* 
 int px_flat_last_rounds(const px_flat* f, int* rounds) {
     if (!f) return fail(PX_ERR_ARG, "null index handle");
     if (rounds) *rounds = f->last_rounds;
+    return PX_OK;
+}
+
+int px_pq_last_rounds(const px_pq* p, int* rounds) {
+    if (!p) return fail(PX_ERR_ARG, "null index handle");
+    if (rounds) *rounds = p->last_rounds;
     return PX_OK;
 }
 

@@ -85,7 +85,7 @@ struct CollectSelectArgs {
     int kk;                  // candidates re-ranked exactly (k + margin)
     int k;
     int metric;
-    const float* corpus;
+    const float* corpus;     // nullptr: keys are exact already (PQ), no re-rank
     const float* queries;
     int dim, dp;
     int64_t* out_ids;
@@ -98,8 +98,11 @@ hipError_t launch_collect_select(const CollectSelectArgs& a, int slots, hipStrea
 // of the 2^-24-wide bin, in total order, that holds the ranks[i]-th smallest), position
 // limit kIdNone (every row with that key passes); rung 0 also goes to thr, rung = 0.
 struct LadderArgs {
-    const float* keys;       // FlatScanArgs::dense layout of the sample scan (8 waves)
-    int blocks;              // splits * tiles per split: 64-key blocks per query
+    const float* keys;       // FlatScanArgs::dense layout of the sample scan (8 waves), or
+                             // row-major [nq][ld] when ld > 0
+    int blocks;              // dense layout: splits * tiles per split (64-key blocks a query)
+    int64_t ld;              // row-major layout: row pitch; count keys a query
+    int count;
     int nq;
     int ranks[kRungs];
     int* ladder_key;         // [nq][kRungs]
@@ -161,11 +164,23 @@ struct PqScanArgs {
     int metric;
     float* part_keys;         // [nq][splits * waves][kl]
     int* part_ids;
+    // Collect mode (launch_pq_collect), as FlatScanArgs: thresholds by query index, regions
+    // [nq slots][splits][waves][cap] with counts [nq slots][splits][waves]; or, with dense,
+    // every key to cand_keys[q][n_eff] (no thresholds, no counts).
+    const int* qlist;
+    const int* thr_key;
+    const int* thr_pos;
+    float* cand_keys;
+    int* cand_pos;
+    int* cand_count;
+    int cap;
+    int dense;
 };
 int pq_list_capacity(int kl);
 int pq_lists_per_split();
 int pq_queries_per_block(int m, int ks);
 hipError_t launch_pq_scan(const PqScanArgs& a, hipStream_t s);
+hipError_t launch_pq_collect(const PqScanArgs& a, hipStream_t s);
 
 // Plain streaming copy (calibrates HBM traffic counters against known bytes).
 hipError_t launch_copy(const float4* src, float4* dst, int64_t n4, hipStream_t s);

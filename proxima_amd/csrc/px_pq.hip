@@ -61,7 +61,10 @@ __device__ __forceinline__ void add_entries(float (&key)[QPB], const float* e) {
 }
 
 // M > 0: compile-time subspace count with a vector code load; M == 0: runtime m.
-template <int QPB, int KP, int M>
+// COLLECT (k past the lists): no lists; each wave appends every row at or below its
+// query's threshold (key, position) to its region of (query slot, split, wave), or, with
+// a.dense, writes every key to cand_keys[q][n_eff].
+template <int QPB, int KP, int M, bool COLLECT = false>
 __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
     extern __shared__ __attribute__((aligned(16))) float lut[];  // [m * ks][QPB]
     __shared__ float lkeys[kPqWaves][QPB][KP];
@@ -73,6 +76,8 @@ __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
     const int qg = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
     const int q0 = qg * QPB;
     const float kInf = __int_as_float(0x7f800000);
+    // query index of slot q0 + qq (a retry round lists the queries it serves)
+    auto qidx = [&](int qq) { return (COLLECT && a.qlist) ? a.qlist[q0 + qq] : q0 + qq; };
 
     // lut[(sub * ks + c) * QPB + qq] = l2_sqr(q_sub, centroid) | -inner_product(q_sub, centroid)
     for (int x = tid; x < QPB * lut_len; x += kPqThreads) {
@@ -82,15 +87,17 @@ __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
         const int c = rest - sub * a.ks;
         float v = 0.f;
         if (q0 + qq < a.nq) {
-            const float* qs = a.queries + (int64_t)(q0 + qq) * a.dim + sub * a.dsub;
+            const float* qs = a.queries + (int64_t)qidx(qq) * a.dim + sub * a.dsub;
             const float* cen = a.codebooks + ((int64_t)sub * a.ks + c) * a.dsub;
             v = a.metric == 0 ? ref_l2_sqr(qs, cen, a.dsub) : -ref_inner_product(qs, cen, a.dsub);
         }
         lut[x] = v;
     }
-    for (int x = lane; x < QPB * KP; x += 64) {
-        lkeys[wave][x / KP][x % KP] = kInf;
-        lids[wave][x / KP][x % KP] = kIdNone;
+    if constexpr (!COLLECT) {
+        for (int x = lane; x < QPB * KP; x += 64) {
+            lkeys[wave][x / KP][x % KP] = kInf;
+            lids[wave][x / KP][x % KP] = kIdNone;
+        }
     }
     __syncthreads();
 
@@ -104,6 +111,20 @@ __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
     bool qok[QPB];
 #pragma unroll
     for (int qq = 0; qq < QPB; ++qq) qok[qq] = q0 + qq < a.nq;
+    // collect mode: thresholds (nothing passes -inf) and append counters
+    float cthr[QPB];
+    int cpos[QPB], ccount[QPB];
+#pragma unroll
+    for (int qq = 0; qq < QPB; ++qq) {
+        cthr[qq] = -kInf;
+        cpos[qq] = -1;
+        ccount[qq] = 0;
+        if (COLLECT && !a.dense && qok[qq]) {
+            cthr[qq] = __int_as_float(a.thr_key[qidx(qq)] ^
+                                      (int)(((unsigned)(a.thr_key[qidx(qq)] >> 31)) >> 1));
+            cpos[qq] = a.thr_pos[qidx(qq)];
+        }
+    }
 
     const int64_t row0 = (int64_t)split * a.rows_per_split;
     const int64_t row1 = min(a.n_eff, row0 + a.rows_per_split);
@@ -127,6 +148,29 @@ __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
                     add_entries<QPB>(key, lut + (sub * a.ks + cp[sub]) * QPB);
             }
         }
+        if constexpr (COLLECT) {
+#pragma unroll
+            for (int qq = 0; qq < QPB; ++qq) {
+                if (a.dense) {
+                    if (valid && qok[qq]) a.cand_keys[(int64_t)(q0 + qq) * a.n_eff + pos] = key[qq];
+                    continue;
+                }
+                const bool p = valid && (key[qq] < cthr[qq] ||
+                                         (key[qq] == cthr[qq] && pos <= (int64_t)cpos[qq]));
+                const unsigned long long m = __ballot(p);
+                if (m) {
+                    const int w = ccount[qq] + __popcll(m & ((1ull << lane) - 1ull));
+                    if (p && w < a.cap) {
+                        const int64_t at =
+                            (((int64_t)(q0 + qq) * a.splits + split) * kPqWaves + wave) * a.cap + w;
+                        a.cand_keys[at] = key[qq];
+                        a.cand_pos[at] = (int)pos;
+                    }
+                    ccount[qq] += __popcll(m);
+                }
+            }
+            continue;
+        }
 #pragma unroll
         for (int qq = 0; qq < QPB; ++qq) {
             unsigned long long msk = __ballot(valid && qok[qq] && key[qq] <= tau_k[qq]);
@@ -142,6 +186,16 @@ __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
         }
     }
 
+    if constexpr (COLLECT) {
+        if (!a.dense && lane == 0) {
+#pragma unroll
+            for (int qq = 0; qq < QPB; ++qq)
+                if (qok[qq])
+                    a.cand_count[((int64_t)(q0 + qq) * a.splits + split) * kPqWaves + wave] =
+                        ccount[qq];
+        }
+        return;
+    }
     // part[q][split * waves + wave][0..kl)
     const int width = a.splits * kPqWaves;
 #pragma unroll
@@ -175,6 +229,28 @@ static hipError_t launch_pq_k(const PqScanArgs& a, hipStream_t s) {
         case 4: return launch_pq_q<4, KP>(a, s);
         case 2: return launch_pq_q<2, KP>(a, s);
         default: return launch_pq_q<1, KP>(a, s);
+    }
+}
+
+template <int QPB>
+static hipError_t launch_pq_collect_q(const PqScanArgs& a, hipStream_t s) {
+    const int64_t groups = (a.nq + QPB - 1) / QPB;
+    const dim3 grid((unsigned)(groups * a.splits));
+    const size_t lds = (size_t)QPB * a.m * a.ks * sizeof(float);
+    if (a.m == 16)
+        hipLaunchKernelGGL((pq_scan_kernel<QPB, 1, 16, true>), grid, dim3(kPqThreads), lds, s, a);
+    else if (a.m == 8)
+        hipLaunchKernelGGL((pq_scan_kernel<QPB, 1, 8, true>), grid, dim3(kPqThreads), lds, s, a);
+    else
+        hipLaunchKernelGGL((pq_scan_kernel<QPB, 1, 0, true>), grid, dim3(kPqThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+hipError_t launch_pq_collect(const PqScanArgs& a, hipStream_t s) {
+    switch (pq_queries_per_block(a.m, a.ks)) {
+        case 4: return launch_pq_collect_q<4>(a, s);
+        case 2: return launch_pq_collect_q<2>(a, s);
+        default: return launch_pq_collect_q<1>(a, s);
     }
 }
 
