@@ -13,6 +13,11 @@ host's cores, and the same sample checks parity of the GPU results.
 
   python bench.py [--steps K] [--warmup W] [--workload flat|pq|copy] [--config 1|2|3|5]
                   [--k K] [--n N] [--nq NQ] [--mask] [--cpu-seconds S] [--gpus 1]
+                  [--envelope PATH]
+
+--envelope also writes the run as a results envelope in the reference's artefact format
+(schema_version 1, provenance, workload, results; crates/core/examples/gpu_knn.rs:274-333,
+bench/results/gpu.json) for the flat and PQ workloads.
 """
 from __future__ import annotations
 
@@ -130,14 +135,32 @@ def bench_flat(args, dev):
     cfg = datagen.CONFIGS[c]
     if cfg["kind"] != "flat":
         raise SystemExit(f"workload {c} is not a FlatIndex workload")
-    n = args.n or cfg["n"]
-    nq = args.nq or cfg["nq"]
-    k = args.k or cfg["k"][0]
-    dim = cfg["dim"]
-    l2 = cfg["metric"] == "L2"
-    log(f"[bench] workload {c}: generating corpus {n} x {dim} ({cfg['dist']}) and {nq} queries")
-    data = datagen.corpus(c, rows=n)
-    queries = datagen.queries(c, rows=nq)
+    gt = None
+    if args.sift:
+        # SIFT1M from its TEXMEX files (bench/bench_sift.py:44-60): L2, recall against the
+        # published ground truth
+        from proxima_amd import datasets
+
+        ds = datasets.load_sift(args.sift)
+        data = np.ascontiguousarray(ds.base[: args.n] if args.n else ds.base)
+        queries = np.ascontiguousarray(ds.queries[: args.nq] if args.nq else ds.queries)
+        if len(data) == len(ds.base):
+            gt = ds.ground_truth[: len(queries)]
+        cfg = dict(cfg, dist="sift1m", metric="L2", mask=None)
+        n, dim = data.shape
+        nq = len(queries)
+        k = args.k or 10
+        l2 = True
+        log(f"[bench] SIFT1M from {args.sift}: base {n} x {dim}, {nq} queries")
+    else:
+        n = args.n or cfg["n"]
+        nq = args.nq or cfg["nq"]
+        k = args.k or cfg["k"][0]
+        dim = cfg["dim"]
+        l2 = cfg["metric"] == "L2"
+        log(f"[bench] workload {c}: generating corpus {n} x {dim} ({cfg['dist']}) and {nq} queries")
+        data = datagen.corpus(c, rows=n)
+        queries = datagen.queries(c, rows=nq)
     mask = datagen.config_mask(c, n) if cfg["mask"] is not None else None
     n_eff = int(mask.sum()) if mask is not None else n
     idx = FlatIndex(dim, Metric.L2 if l2 else Metric.InnerProduct)
@@ -175,9 +198,9 @@ def bench_flat(args, dev):
 
     flops = 2.0 * nq * n_eff * dim
     achieved = flops / (np.mean(scan_ms) * 1e-3) / 1e12
-    headline = (c, n, nq, k) == (3, 1_000_000, 10_000, 10)
+    headline = (c, n, nq, k) == (3, 1_000_000, 10_000, 10) and not args.sift
     desc = (f"FlatIndex exact {'L2' if l2 else 'inner product'}, corpus {n} x {dim} fp32 "
-            f"{ {'gaussian': 'N(0,1)', 'unit': 'unit-normalised Gaussian', 'sift': 'SIFT-like integers in [0,255]'}[cfg['dist']] }, "
+            f"{ {'gaussian': 'N(0,1)', 'unit': 'unit-normalised Gaussian', 'sift': 'SIFT-like integers in [0,255]', 'sift1m': 'SIFT1M base vectors'}[cfg['dist']] }, "
             f"{nq}-query batch, k={k}" + (f", {cfg['mask']:.0%}-density filter" if mask is not None else ""))
     result = {
         "metric": HEADLINE_METRIC if headline else f"exact kNN QPS ({desc}); % fp32 MFMA peak",
@@ -195,6 +218,15 @@ def bench_flat(args, dev):
                      "algorithmic_flop_per_launch": flops},
         "pipeline_ms": float(np.mean(total_ms)),
     }
+    if args.sift:
+        from proxima_amd import datasets
+
+        result["data"] = f"SIFT1M TEXMEX files ({args.sift})"
+        if gt is not None:
+            kk = min(k, gt.shape[1])
+            result["recall_at_k"] = datasets.recall_at_k(ids, gt, kk)
+            log(f"[bench] recall@{kk} against the published ground truth: "
+                f"{result['recall_at_k']:.4f}")
     if args.cpu_seconds > 0:
         log("[bench] CPU oracle baseline + parity sample")
         import oracle
@@ -309,6 +341,11 @@ def main():
     ap.add_argument("--nq", type=int, default=None, help="override the query count")
     ap.add_argument("--copy-mib", type=int, default=1024, help="copy: MiB per launch")
     ap.add_argument("--mask", action="store_true", help="pq: 50%% filter bitmask")
+    ap.add_argument("--sift", default=None,
+                    help="flat: SIFT1M TEXMEX directory (sift_base.fvecs, sift_query.fvecs, "
+                         "sift_groundtruth.ivecs) instead of synthetic data")
+    ap.add_argument("--envelope", default=None,
+                    help="also write a schema_version 1 results envelope to this path")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="CPU oracle budget for the baseline (0 disables)")
     args = ap.parse_args()
@@ -329,11 +366,36 @@ def main():
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True, "scaling": "weak",
-           "vs_baseline": None, "dtype": res.pop("dtype"), "data": "synthetic (seeded SplitMix64)",
+           "vs_baseline": None, "dtype": res.pop("dtype"),
+           "data": res.pop("data", "synthetic (seeded SplitMix64)"),
            "config": res.pop("config")}
     out.update(res)
     out["device"] = _lib.device_info(0)
+    if args.envelope and args.workload != "copy":
+        write_bench_envelope(args.envelope, out)
     print(json.dumps(out), flush=True)
+
+
+def write_bench_envelope(path: str, out: dict) -> None:
+    """The run as a gpu_knn-style envelope: per-search seconds for the whole batch, the CPU
+    oracle's rate extrapolated to the batch, agreement = share of equal ids on its sample."""
+    from proxima_amd import envelope
+
+    cfg = out["config"]
+    nq, k = cfg["nq"], cfg["k"]
+    cb = out.get("cpu_baseline")
+    par = out.get("parity_sample")
+    agree = None
+    if par and par["queries_checked"]:
+        agree = 1.0 - par["id_mismatches"] / (par["queries_checked"] * k)
+    env = envelope.gpu_envelope(
+        n_base=cfg["n"], dim=cfg.get("dim", 128), n_queries=nq, k=k,
+        metric=cfg.get("metric", "L2"), gpu_seconds=out["ms_per_step"] / 1e3,
+        reps=out["steps"], cpu_mt_seconds=(nq / cb["value"]) if cb else None,
+        topk_agreement=agree)
+    env["results"]["bench_line"] = {key: out[key] for key in ("metric", "value", "unit")}
+    envelope.write_envelope(path, env)
+    log(f"[bench] envelope written to {path}")
 
 
 if __name__ == "__main__":

@@ -153,15 +153,20 @@ int px_device_count(void);
 /* name (NUL-terminated, truncated to name_len), compute units, HBM bytes, peak clock kHz */
 int px_device_info(int device, char* name, size_t name_len, int* cu_count, int64_t* hbm_bytes,
                    int* clock_khz, char* arch, size_t arch_len);
+/* HIP runtime and driver versions (hipRuntimeGetVersion / hipDriverGetVersion), for the
+ * provenance of benchmark envelopes; crates/core/examples/gpu_knn.rs:287-295 records the
+ * CUDA runtime and driver versions the same way. */
+int px_hip_versions(int* runtime_version, int* driver_version);
 
 /* Per-handle kernel timing with HIP events on the handle's stream. When enabled, each
  * search records the duration of its scan kernel and of the whole device pipeline. */
 int px_flat_set_timing(px_flat* idx, int enable);
 int px_flat_last_timing(const px_flat* idx, float* scan_ms, float* total_ms, int* splits,
                         int* blocks);
-/* Collect rounds of the handle's last search: 0 when k + 8 <= 128 (per-split candidate
- * lists), else the rounds of the large-k threshold-collect path (1 when every query
- * finished in the first). Diagnostic; no counterpart in the reference. */
+/* Collect rounds of the handle's last search: 0 when it used per-split candidate lists
+ * (k < 16, or batches under 256 queries, with k + 8 <= 128), else the rounds of the
+ * threshold-collect path (1 when every query finished in the first). Diagnostic; no
+ * counterpart in the reference. */
 int px_flat_last_rounds(const px_flat* idx, int* rounds);
 /* The same for PqIndex searches (k <= 128: per-wave lists; above: threshold-collect). */
 int px_pq_last_rounds(const px_pq* idx, int* rounds);

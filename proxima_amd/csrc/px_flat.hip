@@ -815,12 +815,18 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
 
     int p = 1;
     while (p < held) p <<= 1;
-    for (int sp = 0; sp < a.regions; ++sp) {
-        const int o = s_off[sp], c = s_off[sp + 1] - o;
-        for (int x = threadIdx.x; x < c; x += blockDim.x) {
-            sk[o + x] = rk[(int64_t)sp * a.cap + x];
-            si[o + x] = rp[(int64_t)sp * a.cap + x];
+    // candidate x comes from the region r with s_off[r] <= x < s_off[r + 1] (binary search),
+    // so that every thread's loads are independent of each other
+    for (int x = threadIdx.x; x < held; x += blockDim.x) {
+        int lo = 0, hi = a.regions - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_off[mid] <= x) lo = mid;
+            else hi = mid - 1;
         }
+        const int64_t at = (int64_t)lo * a.cap + (x - s_off[lo]);
+        sk[x] = rk[at];
+        si[x] = rp[at];
     }
     for (int x = held + threadIdx.x; x < p; x += blockDim.x) {
         sk[x] = kInf;

@@ -123,8 +123,20 @@ struct Workspace {
     // collect path (k' past the lists)
     DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
     int* h_count = nullptr;  // pinned
+    int* h_status = nullptr; // pinned, h_status_cap ints
+    int64_t h_status_cap = 0;
     int ensure_pinned() {
         if (!h_count) PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_count), sizeof(int)));
+        return PX_OK;
+    }
+    int ensure_status(int64_t n) {
+        if (n <= h_status_cap) return PX_OK;
+        if (h_status) (void)hipHostFree(h_status);
+        h_status = nullptr;
+        h_status_cap = 0;
+        PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_status),
+                             sizeof(int) * std::max<int64_t>(n, 1)));
+        h_status_cap = n;
         return PX_OK;
     }
     void release() {
@@ -134,6 +146,9 @@ struct Workspace {
             b->release();
         if (h_count) (void)hipHostFree(h_count);
         h_count = nullptr;
+        if (h_status) (void)hipHostFree(h_status);
+        h_status = nullptr;
+        h_status_cap = 0;
     }
 };
 
@@ -395,7 +410,9 @@ int run_collect(CollectJob& j) {
         PX_TRY(j.sample(S, stride, r0, r1));
     }
 
-    std::vector<int> h_status((size_t)nq), failing;
+    PX_TRY(ws.ensure_status(nq));
+    int* h_status = ws.h_status;
+    std::vector<int> failing;
     int64_t slots = nq;
     const int* qlist = nullptr;
     for (int round = 0;; ++round) {
@@ -425,17 +442,17 @@ int run_collect(CollectJob& j) {
         c.status = ws.status.as<int>();
         c.kk = (int)kk;
         PX_HIP(px::launch_collect_select(c, (int)slots, s));
-        PX_HIP(hipMemcpyAsync(h_status.data(), ws.status.p, sizeof(int) * nq,
-                              hipMemcpyDeviceToHost, s));
+        if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[2], s));
+        PX_HIP(hipMemcpyAsync(h_status, ws.status.p, sizeof(int) * nq, hipMemcpyDeviceToHost, s));
         PX_HIP(hipStreamSynchronize(s));
         // queries of this round still open
         std::vector<int> next;
         if (qlist) {
             for (int q : failing)
-                if (h_status[(size_t)q]) next.push_back(q);
+                if (h_status[q]) next.push_back(q);
         } else {
             for (int64_t q = 0; q < nq; ++q)
-                if (h_status[(size_t)q]) next.push_back((int)q);
+                if (h_status[q]) next.push_back((int)q);
         }
         if (next.empty()) break;
         if (round >= 10000)
@@ -449,7 +466,7 @@ int run_collect(CollectJob& j) {
         expect = (double)(2 * kk + 1);
     }
     if (j.timing->enabled) {
-        PX_HIP(hipEventRecord(j.timing->ev[2], s));
+        if (*j.last_rounds > 1) PX_HIP(hipEventRecord(j.timing->ev[2], s));
         PX_HIP(hipStreamSynchronize(s));
         PX_HIP(hipEventElapsedTime(&j.timing->scan_ms, j.timing->ev[0], j.timing->ev[1]));
         PX_HIP(hipEventElapsedTime(&j.timing->total_ms, j.timing->ev[0], j.timing->ev[2]));
@@ -1295,6 +1312,15 @@ int px_device_info(int device, char* name, size_t name_len, int* cu_count, int64
     if (cu_count) *cu_count = prop.multiProcessorCount;
     if (hbm_bytes) *hbm_bytes = (int64_t)prop.totalGlobalMem;
     if (clock_khz) *clock_khz = prop.clockRate;
+    return PX_OK;
+}
+
+int px_hip_versions(int* runtime_version, int* driver_version) {
+    int rt = 0, dv = 0;
+    PX_HIP(hipRuntimeGetVersion(&rt));
+    PX_HIP(hipDriverGetVersion(&dv));
+    if (runtime_version) *runtime_version = rt;
+    if (driver_version) *driver_version = dv;
     return PX_OK;
 }
 
