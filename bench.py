@@ -248,10 +248,12 @@ def bench_pq(args, dev):
     pq = PqIndex(dim, Metric.L2, m=m, nbits=8, train_iters=25, train_sample=50_000)
     t0 = time.perf_counter()
     pq.train(data)
-    log(f"[bench] train {time.perf_counter() - t0:.1f} s")
+    train_s = time.perf_counter() - t0
+    log(f"[bench] train {train_s:.2f} s")
     t0 = time.perf_counter()
     pq.add(data)
-    log(f"[bench] encode + upload {time.perf_counter() - t0:.1f} s")
+    add_s = time.perf_counter() - t0
+    log(f"[bench] encode + upload {add_s:.2f} s")
     lib = dev.lib
     dq = dev.put(queries)
     dm = dev.put(mask.view(np.uint8)) if mask is not None else None
@@ -284,6 +286,7 @@ def bench_pq(args, dev):
         "unit": "queries/s",
         "ms_per_step": elapsed / args.steps * 1e3,
         "dtype": "f32",
+        "build_seconds": {"train": train_s, "encode_and_upload": add_s},
         "config": {"workload": f"PqIndex ADC L2, {n} codes x m={m} x 8 bit, {nq}-query batch, "
                                f"k={k}, mask={'50%' if mask is not None else 'none'}",
                    "n": n, "m": m, "nq": nq, "k": k},

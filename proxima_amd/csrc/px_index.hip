@@ -757,6 +757,82 @@ int pq_sync(px_pq* p) {
     return PX_OK;
 }
 
+// Device buffer owned by one call.
+struct TmpBuf {
+    void* p = nullptr;
+    ~TmpBuf() {
+        if (p) (void)hipFree(p);
+    }
+    int alloc(size_t bytes) {
+        PX_HIP(hipMalloc(&p, std::max<size_t>(bytes, 16)));
+        return PX_OK;
+    }
+    template <class T>
+    T* as() const { return static_cast<T*>(p); }
+};
+
+// PQ training on the GPU (pq.rs:54-193): the host plans (sample, initial centroids,
+// generator states) and gathers the sample sub-major; the Lloyd iterations run on the
+// device. Bit-identical to pq_train_host. Caller holds p->mu.
+int pq_train_device(px_pq* p, const float* training, int64_t n_all, int64_t iters,
+                    int64_t train_sample, uint64_t seed, float* books) {
+    const int64_t m = p->m, d = p->dsub;
+    px::PqTrainPlan plan;
+    px::pq_train_plan(n_all, m, p->nbits, train_sample, seed, &plan);
+    const int64_t n = plan.n, ks = plan.ks;
+    std::vector<float> sub((size_t)(m * n * d));
+    px::pq_gather_sample(training, p->dim, m, plan, sub.data());
+    for (int64_t s = 0; s < m; ++s)
+        for (int64_t c = 0; c < ks; ++c)
+            std::memcpy(books + (s * ks + c) * d, sub.data() + (s * n + plan.init_rows[s * ks + c]) * d,
+                        sizeof(float) * d);
+    if (iters == 0) return PX_OK;
+    PX_TRY(pq_bind(p));
+    hipStream_t st = p->stream;
+    TmpBuf data, cents, asg, counts, rng;
+    PX_TRY(data.alloc(sizeof(float) * sub.size()));
+    PX_TRY(cents.alloc(sizeof(float) * m * ks * d));
+    PX_TRY(asg.alloc((size_t)(m * px::pq_train_asg_pitch(n))));
+    PX_TRY(counts.alloc(sizeof(int) * m * ks));
+    PX_TRY(rng.alloc(sizeof(uint64_t) * m));
+    PX_HIP(hipMemcpyAsync(data.p, sub.data(), sizeof(float) * sub.size(), hipMemcpyHostToDevice, st));
+    PX_HIP(hipMemcpyAsync(cents.p, books, sizeof(float) * m * ks * d, hipMemcpyHostToDevice, st));
+    PX_HIP(hipMemcpyAsync(rng.p, plan.rng_after_init.data(), sizeof(uint64_t) * m,
+                          hipMemcpyHostToDevice, st));
+    for (int64_t it = 0; it < iters; ++it)
+        PX_HIP(px::launch_pq_train_iteration(data.as<float>(), n, (int)d, (int)ks, (int)m,
+                                             cents.as<float>(), asg.as<uint8_t>(), counts.as<int>(),
+                                             rng.as<uint64_t>(), st));
+    PX_HIP(hipMemcpyAsync(books, cents.p, sizeof(float) * m * ks * d, hipMemcpyDeviceToHost, st));
+    PX_HIP(hipStreamSynchronize(st));
+    return PX_OK;
+}
+
+// PQ encoding on the GPU (pq.rs:107-121, 266-284), in chunks of 2^20 rows. Caller holds
+// p->mu.
+int pq_encode_device(px_pq* p, const float* vectors, int64_t n, uint8_t* codes) {
+    PX_TRY(pq_bind(p));
+    hipStream_t st = p->stream;
+    const int64_t chunk = std::min<int64_t>(n, (int64_t)1 << 20);
+    TmpBuf books, vec, out;
+    PX_TRY(books.alloc(sizeof(float) * p->codebooks.size()));
+    PX_TRY(vec.alloc(sizeof(float) * chunk * p->dim));
+    PX_TRY(out.alloc((size_t)(chunk * p->m)));
+    PX_HIP(hipMemcpyAsync(books.p, p->codebooks.data(), sizeof(float) * p->codebooks.size(),
+                          hipMemcpyHostToDevice, st));
+    for (int64_t r0 = 0; r0 < n; r0 += chunk) {
+        const int64_t rows = std::min(chunk, n - r0);
+        PX_HIP(hipMemcpyAsync(vec.p, vectors + r0 * p->dim, sizeof(float) * rows * p->dim,
+                              hipMemcpyHostToDevice, st));
+        PX_HIP(px::launch_pq_encode(vec.as<float>(), rows, (int)p->dim, (int)p->dsub, (int)p->ks,
+                                    (int)p->m, books.as<float>(), out.as<uint8_t>(), st));
+        PX_HIP(hipMemcpyAsync(codes + r0 * p->m, out.p, (size_t)(rows * p->m),
+                              hipMemcpyDeviceToHost, st));
+        PX_HIP(hipStreamSynchronize(st));
+    }
+    return PX_OK;
+}
+
 // k past the lists: the threshold-collect path with exact ADC keys (no re-rank, k' = k).
 int pq_run_collect(px_pq* p, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
                    const int* rowidx, int64_t* d_ids, float* d_out) {
@@ -1150,9 +1226,14 @@ int px_pq_train(px_pq* p, const float* training, int64_t n, int64_t train_iters,
     if (!all_finite(training, n * p->dim))
         return fail(PX_ERR_NONFINITE, "training data must not contain NaN or infinite values");
     std::vector<float> books((size_t)(p->m * p->ks * p->dsub));
-    px::pq_train_host(training, n, p->dim, p->m, p->nbits, train_iters, train_sample, seed,
-                      books.data());
     std::lock_guard<std::mutex> lock(p->mu);
+    // on the GPU when one is present, else on the host (as the reference does); both give
+    // the same codebooks bit for bit
+    if (px_device_count() > 0)
+        PX_TRY(pq_train_device(p, training, n, train_iters, train_sample, seed, books.data()));
+    else
+        px::pq_train_host(training, n, p->dim, p->m, p->nbits, train_iters, train_sample, seed,
+                          books.data());
     p->codebooks.swap(books);
     p->trained = true;
     p->books_on_device = false;
@@ -1189,7 +1270,12 @@ int px_pq_add(px_pq* p, const float* vectors, int64_t n) {
     if (!all_finite(vectors, n * p->dim))
         return fail(PX_ERR_NONFINITE, "vectors must not contain NaN or infinite values");
     std::vector<uint8_t> codes((size_t)(n * p->m));
-    px::pq_encode_host(p->codebooks.data(), p->dim, p->m, p->nbits, vectors, n, codes.data());
+    if (px_device_count() > 0) {
+        std::lock_guard<std::mutex> lock(p->mu);
+        PX_TRY(pq_encode_device(p, vectors, n, codes.data()));
+    } else {
+        px::pq_encode_host(p->codebooks.data(), p->dim, p->m, p->nbits, vectors, n, codes.data());
+    }
     return px_pq_add_codes(p, codes.data(), n);
 }
 

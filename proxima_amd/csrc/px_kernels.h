@@ -182,6 +182,17 @@ int pq_queries_per_block(int m, int ks);
 hipError_t launch_pq_scan(const PqScanArgs& a, hipStream_t s);
 hipError_t launch_pq_collect(const PqScanArgs& a, hipStream_t s);
 
+// PQ training and encoding (px_pq_kmeans.hip). One Lloyd iteration over all m subspaces:
+// data sub-major [m][n][d], centroids [m][ks][d] updated in place, asg [m][pitch(n)] bytes,
+// counts [m][ks], rng [m] SplitMix64 states.
+int64_t pq_train_asg_pitch(int64_t n);
+hipError_t launch_pq_train_iteration(const float* data, int64_t n, int d, int ks, int m,
+                                     float* cents, uint8_t* asg, int* counts, uint64_t* rng,
+                                     hipStream_t s);
+// codes[i][sub] = nearest of books[sub] to vectors[i][sub*d ..), vectors [n][dim].
+hipError_t launch_pq_encode(const float* vectors, int64_t n, int dim, int d, int ks, int m,
+                            const float* books, uint8_t* codes, hipStream_t s);
+
 // Plain streaming copy (calibrates HBM traffic counters against known bytes).
 hipError_t launch_copy(const float4* src, float4* dst, int64_t n4, hipStream_t s);
 

@@ -1,11 +1,13 @@
-// px_pq_train.cpp -- host-side product-quantizer training and encoding.
+// px_pq_train.cpp -- product-quantizer training plan, and host training and encoding.
 //
-// PqIndex::train/add run on the host, as in the reference (crates/core/src/pq.rs:54-193,
-// 266-284); only the ADC search runs on the GPU. Deterministic: SplitMix64 sampling,
-// Lloyd iterations with strict '<' argmin ties to the lower centroid, sequential sums
-// in row order and a reciprocal multiply. Built with -ffp-contract=off so a*b+c is never
-// fused (Rust never fuses), which makes the codebooks bit-identical to the reference's
-// for the same inputs.
+// The reference trains and encodes on the host (crates/core/src/pq.rs:54-193, 266-284).
+// With a gfx950 device the library runs the Lloyd iterations and the encoding on the GPU
+// (px_pq_kmeans.hip); without one, here. Both follow the same plan -- SplitMix64 sampling
+// and initial-centroid picks, made here on the host -- and the same arithmetic: strict '<'
+// argmin ties to the lower centroid, sequential sums in row order and a reciprocal
+// multiply, built with -ffp-contract=off so a*b+c is never fused (Rust never fuses). The
+// codebooks are therefore bit-identical to the reference's for the same inputs, on either
+// side.
 #include "px_host.h"
 
 #include <algorithm>
@@ -71,6 +73,47 @@ struct SplitMix {
     }
     uint64_t below(uint64_t n) { return next() % n; }  // pq.rs:34-36
 };
+}  // namespace
+
+// pq.rs:54-95 and 139-148: the training sample, and per subspace the rows of the initial
+// centroids (a partial Fisher-Yates shuffle) and the generator state after them.
+void pq_train_plan(int64_t n_all, int64_t m, int64_t nbits, int64_t train_sample, uint64_t seed,
+                   PqTrainPlan* plan) {
+    const int64_t ks = (int64_t)1 << nbits;
+    SplitMix rng{seed};
+    int64_t n = n_all;
+    if (train_sample > 0) n = std::clamp<int64_t>(train_sample, ks, n_all);
+    plan->n = n;
+    plan->ks = ks;
+    plan->sample.resize(n);
+    if (n == n_all) {
+        for (int64_t i = 0; i < n; ++i) plan->sample[i] = i;
+    } else {
+        for (int64_t i = 0; i < n; ++i) plan->sample[i] = (int64_t)rng.below((uint64_t)n_all);
+    }
+    plan->init_rows.resize(m * ks);
+    plan->rng_after_init.resize(m);
+    std::vector<int64_t> order(n);
+    for (int64_t sub = 0; sub < m; ++sub) {
+        SplitMix r{seed ^ ((uint64_t)sub * 0x9E3779B97F4A7C15ull)};  // pq.rs:95
+        for (int64_t i = 0; i < n; ++i) order[i] = i;
+        for (int64_t c = 0; c < ks; ++c) {
+            const int64_t j = c + (int64_t)r.below((uint64_t)(n - c));
+            std::swap(order[c], order[j]);
+            plan->init_rows[sub * ks + c] = order[c];
+        }
+        plan->rng_after_init[sub] = r.s;
+    }
+}
+
+uint64_t splitmix_below(uint64_t* state, uint64_t n) {
+    SplitMix r{*state};
+    const uint64_t v = r.below(n);
+    *state = r.s;
+    return v;
+}
+
+namespace {
 
 // argmin over ks centroids of dimension d with strict '<' from FLT_MAX (pq.rs:157-165)
 inline uint32_t nearest(const float* v, const float* cents, int64_t ks, int64_t d) {
@@ -86,17 +129,12 @@ inline uint32_t nearest(const float* v, const float* cents, int64_t ks, int64_t 
     return best;
 }
 
-// pq.rs:139-193
-void kmeans(const float* data, int64_t n, int64_t d, int64_t ks, int64_t iters, uint64_t seed,
-            float* cents) {
-    SplitMix rng{seed};
-    std::vector<int64_t> order(n);
-    for (int64_t i = 0; i < n; ++i) order[i] = i;
-    for (int64_t c = 0; c < ks; ++c) {
-        const int64_t j = c + (int64_t)rng.below((uint64_t)(n - c));
-        std::swap(order[c], order[j]);
-        std::memcpy(cents + c * d, data + order[c] * d, sizeof(float) * d);
-    }
+// pq.rs:149-193, from the plan's initial centroids and generator state
+void kmeans(const float* data, int64_t n, int64_t d, int64_t ks, int64_t iters,
+            const int64_t* init_rows, uint64_t rng_state, float* cents) {
+    SplitMix rng{rng_state};
+    for (int64_t c = 0; c < ks; ++c)
+        std::memcpy(cents + c * d, data + init_rows[c] * d, sizeof(float) * d);
     std::vector<uint32_t> assign(n);
     std::vector<float> sums(ks * d);
     std::vector<uint32_t> counts(ks);
@@ -126,28 +164,28 @@ void kmeans(const float* data, int64_t n, int64_t d, int64_t ks, int64_t iters, 
 }
 }  // namespace
 
+// Sub-major copy of the training sample: out[sub][i][x] = training[sample[i]][sub*dsub + x].
+void pq_gather_sample(const float* training, int64_t dim, int64_t m, const PqTrainPlan& plan,
+                      float* out) {
+    const int64_t dsub = dim / m;
+    for (int64_t sub = 0; sub < m; ++sub)
+        for (int64_t i = 0; i < plan.n; ++i)
+            std::memcpy(out + (sub * plan.n + i) * dsub, training + plan.sample[i] * dim + sub * dsub,
+                        sizeof(float) * dsub);
+}
+
 // pq.rs:54-105; arguments validated by the caller
 void pq_train_host(const float* training, int64_t n_all, int64_t dim, int64_t m, int64_t nbits,
                    int64_t iters, int64_t train_sample, uint64_t seed, float* codebooks) {
     const int64_t dsub = dim / m;
-    const int64_t ks = (int64_t)1 << nbits;
-    SplitMix rng{seed};
-    int64_t n = n_all;
-    if (train_sample > 0) n = std::clamp<int64_t>(train_sample, ks, n_all);
-    std::vector<int64_t> sample(n);
-    if (n == n_all) {
-        for (int64_t i = 0; i < n; ++i) sample[i] = i;
-    } else {
-        for (int64_t i = 0; i < n; ++i) sample[i] = (int64_t)rng.below((uint64_t)n_all);
-    }
-    std::vector<float> sub_data(n * dsub);
-    for (int64_t sub = 0; sub < m; ++sub) {
-        for (int64_t i = 0; i < n; ++i)
-            std::memcpy(sub_data.data() + i * dsub, training + sample[i] * dim + sub * dsub,
-                        sizeof(float) * dsub);
-        kmeans(sub_data.data(), n, dsub, ks, iters, seed ^ ((uint64_t)sub * 0x9E3779B97F4A7C15ull),
-               codebooks + sub * ks * dsub);
-    }
+    PqTrainPlan plan;
+    pq_train_plan(n_all, m, nbits, train_sample, seed, &plan);
+    const int64_t n = plan.n, ks = plan.ks;
+    std::vector<float> sub_data(m * n * dsub);
+    pq_gather_sample(training, dim, m, plan, sub_data.data());
+    for (int64_t sub = 0; sub < m; ++sub)
+        kmeans(sub_data.data() + sub * n * dsub, n, dsub, ks, iters, plan.init_rows.data() + sub * ks,
+               plan.rng_after_init[sub], codebooks + sub * ks * dsub);
 }
 
 // pq.rs:107-121 per row, rows in parallel (pq.rs:275-281)

@@ -1,0 +1,65 @@
+"""PQ training and encoding on the GPU, bit for bit against the oracle's restatement of
+the reference's host code (pq.rs:54-193 k-means and sampling, pq.rs:107-121 encoding).
+
+With a device present, PqIndex.train/add run their Lloyd iterations and their argmins on
+the GPU (px_pq_kmeans.hip); the sample, the initial centroids and the generator streams are
+decided on the host. Each case below drives a different part: the sampled path (with
+replacement, train_sample < rows), the unsampled one, empty clusters re-seeded from the
+generator in cluster order, sub-vectors whose length is not a multiple of 8 (the distance's
+remainder loop), and more rows than one encode chunk (2^20).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from proxima_amd import Metric, PqIndex, datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def _train(data, m, nbits, iters, sample, seed=24301):
+    pq = PqIndex(data.shape[1], Metric.L2, m=m, nbits=nbits, train_iters=iters,
+                 train_sample=sample, seed=seed)
+    pq.train(data)
+    return pq
+
+
+@pytest.mark.parametrize("m,nbits,dim,iters,sample", [
+    (16, 8, 128, 25, 20_000),   # the 1M x 128 workload's parameters on a 60k-row set
+    (8, 8, 64, 6, 0),           # no sampling: every row
+    (4, 6, 36, 5, 3000),        # dsub = 9: the remainder of the 8-lane distance
+    (12, 3, 48, 9, 0),
+])
+def test_train_and_encode_bit_exact(gpu, m, nbits, dim, iters, sample):
+    data = datagen.gaussian(60_000 if dim == 128 else 12_000, dim, 900 + m)
+    pq = _train(data, m, nbits, iters, sample)
+    print(f"pq train m={m} nbits={nbits} dim={dim} iters={iters} sample={sample}", flush=True)
+    books = oracle.pq_train(data, m, nbits, iters, sample, 24301)
+    assert np.array_equal(pq.codebooks(), books)
+    pq.add(data[:5000])
+    assert np.array_equal(pq.codes(), oracle.pq_encode(books, data[:5000]))
+
+
+def test_empty_clusters_reseeded(gpu):
+    # 24 distinct rows repeated: most of the 64 clusters of every subspace end up empty and
+    # are re-seeded from the generator each iteration
+    base = datagen.gaussian(24, 16, 910)
+    data = np.tile(base, (40, 1))
+    pq = _train(data, 4, 6, 7, 0, seed=77)
+    assert np.array_equal(pq.codebooks(), oracle.pq_train(data, 4, 6, 7, 0, 77))
+
+
+def test_zero_iterations_and_seed(gpu):
+    data = datagen.gaussian(2000, 32, 911)
+    for seed in (0, 1, 2**63 + 5):
+        pq = _train(data, 4, 8, 0, 500, seed=seed)
+        assert np.array_equal(pq.codebooks(), oracle.pq_train(data, 4, 8, 0, 500, seed))
+
+
+def test_encode_more_than_one_chunk(gpu):
+    data = datagen.gaussian(3000, 8, 912)
+    pq = _train(data, 2, 4, 4, 0)
+    vecs = datagen.gaussian((1 << 20) + 777, 8, 913)
+    pq.add(vecs)
+    assert len(pq) == vecs.shape[0]
+    assert np.array_equal(pq.codes(), oracle.pq_encode(pq.codebooks(), vecs))
