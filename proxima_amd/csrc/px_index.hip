@@ -362,6 +362,19 @@ int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int cus, ListPlan* out, in
 //     the others get a new threshold (next rung, or a tighter one from the candidates) and
 //     go round again, alone. Each round either finishes a query or strictly shrinks its
 //     candidate set, so the loop ends; nearly every query finishes in the first round.
+// Device bytes a collect round's candidate regions may take (retry rounds are split into
+// chunks of queries to stay under it; PX_COLLECT_BYTES overrides it, read once), and the
+// most queries one collect pass serves (the sample keys take 64 KB and the first round's
+// regions up to ~170 KB per query).
+int64_t collect_bytes() {
+    static const int64_t v = [] {
+        const char* e = std::getenv("PX_COLLECT_BYTES");
+        return e && *e ? std::max<int64_t>(1, std::atoll(e)) : (int64_t)4 << 30;
+    }();
+    return v;
+}
+constexpr int64_t kCollectBatch = 16384;
+
 struct CollectJob {
     Workspace* ws = nullptr;
     hipStream_t stream = nullptr;
@@ -371,10 +384,11 @@ struct CollectJob {
     int cus = 1;
     // keys of S rows sampled at the given stride -> ladder rungs r0, r1, thresholds, rung 0
     std::function<int(int64_t S, int64_t stride, int r0, int r1)> sample;
-    // collect scan over `slots` query slots (qlist: their query indices, or null for all);
-    // returns the candidate regions per slot and their capacity
-    std::function<int(int64_t slots, const int* qlist, double expect, int round,
-                      int64_t* regions, int64_t* cap)>
+    // collect scan over the first *slots query slots (qlist: their query indices, or null
+    // for all); with a qlist it may take fewer slots so that the regions stay within
+    // max_bytes, and returns how many it took, the regions per slot and their capacity
+    std::function<int(int64_t* slots, const int* qlist, double expect, int round,
+                      int64_t max_bytes, int64_t* regions, int64_t* cap)>
         scan;
     px::CollectSelectArgs sel{};  // metric, corpus (null: no re-rank), dims, k, outputs
 };
@@ -417,32 +431,39 @@ int run_collect(CollectJob& j) {
     const int* qlist = nullptr;
     for (int round = 0;; ++round) {
         *j.last_rounds = round + 1;
-        int64_t regions = 0, cap = 0;
-        PX_TRY(j.scan(slots, qlist, expect, round, &regions, &cap));
-        if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[1], s));
-        int64_t lcap = 1;
-        while (lcap < std::max<int64_t>(std::min<int64_t>(regions * cap, px::kMaxCollect),
-                                        2 * kk + 1))
-            lcap <<= 1;
-        lcap = std::min<int64_t>(lcap, px::kMaxCollect);
+        // the round's slots, in chunks whose candidate regions fit collect_bytes() (only
+        // retry rounds, which list their queries, are ever split)
+        for (int64_t done = 0; done < slots;) {
+            int64_t take = slots - done, regions = 0, cap = 0;
+            const int* ql = qlist ? qlist + done : nullptr;
+            PX_TRY(j.scan(&take, ql, expect, round, qlist ? collect_bytes() : INT64_MAX, &regions,
+                          &cap));
+            if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[1], s));
+            int64_t lcap = 1;
+            while (lcap < std::max<int64_t>(std::min<int64_t>(regions * cap, px::kMaxCollect),
+                                            2 * kk + 1))
+                lcap <<= 1;
+            lcap = std::min<int64_t>(lcap, px::kMaxCollect);
 
-        px::CollectSelectArgs c = j.sel;
-        c.cand_keys = ws.cand_k.as<float>();
-        c.cand_pos = ws.cand_p.as<int>();
-        c.cand_count = ws.cand_n.as<int>();
-        c.regions = (int)regions;
-        c.cap = (int)cap;
-        c.lcap = (int)lcap;
-        c.qlist = qlist;
-        c.thr_key = ws.thr_k.as<int>();
-        c.thr_pos = ws.thr_p.as<int>();
-        c.ladder_key = ws.lad_k.as<int>();
-        c.ladder_pos = ws.lad_p.as<int>();
-        c.rung = ws.rung.as<int>();
-        c.status = ws.status.as<int>();
-        c.kk = (int)kk;
-        PX_HIP(px::launch_collect_select(c, (int)slots, s));
-        if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[2], s));
+            px::CollectSelectArgs c = j.sel;
+            c.cand_keys = ws.cand_k.as<float>();
+            c.cand_pos = ws.cand_p.as<int>();
+            c.cand_count = ws.cand_n.as<int>();
+            c.regions = (int)regions;
+            c.cap = (int)cap;
+            c.lcap = (int)lcap;
+            c.qlist = ql;
+            c.thr_key = ws.thr_k.as<int>();
+            c.thr_pos = ws.thr_p.as<int>();
+            c.ladder_key = ws.lad_k.as<int>();
+            c.ladder_pos = ws.lad_p.as<int>();
+            c.rung = ws.rung.as<int>();
+            c.status = ws.status.as<int>();
+            c.kk = (int)kk;
+            PX_HIP(px::launch_collect_select(c, (int)take, s));
+            if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[2], s));
+            done += take;
+        }
         PX_HIP(hipMemcpyAsync(h_status, ws.status.p, sizeof(int) * nq, hipMemcpyDeviceToHost, s));
         PX_HIP(hipStreamSynchronize(s));
         // queries of this round still open
@@ -483,8 +504,8 @@ int64_t collect_cap(double expect, int64_t regions, int round, int64_t kk, int64
     return std::max<int64_t>(1, std::min<int64_t>((cap + 31) / 32 * 32, most));
 }
 
-int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
-                     const int* rowidx, int64_t* d_ids, float* d_out, int raw_keys) {
+int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
+                           const int* rowidx, int64_t* d_ids, float* d_out, int raw_keys) {
     Workspace& ws = f->ws;
     hipStream_t s = f->stream;
     const int cus = std::max(f->dev.cus, 1);
@@ -538,18 +559,25 @@ int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_
         PX_HIP(px::launch_ladder(la, s));
         return PX_OK;
     };
-    j.scan = [&](int64_t slots, const int* qlist, double expect, int round, int64_t* regions,
-                 int64_t* cap) -> int {
-        const int64_t groups = (slots + 255) / 256;
-        int64_t splits = std::min<int64_t>(choose_flat_splits(n_eff, groups, 1, cus, false),
-                                           px::kMaxCollectRegions / 2);
-        int64_t rps = (n_eff + splits - 1) / splits;
-        rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
-        splits = std::max<int64_t>(1, (n_eff + rps - 1) / rps);
-        // two regions per split (one per lane of the pair holding a query), each of which
-        // receives at most half the split's rows
-        *regions = 2 * splits;
-        *cap = collect_cap(expect, *regions, round, j.kk, rps / 2);
+    j.scan = [&](int64_t* take, const int* qlist, double expect, int round, int64_t max_bytes,
+                 int64_t* regions, int64_t* cap) -> int {
+        int64_t slots = *take, splits = 1, rps = 64;
+        for (;;) {
+            const int64_t groups = (slots + 255) / 256;
+            splits = std::min<int64_t>(choose_flat_splits(n_eff, groups, 1, cus, false),
+                                       px::kMaxCollectRegions / 2);
+            rps = (n_eff + splits - 1) / splits;
+            rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
+            splits = std::max<int64_t>(1, (n_eff + rps - 1) / rps);
+            // two regions per split (one per lane of the pair holding a query), each of
+            // which receives at most half the split's rows
+            *regions = 2 * splits;
+            *cap = collect_cap(expect, *regions, round, j.kk, rps / 2);
+            const int64_t per = *regions * *cap * 8;
+            if (!qlist || slots == 1 || slots * per <= max_bytes) break;
+            slots = std::max<int64_t>(1, std::min(slots - 1, max_bytes / per));
+        }
+        *take = slots;
         PX_TRY(ws.cand_k.reserve(sizeof(float) * slots * *regions * *cap));
         PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * *regions * *cap));
         PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * *regions));
@@ -574,7 +602,7 @@ int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_
         PX_HIP(px::launch_flat_collect(a, s));
         if (round == 0) {
             f->timing.splits = (int)splits;
-            f->timing.blocks = (int)(groups * splits);
+            f->timing.blocks = (int)(((slots + 255) / 256) * splits);
         }
         return PX_OK;
     };
@@ -589,6 +617,20 @@ int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_
     j.sel.out_dists = d_out;
     j.sel.raw_keys = raw_keys;
     return run_collect(j);
+}
+
+// Batches of at most kCollectBatch queries, one after another.
+int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
+                     const int* rowidx, int64_t* d_ids, float* d_out, int raw_keys) {
+    int rounds = 0;
+    for (int64_t b0 = 0; b0 < nq; b0 += kCollectBatch) {
+        const int64_t b = std::min(kCollectBatch, nq - b0);
+        PX_TRY(flat_run_collect_batch(f, d_q + b0 * f->dp, b, k, n_eff, rowidx, d_ids + b0 * k,
+                                      d_out + b0 * k, raw_keys));
+        rounds = std::max(rounds, f->last_rounds);
+    }
+    f->last_rounds = rounds;
+    return PX_OK;
 }
 
 // Runs the device pipeline. d_q: [nq][dp] on device. Outputs on device.
@@ -834,8 +876,8 @@ int pq_encode_device(px_pq* p, const float* vectors, int64_t n, uint8_t* codes) 
 }
 
 // k past the lists: the threshold-collect path with exact ADC keys (no re-rank, k' = k).
-int pq_run_collect(px_pq* p, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
-                   const int* rowidx, int64_t* d_ids, float* d_out) {
+int pq_run_collect_batch(px_pq* p, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
+                         const int* rowidx, int64_t* d_ids, float* d_out) {
     Workspace& ws = p->ws;
     hipStream_t s = p->stream;
     const int cus = std::max(p->dev.cus, 1);
@@ -900,13 +942,19 @@ int pq_run_collect(px_pq* p, const float* d_q, int64_t nq, int64_t k, int64_t n_
         PX_HIP(px::launch_ladder(la, s));
         return PX_OK;
     };
-    j.scan = [&](int64_t slots, const int* qlist, double expect, int round, int64_t* regions,
-                 int64_t* cap) -> int {
-        int64_t splits, rps;
-        plan(n_eff, slots, &splits, &rps);
-        // one region per wave of a split; a wave takes 64 of every 256 rows
-        *regions = splits * waves;
-        *cap = collect_cap(expect, *regions, round, j.kk, rps / waves);
+    j.scan = [&](int64_t* take, const int* qlist, double expect, int round, int64_t max_bytes,
+                 int64_t* regions, int64_t* cap) -> int {
+        int64_t slots = *take, splits = 1, rps = 256;
+        for (;;) {
+            plan(n_eff, slots, &splits, &rps);
+            // one region per wave of a split; a wave takes 64 of every 256 rows
+            *regions = splits * waves;
+            *cap = collect_cap(expect, *regions, round, j.kk, rps / waves);
+            const int64_t per = *regions * *cap * 8;
+            if (!qlist || slots == 1 || slots * per <= max_bytes) break;
+            slots = std::max<int64_t>(1, std::min(slots - 1, max_bytes / per));
+        }
+        *take = slots;
         PX_TRY(ws.cand_k.reserve(sizeof(float) * slots * *regions * *cap));
         PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * *regions * *cap));
         PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * *regions));
@@ -938,6 +986,19 @@ int pq_run_collect(px_pq* p, const float* d_q, int64_t nq, int64_t k, int64_t n_
     j.sel.out_dists = d_out;
     j.sel.raw_keys = 0;
     return run_collect(j);
+}
+
+int pq_run_collect(px_pq* p, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
+                   const int* rowidx, int64_t* d_ids, float* d_out) {
+    int rounds = 0;
+    for (int64_t b0 = 0; b0 < nq; b0 += kCollectBatch) {
+        const int64_t b = std::min(kCollectBatch, nq - b0);
+        PX_TRY(pq_run_collect_batch(p, d_q + b0 * p->dim, b, k, n_eff, rowidx, d_ids + b0 * k,
+                                    d_out + b0 * k));
+        rounds = std::max(rounds, p->last_rounds);
+    }
+    p->last_rounds = rounds;
+    return PX_OK;
 }
 
 int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,

@@ -202,3 +202,48 @@ def test_k_limit(gpu):
     ids, d = idx.search(np.zeros(8, dtype=np.float32), k=_lib.PX_MAX_K)
     assert ids.shape == (_lib.PX_MAX_K,)
     assert np.array_equal(ids[:10], np.arange(10)) and (ids[10:] == -1).all()
+
+
+def test_more_queries_than_one_collect_batch(gpu):
+    # 17,000 queries: two collect batches of at most 16,384
+    data = datagen.sift_like(2000, 16, 58)
+    q = datagen.sift_like(17_000, 16, 59)
+    rounds = _check(data, q, 20, oracle.L2, exact=True)
+    assert rounds >= 1
+
+
+def test_retry_rounds_in_memory_bounded_chunks(gpu, tmp_path):
+    # The overflow layout of test_sample_far_overflow_round with 300 queries and a 1 MB
+    # budget for the candidate regions: each retry round runs in several chunks of queries.
+    import os
+    import subprocess
+    import sys
+    script = tmp_path / "run.py"
+    script.write_text(f"""
+import sys
+sys.path.insert(0, {repr(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))})
+sys.path.insert(0, {repr(os.path.dirname(os.path.abspath(__file__)))})
+import numpy as np
+import oracle
+from proxima_amd import FlatIndex, Metric, datagen
+n, k = 40_000, 992
+s = max(1, min(n, 16384, 80 * n // (k + 8)))
+rng = np.random.default_rng(45)
+data = rng.integers(0, 4, size=(n, 48)).astype(np.float32)
+data[::n // s] = 255.0
+q = rng.integers(0, 3, size=(300, 48)).astype(np.float32)
+idx = FlatIndex(48, Metric.L2)
+idx.add(data)
+ids, d = idx.search_batch(q, k=k)
+o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2)
+assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
+import ctypes
+r = ctypes.c_int(-1)
+assert idx._lib.px_flat_last_rounds(idx._h, ctypes.byref(r)) == 0 and r.value >= 2, r.value
+print("ok", r.value)
+""")
+    env = dict(os.environ, PX_COLLECT_BYTES=str(1 << 20))
+    out = subprocess.run([sys.executable, str(script)], capture_output=True, text=True,
+                         timeout=240, env=env)
+    assert out.returncode == 0, out.stdout[-2000:] + out.stderr[-2000:]
+    assert out.stdout.strip().startswith("ok")
