@@ -426,12 +426,26 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                         }
                     }
                 } else {
-                // tested during the next tile's MFMAs (or after the last tile)
+                // tested during the next tile's MFMAs (or after the last tile); with MULTI
+                // (several chunks per tile, and the next query chunk held in registers) the
+                // keys are tested here instead, so that they are not held across the MFMAs
 #pragma unroll
                 for (int x = 0; x < 32; ++x) pkey[x] = key[x];
                 pt0 = (int)t0;
                 prem = rem;
                 pend = __ballot(kmin <= cthr) != 0;
+                if constexpr (MULTI) {
+                    if (pend) {
+#pragma unroll
+                        for (int g = 0; g < 16; ++g) {
+                            if (__ballot(pkey[2 * g] <= cthr || pkey[2 * g + 1] <= cthr)) {
+                                collect_x(2 * g);
+                                collect_x(2 * g + 1);
+                            }
+                        }
+                    }
+                    pend = false;
+                }
                 }
             } else {
             // Padding queries get a threshold nothing passes; rows past the split's end
