@@ -395,8 +395,9 @@ def test_train_sample_with_replacement_uses_splitmix_draws():
 
 
 def test_product_training_equals_oracle():
-    # libproxima_px.so trains on the host (px_pq_train); it is a separate implementation and
-    # must agree with the oracle bit for bit, including the sampled path.
+    # libproxima_px.so trains with its own code (on the host here, where no device is
+    # visible; its GPU kernels are checked the same way in test_gpu_pq_train.py); it must
+    # agree with the oracle bit for bit, including the sampled path.
     from proxima_amd import Metric, PqIndex
 
     data = datagen.gaussian(3000, 32, 16)
