@@ -76,12 +76,21 @@ def test_config3_reduced_sift_integers_bit_exact(gpu, k):
     assert np.array_equal(d, o_d)
 
 
-@pytest.mark.parametrize("dim", [1, 4, 7, 12, 24, 100, 130, 200, 384])
+@pytest.mark.parametrize("dim", [1, 4, 7, 12, 24, 100, 130, 200, 384, 1000, 2051])
 def test_odd_dims(gpu, dim):
     data = datagen.gaussian(3000, dim, 11 + dim)
     q = datagen.gaussian(40, dim, 12 + dim)
     for metric in (oracle.L2, oracle.IP):
         _check(data, q, 10, metric)
+
+
+@pytest.mark.parametrize("dim", [3, 1000, 2051])
+def test_odd_dims_collect_path(gpu, dim):
+    # 260 queries and k = 20: the threshold-collect path, with 1 and with 8 / 17 query chunks
+    data = datagen.gaussian(4000, dim, 21 + dim)
+    q = datagen.gaussian(260, dim, 22 + dim)
+    for metric in (oracle.L2, oracle.IP):
+        _check(data, q, 20, metric)
 
 
 @pytest.mark.parametrize("p", [0.0, 0.001, 0.2, 0.5, 1.0])
