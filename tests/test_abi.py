@@ -4,6 +4,7 @@ No compute call is made."""
 import ctypes
 import os
 import re
+import subprocess
 
 import numpy as np
 import pytest
@@ -120,3 +121,19 @@ def test_no_device_search_fails_loudly():
     finally:
         lib.px_flat_destroy(h)
     assert lib.knn_gpu_create(_lib.f32p(np.ones((2, 4), np.float32)), 2, 4) is None
+
+
+def _abi_check_binary():
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c_abi", "abi_check")
+    if not os.path.exists(path):
+        pytest.fail(f"{path} is missing: build it with __graft_entry__.build() "
+                    "(make -C tests/c_abi)")
+    return path
+
+
+@pytest.mark.skipif(_lib.device_count() > 0, reason="checks the no-device path")
+def test_c_program_no_device():
+    # the same binary runs the gfx950 known answers on a GPU box (test_gpu_c_abi.py)
+    out = subprocess.run([_abi_check_binary()], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0, out.stderr
+    assert out.stdout.startswith("abi_check ok (no-device path")
