@@ -346,6 +346,21 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     }
     __syncthreads();
 
+    if constexpr (!COLLECT) {
+        // A wave whose 32 queries are all padding (small batches) only helps stage the
+        // corpus: same loads, same barriers, no MFMAs, no selection. A separate loop, so
+        // that the live waves' code is the one the full batches run.
+        if (qt * (WAVES * 32) + wave * 32 >= a.nq) {
+            for (int64_t s = 0; s < nstages; ++s) {
+                fetch(s + 1);
+                tile_ids((s + 2) / nch);
+                commit(s + 1);
+                __syncthreads();
+            }
+            return;
+        }
+    }
+
     f32x16 acc0 = {0.f}, acc1 = {0.f};
     for (int64_t s = 0; s < nstages; ++s) {
         const int c = MULTI ? (int)(s % nch) : 0;
@@ -676,7 +691,7 @@ __device__ void bitonic_sort(float* sk, int* si, int p) {
 // One workgroup per query: sort all split candidates, keep the best kl, re-rank them
 // exactly (flat), sort again and emit the best k with the reference's finishing and
 // padding (flat.rs:229-237; gpu.rs:80-93 for raw keys).
-__global__ __launch_bounds__(256) void flat_merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
     extern __shared__ __attribute__((aligned(16))) char msmem[];
     int p = 1;
     while (p < a.width) p <<= 1;
@@ -749,7 +764,9 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {
         if (e != hipSuccess) return e;
         big_lds = true;
     }
-    hipLaunchKernelGGL(flat_merge_kernel, dim3((unsigned)a.nq), dim3(256), lds, s, a);
+    // long sorts (many splits: small batches spread over the whole GPU) get 1,024 threads
+    const int threads = p >= 4096 ? 1024 : 256;
+    hipLaunchKernelGGL(flat_merge_kernel, dim3((unsigned)a.nq), dim3(threads), lds, s, a);
     return hipGetLastError();
 }
 
