@@ -244,7 +244,13 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     // collect mode: this query's threshold (nothing passes -inf) and region
     float cthr = -kInf;
     int cpos = -1, ccount = 0;
-    float pkey[COLLECT ? 32 : 1];  // keys of the previous tile, tested during this one
+    // list mode with one query chunk: the insertions of a tile's second row block run during
+    // the next tile's MFMAs (an insertion otherwise holds up the stage barrier for all eight
+    // waves); the first block's run in the epilogue, as do all of them with MULTI
+    constexpr bool LDEFER = !COLLECT && !MULTI;
+    float pkey[COLLECT ? 32 : (LDEFER ? 16 : 1)];  // keys of the previous tile tested during this one
+    float pthr = -kInf;            // list mode: the previous tile's threshold ...
+    bool peq = false;              // ... and whether keys equal to it may still enter
     int pt0 = 0, prem = 0;         // its first position and row count
     bool pend = false;             // some lane of the wave has a key at or below its threshold
     auto collect_x = [&](int x) {
@@ -260,6 +266,52 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     a.cand_pos[at] = pt0 + off;
                 }
                 ++ccount;
+            }
+        }
+    };
+    // list mode: the candidates of row x (16..31) of the previous tile, one insertion at a
+    // time in lane order, each checked against the current tail of its query's list
+    auto list_x = [&](int x) {
+        if constexpr (LDEFER) {
+            const int r = x & 15;
+            const int off = 32 + mfma_row(r, h);
+            unsigned long long m =
+                __ballot(off < prem && (pkey[r] < pthr || (pkey[r] == pthr && peq)));
+            while (m) {
+                const int src = __builtin_ctzll(m);
+                m &= m - 1;
+                const float ck = readlane_f(pkey[r], src);
+                const int cid = pt0 + 32 + mfma_row(r, src >> 5);
+                const float tk = readlane_f(tau_k, src);
+                const int ti = readlane_i(tau_i, src);
+                if (!cand_less(ck, cid, tk, ti)) continue;
+                const int ql = src & 31;
+                float nk;
+                int ni;
+                list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], (int)row0, a.kl, ck,
+                                cid, nk, ni);
+                if (j == ql) {
+                    tau_k = nk;
+                    tau_i = ni;
+                }
+            }
+        }
+    };
+    // list mode: publish a tightened list tail as the query's shared bound, and the key in
+    // list slot pub_m - 1 to the query's gbest slot of this split. atomicMin, not a plain
+    // store: a plain store would stay in this XCD's L2, out of sight of the splits running
+    // on the other XCDs.
+    auto publish = [&]() {
+        if constexpr (!COLLECT) {
+            const int tk = total_key(tau_k);
+            if (h == 0 && qvalid && tau_i != kIdNone && tk < published) {
+                atomicMin(gtau, tk);
+                published = tk;
+            }
+            const int bk = total_key(lkeys[wave][j][pub_m - 1]);
+            if (h == 0 && qvalid && bk < published_best) {
+                atomicMin(gbest + (split & 31), bk);
+                published_best = bk;
             }
         }
     };
@@ -395,8 +447,17 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     collect_x(2 * g + 1);
                 }
             }
+            if constexpr (LDEFER) {
+                if (pend) list_x(16 + g);
+            }
         }
         if constexpr (COLLECT) pend = false;
+        if constexpr (LDEFER) {
+            if (pend) {
+                publish();
+                pend = false;
+            }
+        }
 
         if (c == nch - 1 && wave_live) {
             // Epilogue, branch-free: keys of the 32 rows this lane holds for query j.
@@ -493,58 +554,56 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                 // and the pair writes the query's best kl as its list.
                 first_tile_lists(key, t0, row1, qvalid, a.kl, &lkeys[wave][j][0],
                                  &lids[wave][j][0], (int)row0, tau_k, tau_i);
-                const int tk = total_key(tau_k);
-                if (h == 0 && qvalid && tau_i != kIdNone && tk < published) {
-                    atomicMin(gtau, tk);
-                    published = tk;
-                }
-                // atomicMin, not a plain store: a plain store would stay in this XCD's L2,
-                // out of sight of the splits running on the other XCDs
-                const int bk = total_key(lkeys[wave][j][pub_m - 1]);
-                if (h == 0 && qvalid && bk < published_best) {
-                    atomicMin(gbest + (split & 31), bk);
-                    published_best = bk;
-                }
-            } else if (__ballot(kmin <= thr)) {
+                publish();
+            } else {
                 const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
                 const bool eq_ok = thr < tau_k || tau_i >= t0;
+                // rows of the first block now (all of them without LDEFER)
+                constexpr int XN = LDEFER ? 16 : 32;
+                float kmin0 = kInf;
 #pragma unroll
-                for (int x = 0; x < 32; ++x) {
-                    const int rb = x >> 4, r = x & 15;
-                    const int off = rb * 32 + mfma_row(r, h);
-                    unsigned long long m = __ballot(
-                        off < rem && (key[x] < thr || (key[x] == thr && eq_ok)));
-                    while (m) {
-                        const int src = __builtin_ctzll(m);
-                        m &= m - 1;
-                        const float ck = readlane_f(key[x], src);
-                        const int cid = (int)(t0 + rb * 32 + mfma_row(r, src >> 5));
-                        const float tk = readlane_f(tau_k, src);
-                        const int ti = readlane_i(tau_i, src);
-                        if (!cand_less(ck, cid, tk, ti)) continue;
-                        const int ql = src & 31;
-                        float nk;
-                        int ni;
-                        list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], (int)row0,
-                                        a.kl, ck, cid, nk, ni);
-                        if (j == ql) {
-                            tau_k = nk;
-                            tau_i = ni;
+                for (int x = 0; x < XN; ++x) kmin0 = fminf(kmin0, key[x]);
+                if (__ballot(kmin0 <= thr)) {
+#pragma unroll
+                    for (int x = 0; x < XN; ++x) {
+                        const int rb = x >> 4, r = x & 15;
+                        const int off = rb * 32 + mfma_row(r, h);
+                        unsigned long long m = __ballot(
+                            off < rem && (key[x] < thr || (key[x] == thr && eq_ok)));
+                        while (m) {
+                            const int src = __builtin_ctzll(m);
+                            m &= m - 1;
+                            const float ck = readlane_f(key[x], src);
+                            const int cid = (int)(t0 + rb * 32 + mfma_row(r, src >> 5));
+                            const float tk = readlane_f(tau_k, src);
+                            const int ti = readlane_i(tau_i, src);
+                            if (!cand_less(ck, cid, tk, ti)) continue;
+                            const int ql = src & 31;
+                            float nk;
+                            int ni;
+                            list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], (int)row0,
+                                            a.kl, ck, cid, nk, ni);
+                            if (j == ql) {
+                                tau_k = nk;
+                                tau_i = ni;
+                            }
                         }
                     }
+                    publish();
                 }
-                // publish a tightened list tail as the query's shared bound
-                const int tk = total_key(tau_k);
-                if (h == 0 && qvalid && tau_i != kIdNone && tk < published) {
-                    atomicMin(gtau, tk);
-                    published = tk;
-                }
-                // atomicMin, not a plain store: a plain store would stay in this XCD's L2,
-                // out of sight of the splits running on the other XCDs
-                const int bk = total_key(lkeys[wave][j][pub_m - 1]);
-                if (h == 0 && qvalid && bk < published_best) {
-                    atomicMin(gbest + (split & 31), bk);
-                    published_best = bk;
+                if constexpr (LDEFER) {
+                    // the second block: during the next tile's MFMAs (or after the last)
+                    float kmin1 = kInf;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        pkey[r] = key[16 + r];
+                        kmin1 = fminf(kmin1, key[16 + r]);
+                    }
+                    pt0 = (int)t0;
+                    prem = rem;
+                    pthr = thr;
+                    peq = eq_ok;
+                    pend = __ballot(kmin1 <= thr) != 0;
                 }
             }
             }  // !COLLECT
@@ -566,6 +625,12 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         }
         if (qvalid && !a.dense) a.cand_count[((int64_t)slot * a.splits + split) * 2 + h] = ccount;
         return;
+    }
+    if constexpr (LDEFER) {
+        if (pend) {
+#pragma unroll
+            for (int x = 16; x < 32; ++x) list_x(x);
+        }
     }
     // Write this split's lists: part[q][split][0..kl)
     const int qbase = qt * (WAVES * 32) + wave * 32;
