@@ -308,9 +308,8 @@ int flat_sync(px_flat* f) {
 
 // Smallest k served by the threshold-collect path for batches of at least
 // kCollectMinQueries queries. Below it the per-split lists are faster (1M x 128, 10,000
-// queries: 24.0 ms a batch at k = 10 against 25.4); at k = 16 the two tie (25.3 / 25.5 ms)
-// and from there the collect path pulls ahead (28.1 / 25.5 ms at k = 24, 46.5 / 25.9 at
-// k = 64). Smaller batches keep the lists, which need no sample pass and no host round
+// queries: 23.6 ms a batch at k = 10 against 24.4); from k = 16 the collect path is ahead
+// (24.8 / 23.7 ms at k = 16, 27.9 / 24.5 at k = 24, 46.5 / 25.9 at k = 64). Smaller batches keep the lists, which need no sample pass and no host round
 // trip. The PX_FLAT_COLLECT_FROM_K environment variable overrides the k (read once).
 constexpr int64_t kCollectMinQueries = 256;
 int64_t collect_from_k() {
