@@ -993,7 +993,6 @@ __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
     __shared__ unsigned s_prefix[kRungs], s_rank[kRungs];
     const int q = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const int total = a.ld ? a.count : a.blocks * 64;
     const float* base = a.ld ? a.keys + (int64_t)q * a.ld
                              : a.keys + (int64_t)(q >> 5) * a.blocks * (64 * 32) + (q & 31) * 32;
     unsigned u[kPer];
@@ -1001,9 +1000,13 @@ __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
     for (int i = 0; i < kPer; ++i) {
         const int e = t + i * 1024;
         const int b = e >> 6, hh = (e >> 5) & 1, x = e & 31;
-        const float kv = e >= total ? __int_as_float(0x7f800000)
-                         : a.ld    ? base[e]
-                                   : base[(int64_t)b * (64 * 32) + hh * (32 * 32) + x];
+        // dense layout: block b holds sampled rows 64 b .. 64 b + 63 (splits are whole
+        // tiles); blocks past the sample's end were never written
+        const bool in = a.ld ? e < a.count
+                             : b * 64 + (x >> 4) * 32 + mfma_row(x & 15, hh) < a.count;
+        const float kv = !in   ? __int_as_float(0x7f800000)
+                         : a.ld ? base[e]
+                                : base[(int64_t)b * (64 * 32) + hh * (32 * 32) + x];
         // +inf (rows past a split's end) is left out
         u[i] = kv < __int_as_float(0x7f800000) ? (unsigned)total_key(kv) ^ 0x80000000u : kNone;
     }

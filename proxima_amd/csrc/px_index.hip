@@ -180,13 +180,20 @@ int choose_splits(int64_t n_eff, int64_t groups, int lists_per_split, int kl, in
     return (int)std::max<int64_t>(s, 1);
 }
 
-// Corpus splits for the flat scan. Its workgroups fill a CU each (134-160 KB of LDS), so
-// the grid is sized in whole rounds of `cus` workgroups. Splits are multiples of 8 where
-// possible (each XCD then sees a fixed subset of splits across query tiles), keep at least
-// 256 rows, fit the merge (splits * kl <= kMaxMerge) and, for lists with 16-bit positions,
-// at most kMaxNarrowSplitRows rows. Every split starts its own lists, and list insertions
-// grow with splits x kl, so small lists take the smallest split count giving four rounds
-// with at most 5% idle in the last, large lists the smallest giving one round at 90%.
+// Corpus splits for the flat scan. Splits keep at least 256 rows, fit the merge
+// (splits * kl <= kMaxMerge) and, for lists with 16-bit positions, at most
+// kMaxNarrowSplitRows rows; a split count s gives rps = ceil(n_eff / s) rounded up to a
+// whole tile and ceil(n_eff / rps) splits, as the callers compute them.
+//  - Small lists (kl <= 32) and the collect scans: a workgroup holds a whole CU (its LDS
+//    and registers allow one per CU), so a grid of B workgroups runs in ceil(B / cus)
+//    rounds, each about as long as one split: rps rows plus about one tile of fixed cost
+//    (query loads, the first tile's sort, the write-back). The count minimising
+//    rounds * (rps + 64) is taken; among counts within 1% of that minimum, the one giving
+//    the most rounds up to four (later rounds even out workgroups that finish at
+//    different times), then a multiple of 8 (each XCD then sees a fixed subset of splits
+//    across query tiles), then the fewest splits (less to merge).
+//  - Large lists: every split builds its own list, and insertions grow with splits x kl,
+//    so the smallest count giving one round at 90% occupancy.
 int choose_flat_splits(int64_t n_eff, int64_t groups, int kl, int cus, bool narrow_ids) {
     cus = std::max(cus, 1);
     const int64_t min_s =
@@ -195,23 +202,54 @@ int choose_flat_splits(int64_t n_eff, int64_t groups, int kl, int cus, bool narr
                    : 1;
     const int64_t max_s = std::max<int64_t>(
         min_s, std::min<int64_t>(n_eff / 256, px::kMaxMerge / std::max(kl, 1)));
-    const bool large = kl > 32;
-    const int64_t want_rounds = large ? 1 : 4;
-    const double want_eff = large ? 0.90 : 0.95;
-    int64_t best = min_s;
-    double best_eff = -1.0;
-    for (int64_t s = 1; s <= std::min<int64_t>(max_s, 512); s = s < 8 ? s * 2 : s + 8) {
-        if (s < min_s) continue;
-        const int64_t blocks = groups * s;
-        const int64_t rounds = (blocks + cus - 1) / cus;
-        const double eff = (double)blocks / (double)(rounds * cus);
-        if (rounds >= want_rounds && eff >= want_eff) return (int)s;
-        if (eff > best_eff + 1e-9 || (rounds < want_rounds && eff >= best_eff - 1e-9)) {
+    const int64_t top = std::max<int64_t>(min_s, std::min<int64_t>(max_s, 512));
+    auto shape = [&](int64_t s, int64_t* rps, int64_t* splits) {
+        int64_t r = (n_eff + s - 1) / s;
+        r = std::max<int64_t>((r + 63) / 64 * 64, 64);
+        if (narrow_ids) r = std::min<int64_t>(r, px::kMaxNarrowSplitRows);
+        *rps = r;
+        *splits = std::max<int64_t>(1, (n_eff + r - 1) / r);
+    };
+    if (kl > 32) {
+        int64_t best = min_s;
+        double best_eff = -1.0;
+        for (int64_t s = 1; s <= top; s = s < 8 ? s * 2 : s + 8) {
+            if (s < min_s) continue;
+            const int64_t blocks = groups * s;
+            const double eff = (double)blocks / (double)(((blocks + cus - 1) / cus) * cus);
+            if (eff >= 0.90) return (int)s;
+            if (eff > best_eff + 1e-9) {
+                best = s;
+                best_eff = eff;
+            }
+        }
+        return (int)std::max<int64_t>(best, min_s);
+    }
+    double min_cost = 0.0;
+    for (int64_t s = min_s; s <= top; ++s) {
+        int64_t rps, splits;
+        shape(s, &rps, &splits);
+        const double cost = (double)((groups * splits + cus - 1) / cus) * (double)(rps + 64);
+        if (s == min_s || cost < min_cost) min_cost = cost;
+    }
+    int64_t best = min_s, best_rounds = -1, best_splits = 0;
+    bool best_m8 = false;
+    for (int64_t s = min_s; s <= top; ++s) {
+        int64_t rps, splits;
+        shape(s, &rps, &splits);
+        const int64_t rounds = (groups * splits + cus - 1) / cus;
+        if ((double)rounds * (double)(rps + 64) > 1.01 * min_cost) continue;
+        const int64_t r4 = std::min<int64_t>(rounds, 4);
+        const bool m8 = splits % 8 == 0;
+        if (r4 > best_rounds || (r4 == best_rounds && m8 && !best_m8) ||
+            (r4 == best_rounds && m8 == best_m8 && splits < best_splits)) {
             best = s;
-            best_eff = eff;
+            best_rounds = r4;
+            best_m8 = m8;
+            best_splits = splits;
         }
     }
-    return (int)std::max<int64_t>(best, min_s);
+    return (int)best;
 }
 
 }  // namespace
@@ -547,6 +585,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         px::LadderArgs la{};
         la.keys = a.cand_keys;
         la.blocks = (int)blocks;
+        la.count = (int)S;
         la.nq = (int)nq;
         la.ranks[0] = r0;
         la.ranks[1] = r1;

@@ -101,8 +101,8 @@ struct LadderArgs {
     const float* keys;       // FlatScanArgs::dense layout of the sample scan (8 waves), or
                              // row-major [nq][ld] when ld > 0
     int blocks;              // dense layout: splits * tiles per split (64-key blocks a query)
-    int64_t ld;              // row-major layout: row pitch; count keys a query
-    int count;
+    int64_t ld;              // row-major layout: row pitch
+    int count;               // sampled rows (keys a query)
     int nq;
     int ranks[kRungs];
     int* ladder_key;         // [nq][kRungs]

@@ -168,6 +168,25 @@ def test_sample_near_underflow_rounds(gpu):
     assert rounds >= 3
 
 
+def test_sample_short_of_its_last_split(gpu):
+    # 10,000 rows at k = 100 sample 7,407 rows, which leave the sample scan's last split
+    # four 64-row tiles short of its layout. Those key blocks are never written and must
+    # not count as sampled keys: zeros or an earlier search's candidate keys there make
+    # every threshold too tight and cost extra rounds. Two searches in a row on one
+    # handle, each exact and finished in one round.
+    data = datagen.gaussian(10_000, 128, 61)
+    q = datagen.gaussian(300, 128, 62)
+    k = 100
+    print(f"case n=10000 dim=128 nq=300 k={k} L2, twice", flush=True)
+    idx = FlatIndex(128, Metric.L2)
+    idx.add(data)
+    o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2)
+    for _ in range(2):
+        ids, d = idx.search_batch(q, k=k)
+        assert_parity(ids, d, o_ids, o_d, _key_of(data, q, oracle.L2))
+        assert _rounds(idx) == 1
+
+
 def test_sift_1m_subset(gpu):
     # the 1M x 128 SIFT-like corpus, 16 of its queries, k = 1000
     data = datagen.corpus(3)
