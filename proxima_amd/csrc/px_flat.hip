@@ -166,8 +166,9 @@ __device__ __forceinline__ int kth_smallest32(int (&v)[16], int rank) {
 // Pipeline: the corpus streams through LDS in stages of 64 rows x 128 dims (one tile is
 // ceil(dp / 128) stages; MULTI when that is more than one). While the waves run the MFMAs
 // of stage s out of one LDS buffer, every thread holds the global loads of stage s + 1 in
-// registers (and, with MULTI, each wave the next query chunk) and writes them to the other
-// buffer afterwards: one barrier per stage. Every load is issued in a fixed order on a
+// registers and writes them to the other buffer afterwards: one barrier per stage. With
+// MULTI each wave's query-chunk registers take the next stage's chunk group by group, as
+// the MFMAs release them. Every load is issued in a fixed order on a
 // static path, so waiting for one never waits for the prefetch behind it (vector loads
 // retire in order). FILT scans the compacted row ids of a filter; the ids of the next
 // tile are loaded one stage ahead of the rows themselves.
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             tnorm[(s / nch) & 1][tid] = (pvalid >> kPF) & 1u ? pn : 0.f;
     };
 
-    float4 b[16], bn[MULTI ? 16 : 1];
+    float4 b[16];
     load_b(0, b);
 #pragma unroll
     for (int g = 0; g < 16; ++g) b[g] = zero_unless(b_valid(0, g), b[g]);
@@ -421,7 +422,12 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         if constexpr (!COLLECT)
             gt_raw = __hip_atomic_load(gtau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         const int64_t ti = s / nch;
-        if constexpr (MULTI) load_b((c + 1) % nch, bn);
+        // MULTI: each b[g] takes the next stage's query chunk as soon as this stage's MFMAs
+        // have read it. Those loads are not zeroed past the chunk's end or for padding
+        // queries: the corpus tile is zero in columns past the chunk's end, every value is
+        // finite, and padding queries' keys are never used.
+        const int cn = MULTI ? (c + 1) % nch : 0;
+        const int dcn = min(kChunk, a.dp - cn * kChunk);
         fetch(s + 1);  // past the last stage every row is -1: harmless clamped loads
         tile_ids((s + 2) / nch);  // ids for the tile of stage s + 2
         if (c == 0) {
@@ -439,6 +445,9 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                 acc0 = mfma4(a0, b[g], acc0);
                 acc1 = mfma4(a1, b[g], acc1);
             }
+            if constexpr (MULTI)
+                b[g] = *reinterpret_cast<const float4*>(qrow + cn * kChunk +
+                                                        min(g * 8 + h * 4, dcn - 4));
             if constexpr (COLLECT) {
                 // one compare per row and one uniform branch per pair of rows; the exact
                 // test and the append only where some lane has a row at or below
@@ -610,11 +619,6 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         }
 
         commit(s + 1);
-        if constexpr (MULTI) {
-            const int cn = (c + 1) % nch;
-#pragma unroll
-            for (int g = 0; g < 16; ++g) b[g] = zero_unless(b_valid(cn, g), bn[g]);
-        }
         __syncthreads();
     }
 
