@@ -685,6 +685,142 @@ hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s) {
     }
 }
 
+// Sum over the 8 lanes of each aligned group of 8 (every lane of the group gets it):
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], then row_half_mirror pairs the two quads.
+__device__ __forceinline__ float sum8_lanes(float v) {
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
+    v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x141, 0xF, 0xF, true));
+    return v;
+}
+
+// Collect scan for at most NQ query slots on the vector ALUs. Workgroup = one split of
+// rows_per_split positions, 8 waves. Eight lanes share a row: lane c8 = lane % 8 reads the
+// row's 16-byte columns c8, c8 + 8, ... (each load instruction of a wave reads 8 rows x
+// 128 contiguous bytes), and the 8 partial dot products are summed across the lanes. Each
+// wave takes 16 rows a step (two per lane group, for more loads in flight); the queries
+// sit in LDS and every lane of a row group reads the same address (a broadcast). A row at
+// or below a slot's threshold (key, then position) is appended to the slot's region of
+// this split through an LDS counter; with dense set, every key goes to cand_keys
+// [slot][n_eff] instead (the threshold sample of a few-query batch).
+template <int NQ, bool L2, bool FILT>
+__global__ __launch_bounds__(512) void flat_vcollect_kernel(FlatScanArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float sq[];  // [NQ][dp]
+    __shared__ float s_thr[NQ];
+    __shared__ int s_tpos[NQ], s_cnt[NQ];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c8 = lane & 7, rsub = lane >> 3;
+    const int split = blockIdx.x;
+    const int64_t row0 = (int64_t)split * a.rows_per_split;
+    const int64_t row1 = min(a.n_eff, row0 + a.rows_per_split);
+    const int dp = a.dp;
+    for (int x = tid; x < NQ * dp; x += blockDim.x) {
+        const int sl = x / dp;
+        float v = 0.f;
+        if (sl < a.nq) {
+            const int q = a.qlist ? a.qlist[sl] : sl;
+            v = a.queries[(int64_t)q * dp + (x - sl * dp)];
+        }
+        sq[x] = v;
+    }
+    if (tid < NQ) {
+        float thr = -__int_as_float(0x7f800000);  // padding slots: nothing passes
+        int tpos = -1;
+        if (tid < a.nq && !a.dense) {  // dense mode has no thresholds
+            const int q = a.qlist ? a.qlist[tid] : tid;
+            thr = from_total_key(a.thr_key[q]);
+            tpos = a.thr_pos[q];
+        }
+        s_thr[tid] = thr;
+        s_tpos[tid] = tpos;
+        s_cnt[tid] = 0;
+    }
+    __syncthreads();
+
+    for (int64_t r = row0 + wave * 16; r < row1; r += 16 * 8) {
+        const int64_t pa = r + rsub, pb = r + 8 + rsub;
+        const bool va = pa < row1, vb = pb < row1;
+        const int ia = FILT ? a.rowidx[va ? pa : row0] : (int)(va ? pa : row0);
+        const int ib = FILT ? a.rowidx[vb ? pb : row0] : (int)(vb ? pb : row0);
+        const float* xa = a.corpus + (int64_t)ia * dp;
+        const float* xb = a.corpus + (int64_t)ib * dp;
+        float da[NQ], db[NQ];
+#pragma unroll
+        for (int qq = 0; qq < NQ; ++qq) {
+            da[qq] = 0.f;
+            db[qq] = 0.f;
+        }
+#pragma unroll 4
+        for (int c = c8 * 4; c < dp; c += 32) {
+            const float4 ua = *reinterpret_cast<const float4*>(xa + c);
+            const float4 ub = *reinterpret_cast<const float4*>(xb + c);
+#pragma unroll
+            for (int qq = 0; qq < NQ; ++qq) {
+                const float4 qv = *reinterpret_cast<const float4*>(sq + qq * dp + c);
+                da[qq] = __builtin_fmaf(ua.x, qv.x, da[qq]);
+                da[qq] = __builtin_fmaf(ua.y, qv.y, da[qq]);
+                da[qq] = __builtin_fmaf(ua.z, qv.z, da[qq]);
+                da[qq] = __builtin_fmaf(ua.w, qv.w, da[qq]);
+                db[qq] = __builtin_fmaf(ub.x, qv.x, db[qq]);
+                db[qq] = __builtin_fmaf(ub.y, qv.y, db[qq]);
+                db[qq] = __builtin_fmaf(ub.z, qv.z, db[qq]);
+                db[qq] = __builtin_fmaf(ub.w, qv.w, db[qq]);
+            }
+        }
+        const float na = L2 ? a.norms[ia] : 0.f, nb = L2 ? a.norms[ib] : 0.f;
+#pragma unroll
+        for (int qq = 0; qq < NQ; ++qq) {
+            if (qq >= a.nq) break;
+            const float sa = sum8_lanes(da[qq]), sb = sum8_lanes(db[qq]);
+            // L2 drops ||q||^2, as the MFMA scan does: key = ||x||^2 - 2 q.x; IP: -q.x
+            const float ka = L2 ? __builtin_fmaf(-2.0f, sa, na) : -sa;
+            const float kb = L2 ? __builtin_fmaf(-2.0f, sb, nb) : -sb;
+            if (a.dense) {
+                // every key, row-major [slot][n_eff]
+                if (c8 == 0 && va) a.cand_keys[(int64_t)qq * a.n_eff + pa] = ka;
+                if (c8 == 1 && vb) a.cand_keys[(int64_t)qq * a.n_eff + pb] = kb;
+                continue;
+            }
+            const float thr = s_thr[qq];
+            const int tpos = s_tpos[qq];
+            const bool ta = c8 == 0 && va && (ka < thr || (ka == thr && pa <= tpos));
+            const bool tb = c8 == 1 && vb && (kb < thr || (kb == thr && pb <= tpos));
+            if (ta || tb) {
+                const int at = atomicAdd(&s_cnt[qq], 1);
+                if (at < a.cap) {
+                    const int64_t o = ((int64_t)qq * a.splits + split) * a.cap + at;
+                    a.cand_keys[o] = ta ? ka : kb;
+                    a.cand_pos[o] = (int)(ta ? pa : pb);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    if (!a.dense && tid < a.nq) a.cand_count[(int64_t)tid * a.splits + split] = s_cnt[tid];
+}
+
+template <int NQ>
+static void launch_vcollect_n(const FlatScanArgs& a, hipStream_t s) {
+    const dim3 grid((unsigned)a.splits), block(512);
+    const size_t lds = sizeof(float) * NQ * a.dp;
+    if (a.metric == 0) {
+        if (a.rowidx) hipLaunchKernelGGL((flat_vcollect_kernel<NQ, true, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((flat_vcollect_kernel<NQ, true, false>), grid, block, lds, s, a);
+    } else {
+        if (a.rowidx) hipLaunchKernelGGL((flat_vcollect_kernel<NQ, false, true>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((flat_vcollect_kernel<NQ, false, false>), grid, block, lds, s, a);
+    }
+}
+
+hipError_t launch_flat_vcollect(const FlatScanArgs& a, hipStream_t s) {
+    if (a.nq < 1 || a.nq > kVecQueries || a.dp > kVecMaxDp) return hipErrorInvalidValue;
+    if (a.nq == 1) launch_vcollect_n<1>(a, s);
+    else if (a.nq == 2) launch_vcollect_n<2>(a, s);
+    else if (a.nq <= 4) launch_vcollect_n<4>(a, s);
+    else launch_vcollect_n<8>(a, s);
+    return hipGetLastError();
+}
+
 hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s) {
     constexpr int kWaves = 8;
     const int64_t qtiles = (a.nq + 32 * kWaves - 1) / (32 * kWaves);

@@ -535,6 +535,11 @@ int run_collect(CollectJob& j) {
 // Region capacity of a collect round: 3x the expected candidates spread over the regions,
 // at least 2 k' + 1 after the first round (so an overflowing region holds enough to
 // tighten from), whole multiples of 32, never more than a region can receive.
+// Whether a collect scan of `slots` query slots runs on the vector ALUs.
+bool vec_collect(int64_t slots, int64_t dp) {
+    return slots >= 1 && slots <= px::kVecQueries && dp <= px::kVecMaxDp;
+}
+
 int64_t collect_cap(double expect, int64_t regions, int round, int64_t kk, int64_t most) {
     int64_t cap = (int64_t)std::ceil(3.0 * expect / (double)regions);
     if (round > 0) cap = std::max<int64_t>(cap, 2 * kk + 1);
@@ -558,6 +563,41 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     j.sample = [&](int64_t S, int64_t stride, int r0, int r1) -> int {
         PX_TRY(ws.samp_row.reserve(sizeof(int) * S));
         PX_HIP(px::launch_sample_rows(rowidx, S, stride, ws.samp_row.as<int>(), s));
+        if (vec_collect(nq, f->dp)) {
+            // a few queries: the sampled rows' keys from the vector-ALU scan, row-major
+            const int64_t want = std::min<int64_t>(px::kMaxCollectRegions, 4 * (int64_t)cus);
+            int64_t rps = (S + want - 1) / want;
+            rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
+            PX_TRY(ws.cand_k.reserve(sizeof(float) * nq * S));
+            px::FlatScanArgs a{};
+            a.corpus = f->d_x;
+            a.norms = f->d_norm;
+            a.queries = d_q;
+            a.rowidx = ws.samp_row.as<int>();
+            a.n_eff = S;
+            a.rows_per_split = rps;
+            a.dp = (int)f->dp;
+            a.nq = (int)nq;
+            a.splits = (int)((S + rps - 1) / rps);
+            a.metric = f->metric;
+            a.cand_keys = ws.cand_k.as<float>();
+            a.dense = 1;
+            PX_HIP(px::launch_flat_vcollect(a, s));
+            px::LadderArgs la{};
+            la.keys = a.cand_keys;
+            la.ld = S;
+            la.count = (int)S;
+            la.nq = (int)nq;
+            la.ranks[0] = r0;
+            la.ranks[1] = r1;
+            la.ladder_key = ws.lad_k.as<int>();
+            la.ladder_pos = ws.lad_p.as<int>();
+            la.thr_key = ws.thr_k.as<int>();
+            la.thr_pos = ws.thr_p.as<int>();
+            la.rung = ws.rung.as<int>();
+            PX_HIP(px::launch_ladder(la, s));
+            return PX_OK;
+        }
         // dense keys of the sample: [query tile][wave][split][tile][lane][32]
         const int64_t groups = (nq + 255) / 256;
         int64_t splits = choose_flat_splits(S, groups, 1, cus, false);
@@ -600,6 +640,43 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     j.scan = [&](int64_t* take, const int* qlist, double expect, int round, int64_t max_bytes,
                  int64_t* regions, int64_t* cap) -> int {
         int64_t slots = *take, splits = 1, rps = 64;
+        if (vec_collect(slots, f->dp)) {
+            // a few slots: the vector-ALU scan, one region per (slot, split), up to four
+            // workgroups of 512 threads per CU
+            const int64_t want = std::min<int64_t>(px::kMaxCollectRegions, 4 * (int64_t)cus);
+            rps = (n_eff + want - 1) / want;
+            rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
+            splits = std::max<int64_t>(1, (n_eff + rps - 1) / rps);
+            *regions = splits;
+            *cap = collect_cap(expect, *regions, round, j.kk, rps);
+            PX_TRY(ws.cand_k.reserve(sizeof(float) * slots * *regions * *cap));
+            PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * *regions * *cap));
+            PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * *regions));
+            px::FlatScanArgs a{};
+            a.corpus = f->d_x;
+            a.norms = f->d_norm;
+            a.queries = d_q;
+            a.rowidx = rowidx;
+            a.n_eff = n_eff;
+            a.rows_per_split = rps;
+            a.dp = (int)f->dp;
+            a.nq = (int)slots;
+            a.splits = (int)splits;
+            a.metric = f->metric;
+            a.qlist = qlist;
+            a.thr_key = ws.thr_k.as<int>();
+            a.thr_pos = ws.thr_p.as<int>();
+            a.cand_keys = ws.cand_k.as<float>();
+            a.cand_pos = ws.cand_p.as<int>();
+            a.cand_count = ws.cand_n.as<int>();
+            a.cap = (int)*cap;
+            PX_HIP(px::launch_flat_vcollect(a, s));
+            if (round == 0) {
+                f->timing.splits = (int)splits;
+                f->timing.blocks = (int)splits;
+            }
+            return PX_OK;
+        }
         for (;;) {
             const int64_t groups = (slots + 255) / 256;
             splits = std::min<int64_t>(choose_flat_splits(n_eff, groups, 1, cus, false),
@@ -680,8 +757,11 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     const int* rowidx = nullptr;
     if (d_mask) PX_TRY(compact_mask(ws, d_mask, f->d_rows, s, &n_eff, &rowidx));
     f->last_rounds = 0;
+    // lists for batches of moderate size and small k; the collect path for large k, for
+    // larger k on large batches, and for the few-query batches the vector-ALU scan serves
     const bool collect = k + kReRankMargin > px::kMaxList ||
-                         (k >= collect_from_k() && nq >= kCollectMinQueries);
+                         (k >= collect_from_k() && nq >= kCollectMinQueries) ||
+                         vec_collect(nq, f->dp);
     if (collect && n_eff > 0)
         return flat_run_collect(f, d_q, nq, k, n_eff, rowidx, d_ids, d_out, raw_keys);
 

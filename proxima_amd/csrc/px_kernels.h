@@ -60,6 +60,14 @@ constexpr int kTotalKeyInf = 0x7f800000;
 // strided sample, one collect scan, per-query select; queries whose threshold proved too
 // tight or too loose go round again.
 hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s);
+// The collect scan for a few query slots (nq <= kVecQueries, dp <= kVecMaxDp) on the
+// vector ALUs: the MFMA scan's 32-query tiles would be nearly all padding, so this one
+// streams the corpus at memory speed instead. One region per (slot, split):
+// cand_keys [nq slots][splits][cap], cand_count [nq slots][splits]; dense: every key to
+// cand_keys [nq slots][n_eff] (no thresholds, no counts).
+constexpr int kVecQueries = 8;
+constexpr int kVecMaxDp = 1024;
+hipError_t launch_flat_vcollect(const FlatScanArgs& a, hipStream_t s);
 // Threshold ladder rungs taken from the sample, loosest last; past the last rung a query's
 // threshold is +inf (every row passes).
 constexpr int kRungs = 2;
