@@ -19,6 +19,7 @@
 namespace px {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kTileRows = 64;            // corpus rows per tile: two 32-row MFMA blocks
 constexpr int kChunk = 128;              // dims per staged K-chunk (16 groups of 8)
@@ -698,7 +699,7 @@ __device__ __forceinline__ float sum8_lanes(float v) {
 // rows_per_split positions, 8 waves. Eight lanes share a row: lane c8 = lane % 8 reads the
 // row's 16-byte columns c8, c8 + 8, ... (each load instruction of a wave reads 8 rows x
 // 128 contiguous bytes), and the 8 partial dot products are summed across the lanes. Each
-// wave takes 16 rows a step (two per lane group, for more loads in flight); the queries
+// wave takes 8 R rows a step (R per lane group, for more loads in flight); the queries
 // sit in LDS and every lane of a row group reads the same address (a broadcast). A row at
 // or below a slot's threshold (key, then position) is appended to the slot's region of
 // this split through an LDS counter; with dense set, every key goes to cand_keys
@@ -737,60 +738,77 @@ __global__ __launch_bounds__(512) void flat_vcollect_kernel(FlatScanArgs a) {
     }
     __syncthreads();
 
-    for (int64_t r = row0 + wave * 16; r < row1; r += 16 * 8) {
-        const int64_t pa = r + rsub, pb = r + 8 + rsub;
-        const bool va = pa < row1, vb = pb < row1;
-        const int ia = FILT ? a.rowidx[va ? pa : row0] : (int)(va ? pa : row0);
-        const int ib = FILT ? a.rowidx[vb ? pb : row0] : (int)(vb ? pb : row0);
-        const float* xa = a.corpus + (int64_t)ia * dp;
-        const float* xb = a.corpus + (int64_t)ib * dp;
-        float da[NQ], db[NQ];
+    // R rows per lane group a step: four with one or two slots, two with more (registers)
+    constexpr int R = NQ <= 2 ? 4 : 2;
+    for (int64_t r = row0 + wave * (8 * R); r < row1; r += 8 * R * 8) {
+        int64_t pr[R];
+        bool vr[R];
+        int ir[R];
+        const float* xr[R];
+        float d[R][NQ];
 #pragma unroll
-        for (int qq = 0; qq < NQ; ++qq) {
-            da[qq] = 0.f;
-            db[qq] = 0.f;
+        for (int u = 0; u < R; ++u) {
+            pr[u] = r + 8 * u + rsub;
+            vr[u] = pr[u] < row1;
+            const int64_t pp = vr[u] ? pr[u] : row0;
+            ir[u] = FILT ? a.rowidx[pp] : (int)pp;
+            xr[u] = a.corpus + (int64_t)ir[u] * dp;
+#pragma unroll
+            for (int qq = 0; qq < NQ; ++qq) d[u][qq] = 0.f;
         }
 #pragma unroll 4
         for (int c = c8 * 4; c < dp; c += 32) {
-            const float4 ua = *reinterpret_cast<const float4*>(xa + c);
-            const float4 ub = *reinterpret_cast<const float4*>(xb + c);
+            // the corpus is read once: nontemporal loads keep it from evicting the rest
+            f32x4v v[R];
+#pragma unroll
+            for (int u = 0; u < R; ++u)
+                v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(xr[u] + c));
 #pragma unroll
             for (int qq = 0; qq < NQ; ++qq) {
                 const float4 qv = *reinterpret_cast<const float4*>(sq + qq * dp + c);
-                da[qq] = __builtin_fmaf(ua.x, qv.x, da[qq]);
-                da[qq] = __builtin_fmaf(ua.y, qv.y, da[qq]);
-                da[qq] = __builtin_fmaf(ua.z, qv.z, da[qq]);
-                da[qq] = __builtin_fmaf(ua.w, qv.w, da[qq]);
-                db[qq] = __builtin_fmaf(ub.x, qv.x, db[qq]);
-                db[qq] = __builtin_fmaf(ub.y, qv.y, db[qq]);
-                db[qq] = __builtin_fmaf(ub.z, qv.z, db[qq]);
-                db[qq] = __builtin_fmaf(ub.w, qv.w, db[qq]);
+#pragma unroll
+                for (int u = 0; u < R; ++u) {
+                    d[u][qq] = __builtin_fmaf(v[u].x, qv.x, d[u][qq]);
+                    d[u][qq] = __builtin_fmaf(v[u].y, qv.y, d[u][qq]);
+                    d[u][qq] = __builtin_fmaf(v[u].z, qv.z, d[u][qq]);
+                    d[u][qq] = __builtin_fmaf(v[u].w, qv.w, d[u][qq]);
+                }
             }
         }
-        const float na = L2 ? a.norms[ia] : 0.f, nb = L2 ? a.norms[ib] : 0.f;
+        float nr[R];
+#pragma unroll
+        for (int u = 0; u < R; ++u) nr[u] = L2 ? a.norms[ir[u]] : 0.f;
 #pragma unroll
         for (int qq = 0; qq < NQ; ++qq) {
             if (qq >= a.nq) break;
-            const float sa = sum8_lanes(da[qq]), sb = sum8_lanes(db[qq]);
-            // L2 drops ||q||^2, as the MFMA scan does: key = ||x||^2 - 2 q.x; IP: -q.x
-            const float ka = L2 ? __builtin_fmaf(-2.0f, sa, na) : -sa;
-            const float kb = L2 ? __builtin_fmaf(-2.0f, sb, nb) : -sb;
+            // lane c8 == u of each row group tests row u (every lane holds the sums)
+            float kmine = 0.f;
+            int64_t pmine = 0;
+            bool vmine = false;
+#pragma unroll
+            for (int u = 0; u < R; ++u) {
+                const float su = sum8_lanes(d[u][qq]);
+                // L2 drops ||q||^2, as the MFMA scan does: key = ||x||^2 - 2 q.x; IP: -q.x
+                const float ku = L2 ? __builtin_fmaf(-2.0f, su, nr[u]) : -su;
+                if (c8 == u) {
+                    kmine = ku;
+                    pmine = pr[u];
+                    vmine = vr[u];
+                }
+            }
             if (a.dense) {
                 // every key, row-major [slot][n_eff]
-                if (c8 == 0 && va) a.cand_keys[(int64_t)qq * a.n_eff + pa] = ka;
-                if (c8 == 1 && vb) a.cand_keys[(int64_t)qq * a.n_eff + pb] = kb;
+                if (c8 < R && vmine) a.cand_keys[(int64_t)qq * a.n_eff + pmine] = kmine;
                 continue;
             }
             const float thr = s_thr[qq];
             const int tpos = s_tpos[qq];
-            const bool ta = c8 == 0 && va && (ka < thr || (ka == thr && pa <= tpos));
-            const bool tb = c8 == 1 && vb && (kb < thr || (kb == thr && pb <= tpos));
-            if (ta || tb) {
+            if (c8 < R && vmine && (kmine < thr || (kmine == thr && pmine <= tpos))) {
                 const int at = atomicAdd(&s_cnt[qq], 1);
                 if (at < a.cap) {
                     const int64_t o = ((int64_t)qq * a.splits + split) * a.cap + at;
-                    a.cand_keys[o] = ta ? ka : kb;
-                    a.cand_pos[o] = (int)(ta ? pa : pb);
+                    a.cand_keys[o] = kmine;
+                    a.cand_pos[o] = (int)pmine;
                 }
             }
         }
@@ -893,11 +911,18 @@ __device__ void bitonic_sort(float* sk, int* si, int p) {
     __syncthreads();
 }
 
-// One workgroup per query: sort all split candidates, keep the best kl, re-rank them
+// Candidates a bounded merge sorts at most; more at or below the bound (ties at the bound)
+// and the merge sorts all of them.
+constexpr int kMergeFiltered = 256;
+
+// One workgroup per query: sort the split candidates, keep the best kl, re-rank them
 // exactly (flat), sort again and emit the best k with the reference's finishing and
-// padding (flat.rs:229-237; gpu.rs:80-93 for raw keys).
+// padding (flat.rs:229-237; gpu.rs:80-93 for raw keys). With a bound, only candidates at or
+// below it are sorted (usually about kl of them): no candidate above a full split list's
+// tail can be among the best kl.
 __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
     extern __shared__ __attribute__((aligned(16))) char msmem[];
+    __shared__ int s_n;
     int p = 1;
     while (p < a.width) p <<= 1;
     float* sk = reinterpret_cast<float*>(msmem);
@@ -909,25 +934,72 @@ __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
     const float kInf = __int_as_float(0x7f800000);
     const float* pk = a.part_keys + (int64_t)q * a.width;
     const int* pi = a.part_ids + (int64_t)q * a.width;
-    for (int x = threadIdx.x; x < p; x += blockDim.x) {
-        float kv = kInf;
-        int id = kIdNone;
-        if (x < a.width) {
-            kv = pk[x];
-            id = pi[x];
-            if (id != kIdNone && a.rowidx) id = a.rowidx[id];
+    int bound = a.bound ? a.bound[q] : kTotalKeyInf;
+    if (a.gbest) {
+        __shared__ int s_gb[32], s_kth;
+        const int t = threadIdx.x;
+        if (t < 32) s_gb[t] = a.gbest[(int64_t)q * 32 + t];
+        __syncthreads();
+        const int pm = (a.kl + min(a.splits, 32) - 1) / min(a.splits, 32);
+        const int rank = (a.kl + pm - 1) / pm;  // <= min(splits, 32)
+        if (t < 32) {
+            // position of slot t in (key, slot) order; exactly one slot has rank - 1
+            const int v = s_gb[t];
+            int below = 0;
+            for (int u = 0; u < 32; ++u) below += s_gb[u] < v || (s_gb[u] == v && u < t);
+            if (below == rank - 1) s_kth = v;
         }
-        sk[x] = kv;
-        si[x] = id;
+        __syncthreads();
+        bound = min(bound, s_kth);
     }
-    bitonic_sort(sk, si, p);
+    int n = -1;  // candidates compacted below the bound; -1: sort them all
+    if (bound != kTotalKeyInf) {
+        if (threadIdx.x == 0) s_n = 0;
+        __syncthreads();
+        for (int x = threadIdx.x; x < a.width; x += blockDim.x) {
+            int id = pi[x];
+            const float kv = pk[x];
+            if (id != kIdNone && total_key(kv) <= bound) {
+                const int at = atomicAdd(&s_n, 1);
+                if (a.rowidx) id = a.rowidx[id];
+                sk[at] = kv;  // at < width <= p
+                si[at] = id;
+            }
+        }
+        __syncthreads();
+        n = s_n;
+        if (n > kMergeFiltered) n = -1;
+    }
+    int ps = p;  // entries sorted
+    if (n >= 0) {
+        ps = 1;
+        while (ps < n || ps < a.kl) ps <<= 1;
+        ps = min(ps, p);
+        for (int x = n + threadIdx.x; x < ps; x += blockDim.x) {
+            sk[x] = kInf;
+            si[x] = kIdNone;
+        }
+    } else {
+        for (int x = threadIdx.x; x < p; x += blockDim.x) {
+            float kv = kInf;
+            int id = kIdNone;
+            if (x < a.width) {
+                kv = pk[x];
+                id = pi[x];
+                if (id != kIdNone && a.rowidx) id = a.rowidx[id];
+            }
+            sk[x] = kv;
+            si[x] = id;
+        }
+    }
+    bitonic_sort(sk, si, ps);
 
     int p2 = 1;
     while (p2 < a.kl) p2 <<= 1;
     for (int x = threadIdx.x; x < p2; x += blockDim.x) {
         float kv = kInf;
         int id = kIdNone;
-        if (x < a.kl && x < p) {
+        if (x < a.kl && x < ps) {
             id = si[x];
             kv = sk[x];
             if (id != kIdNone && a.corpus) {

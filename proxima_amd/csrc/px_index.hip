@@ -804,6 +804,9 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     mg.part_ids = a.part_ids;
     mg.rowidx = rowidx;
     mg.width = n_eff > 0 ? splits * kl : 0;
+    mg.bound = ws.gtau.as<int>();
+    mg.gbest = ws.gbest.as<int>();
+    mg.splits = splits;
     mg.nq = (int)nq;
     mg.kl = kl;
     mg.k = (int)k;

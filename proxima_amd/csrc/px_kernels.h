@@ -132,6 +132,14 @@ struct MergeArgs {
     const int* part_ids;
     const int* rowidx;       // optional: position -> row id
     int width;               // candidates per query (splits * kl)
+    // optional [nq] total-order key bounds (the scan's gtau): a split's full list tail, so
+    // every candidate of the best kl has a key at or below it; +inf: no bound
+    const int* bound;
+    // optional [nq][32] published split keys (the scan's gbest) and the scan's split count:
+    // slot i holds a key with m = ceil(kl / min(splits, 32)) candidates of one split at or
+    // below it, so the ceil(kl / m)-th smallest slot bounds the best kl as well
+    const int* gbest;
+    int splits;
     int nq;
     int kl;                  // candidates kept after the first sort
     int k;                   // outputs per query
