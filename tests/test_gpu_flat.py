@@ -301,3 +301,24 @@ def test_large_k_filtered_multichunk(gpu):
     for k in (40, 100):
         for metric in (oracle.L2, oracle.IP):
             _check(data, q, k, metric, mask=mask)
+
+
+def test_merge_bound_with_many_ties(gpu):
+    # 0/1 rows: thousands of rows share each distance, so more than 256 split candidates sit
+    # at the scan's published bound and the merge sorts all of them; ties to the lower row
+    rng = np.random.default_rng(74)
+    data = rng.integers(0, 2, size=(30_000, 16)).astype(np.float32)
+    q = rng.integers(0, 2, size=(40, 16)).astype(np.float32)
+    for metric in (oracle.L2, oracle.IP):
+        ids, d, o_ids, o_d = _run(data, q, 10, metric)
+        assert np.array_equal(ids, o_ids), metric
+        assert np.array_equal(d, o_d), metric
+
+
+def test_merge_bound_gaussian_many_splits(gpu):
+    # a query tile spread over many splits (each publishing its bounds): the merge sorts
+    # only the candidates at or below them
+    data = datagen.gaussian(200_000, 64, 75)
+    q = datagen.gaussian(20, 64, 76)
+    for k in (1, 10, 20):
+        _check(data, q, k, oracle.L2)
