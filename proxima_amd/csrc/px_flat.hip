@@ -738,8 +738,8 @@ __global__ __launch_bounds__(512) void flat_vcollect_kernel(FlatScanArgs a) {
     }
     __syncthreads();
 
-    // R rows per lane group a step: four with one or two slots, two with more (registers)
-    constexpr int R = NQ <= 2 ? 4 : 2;
+    // R rows per lane group a step: four with one or two slots, fewer with more (registers)
+    constexpr int R = NQ <= 2 ? 4 : (NQ <= 8 ? 2 : 1);
     for (int64_t r = row0 + wave * (8 * R); r < row1; r += 8 * R * 8) {
         int64_t pr[R];
         bool vr[R];
@@ -820,7 +820,7 @@ __global__ __launch_bounds__(512) void flat_vcollect_kernel(FlatScanArgs a) {
 template <int NQ>
 static void launch_vcollect_n(const FlatScanArgs& a, hipStream_t s) {
     const dim3 grid((unsigned)a.splits), block(512);
-    const size_t lds = sizeof(float) * NQ * a.dp;
+    const size_t lds = sizeof(float) * NQ * a.dp;  // at most 64 KB (checked by the caller)
     if (a.metric == 0) {
         if (a.rowidx) hipLaunchKernelGGL((flat_vcollect_kernel<NQ, true, true>), grid, block, lds, s, a);
         else hipLaunchKernelGGL((flat_vcollect_kernel<NQ, true, false>), grid, block, lds, s, a);
@@ -831,11 +831,17 @@ static void launch_vcollect_n(const FlatScanArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_flat_vcollect(const FlatScanArgs& a, hipStream_t s) {
-    if (a.nq < 1 || a.nq > kVecQueries || a.dp > kVecMaxDp) return hipErrorInvalidValue;
+    // the slot count rounds up to a power of two: that many query rows of LDS
+    int np = 1;
+    while (np < a.nq) np <<= 1;
+    if (a.nq < 1 || a.nq > kVecQueries || a.dp > kVecMaxDp ||
+        (int64_t)np * a.dp > kVecMaxQueryFloats)
+        return hipErrorInvalidValue;
     if (a.nq == 1) launch_vcollect_n<1>(a, s);
     else if (a.nq == 2) launch_vcollect_n<2>(a, s);
     else if (a.nq <= 4) launch_vcollect_n<4>(a, s);
-    else launch_vcollect_n<8>(a, s);
+    else if (a.nq <= 8) launch_vcollect_n<8>(a, s);
+    else launch_vcollect_n<16>(a, s);
     return hipGetLastError();
 }
 

@@ -537,7 +537,10 @@ int run_collect(CollectJob& j) {
 // tighten from), whole multiples of 32, never more than a region can receive.
 // Whether a collect scan of `slots` query slots runs on the vector ALUs.
 bool vec_collect(int64_t slots, int64_t dp) {
-    return slots >= 1 && slots <= px::kVecQueries && dp <= px::kVecMaxDp;
+    int64_t np = 1;  // slots rounded up to the kernel's power of two
+    while (np < slots) np <<= 1;
+    return slots >= 1 && slots <= px::kVecQueries && dp <= px::kVecMaxDp &&
+           np * dp <= px::kVecMaxQueryFloats;
 }
 
 int64_t collect_cap(double expect, int64_t regions, int round, int64_t kk, int64_t most) {

@@ -65,8 +65,12 @@ hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s);
 // streams the corpus at memory speed instead. One region per (slot, split):
 // cand_keys [nq slots][splits][cap], cand_count [nq slots][splits]; dense: every key to
 // cand_keys [nq slots][n_eff] (no thresholds, no counts).
-constexpr int kVecQueries = 8;
+// (16 queries: 1M x 128 took 0.31 ms against the lists' 0.39 ms; 24 queries: 0.45 against
+// 0.41 ms, the vector ALUs' FMAs growing with the slots)
+constexpr int kVecQueries = 16;
 constexpr int kVecMaxDp = 1024;
+constexpr int kVecMaxQueryFloats = 16384;  // nq * dp: the queries' 64 KB of LDS
+static_assert(kVecQueries * kVecMaxDp <= kVecMaxQueryFloats, "query rows past 64 KB of LDS");
 hipError_t launch_flat_vcollect(const FlatScanArgs& a, hipStream_t s);
 // Threshold ladder rungs taken from the sample, loosest last; past the last rung a query's
 // threshold is +inf (every row passes).

@@ -1,6 +1,6 @@
 """GPU parity of few-query FlatIndex searches (the vector-ALU collect scan).
 
-A batch of at most 8 queries over rows of at most 1,024 padded dims runs the collect path
+A batch of at most 16 queries over rows of at most 1,024 padded dims runs the collect path
 with the corpus streamed on the vector ALUs (8 lanes per row, partial dot products summed
 across the lanes) instead of the MFMA tiles, whose 32-query tiles would be nearly all
 padding; the threshold sample runs the same way. These tests compare it with the oracle
@@ -112,9 +112,23 @@ def test_repeated_searches_one_handle(gpu):
     assert _check(data, q, 10, oracle.IP, searches=3) >= 1
 
 
-def test_nine_queries_use_the_lists(gpu):
+@pytest.mark.parametrize("nq", [9, 12, 16])
+def test_up_to_16_queries(gpu, nq):
     data = datagen.gaussian(20_000, 128, 87)
-    q = datagen.gaussian(9, 128, 88)
+    q = datagen.gaussian(nq, 128, 88)
+    assert _check(data, q, 10, oracle.IP) >= 1
+
+
+def test_16_queries_1024_dims(gpu):
+    # the largest query block: 16 x 1,024 floats, the 64 KB of LDS
+    data = datagen.gaussian(6_000, 1024, 94)
+    q = datagen.gaussian(16, 1024, 95)
+    assert _check(data, q, 10, oracle.L2) >= 1
+
+
+def test_17_queries_use_the_lists(gpu):
+    data = datagen.gaussian(20_000, 128, 92)
+    q = datagen.gaussian(17, 128, 93)
     assert _check(data, q, 10, oracle.L2) == 0
 
 
