@@ -925,7 +925,8 @@ constexpr int kMergeFiltered = 256;
 // exactly (flat), sort again and emit the best k with the reference's finishing and
 // padding (flat.rs:229-237; gpu.rs:80-93 for raw keys). With a bound, only candidates at or
 // below it are sorted (usually about kl of them): no candidate above a full split list's
-// tail can be among the best kl.
+// tail can be among the best kl. PQ lists publish no bounds; their kl-th smallest list
+// head serves instead.
 __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
     extern __shared__ __attribute__((aligned(16))) char msmem[];
     __shared__ int s_n;
@@ -957,6 +958,19 @@ __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
         }
         __syncthreads();
         bound = min(bound, s_kth);
+    }
+    if (a.sorted_lists && !a.bound && !a.gbest && a.width / a.kl >= a.kl) {
+        // kl distinct lists each hold a candidate at or below the kl-th smallest head
+        const int nl = a.width / a.kl;
+        int ph = 1;
+        while (ph < nl) ph <<= 1;
+        for (int x = threadIdx.x; x < ph; x += blockDim.x) {
+            sk[x] = x < nl ? pk[(int64_t)x * a.kl] : kInf;
+            si[x] = x;
+        }
+        bitonic_sort(sk, si, ph);
+        bound = total_key(sk[a.kl - 1]);
+        __syncthreads();  // every thread has read it before sk is reused
     }
     int n = -1;  // candidates compacted below the bound; -1: sort them all
     if (bound != kTotalKeyInf) {

@@ -1179,6 +1179,7 @@ int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_m
     mg.k = (int)k;
     mg.metric = p->metric;
     mg.corpus = nullptr;  // ADC keys are already the reference's
+    mg.sorted_lists = 1;
     mg.out_ids = d_ids;
     mg.out_dists = d_out;
     mg.raw_keys = 0;

@@ -144,6 +144,9 @@ struct MergeArgs {
     // below it, so the ceil(kl / m)-th smallest slot bounds the best kl as well
     const int* gbest;
     int splits;
+    // nonzero: the candidates are width / kl lists of kl, each in ascending order (PQ); with
+    // no published bounds, the kl-th smallest list head bounds the best kl
+    int sorted_lists;
     int nq;
     int kl;                  // candidates kept after the first sort
     int k;                   // outputs per query

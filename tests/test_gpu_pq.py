@@ -110,3 +110,29 @@ def test_pq_padding_and_empty(gpu):
     o_ids, o_d, _ = oracle.pq_search(pq.codebooks(), pq.codes(), data[:1], 120, oracle.IP)
     assert np.array_equal(ids, o_ids[0]) and np.array_equal(d, o_d[0])
     assert (ids[100:] == -1).all() and sorted(ids[:100].tolist()) == list(range(100))
+
+
+@pytest.mark.parametrize("nq", [1, 3])
+def test_pq_few_queries_many_lists_exact(gpu, nq):
+    # a few queries spread over hundreds of splits x 4 wave lists: the merge sorts only the
+    # candidates at or below the k'-th smallest list head
+    data = datagen.gaussian(200_000, 32, 301)
+    q = datagen.gaussian(nq, 32, 302)
+    pq = _index(data, 8, 8, oracle.L2, iters=4, sample=5000)
+    for k in (1, 10, 50):
+        ids, d = pq.search_batch(q, k=k)
+        o_ids, o_d, _ = oracle.pq_search(pq.codebooks(), pq.codes(), q, k, oracle.L2)
+        assert np.array_equal(ids, o_ids), k
+        assert np.array_equal(d, o_d), k
+
+
+def test_pq_few_queries_heavy_ties(gpu):
+    # 2-bit codebooks over 2 subspaces: 16 distinct codes, so thousands of rows share each
+    # key and more than 256 candidates sit at the list-head bound (the merge sorts all)
+    data = datagen.gaussian(100_000, 8, 303)
+    q = datagen.gaussian(2, 8, 304)
+    pq = _index(data, 2, 2, oracle.IP, iters=3, sample=2000)
+    ids, d = pq.search_batch(q, k=20)
+    o_ids, o_d, _ = oracle.pq_search(pq.codebooks(), pq.codes(), q, 20, oracle.IP)
+    assert np.array_equal(ids, o_ids)
+    assert np.array_equal(d, o_d)
