@@ -122,9 +122,25 @@ struct Workspace {
     DevBuf q, qn, mask, rowidx, scratch, count, part_k, part_i, out_ids, out_d, gtau, gbest;
     // collect path (k' past the lists)
     DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
+    DevBuf qraw;             // host-path queries before padding to dp
     int* h_count = nullptr;  // pinned
     int* h_status = nullptr; // pinned, h_status_cap ints
     int64_t h_status_cap = 0;
+    // pinned staging for the host-buffer entry points: queries in, results out (pageable
+    // copies are staged by the runtime, and 2-D ones row by row)
+    char* h_in = nullptr;
+    char* h_out = nullptr;
+    size_t h_in_cap = 0, h_out_cap = 0;
+    static int ensure_host(char*& buf, size_t& cap, size_t bytes) {
+        if (bytes <= cap) return PX_OK;
+        if (buf) (void)hipHostFree(buf);
+        buf = nullptr;
+        cap = 0;
+        const size_t want = std::max<size_t>(bytes, 4096);
+        PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&buf), want));
+        cap = want;
+        return PX_OK;
+    }
     int ensure_pinned() {
         if (!h_count) PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_count), sizeof(int)));
         return PX_OK;
@@ -149,8 +165,44 @@ struct Workspace {
         if (h_status) (void)hipHostFree(h_status);
         h_status = nullptr;
         h_status_cap = 0;
+        qraw.release();
+        if (h_in) (void)hipHostFree(h_in);
+        if (h_out) (void)hipHostFree(h_out);
+        h_in = h_out = nullptr;
+        h_in_cap = h_out_cap = 0;
     }
 };
+
+// Host queries [nq][dim] to device [nq][dp] (zero pad columns) through pinned staging.
+int upload_queries(Workspace& ws, const float* queries, int64_t nq, int64_t dim, int64_t dp,
+                   hipStream_t s, const float** d_q) {
+    const size_t bytes = sizeof(float) * (size_t)(nq * dim);
+    PX_TRY(Workspace::ensure_host(ws.h_in, ws.h_in_cap, bytes));
+    std::memcpy(ws.h_in, queries, bytes);
+    PX_TRY(ws.q.reserve(sizeof(float) * nq * dp));
+    if (dp == dim) {
+        PX_HIP(hipMemcpyAsync(ws.q.p, ws.h_in, bytes, hipMemcpyHostToDevice, s));
+    } else {
+        PX_TRY(ws.qraw.reserve(bytes));
+        PX_HIP(hipMemcpyAsync(ws.qraw.p, ws.h_in, bytes, hipMemcpyHostToDevice, s));
+        PX_HIP(px::launch_pad_rows(ws.qraw.as<float>(), nq, (int)dim, (int)dp, ws.q.as<float>(), s));
+    }
+    *d_q = ws.q.as<float>();
+    return PX_OK;
+}
+
+// Device results [nq][k] to the caller's host buffers through pinned staging; waits.
+int download_results(Workspace& ws, int64_t nq, int64_t k, hipStream_t s, int64_t* out_ids,
+                     float* out_d) {
+    const size_t bi = sizeof(int64_t) * (size_t)(nq * k), bd = sizeof(float) * (size_t)(nq * k);
+    PX_TRY(Workspace::ensure_host(ws.h_out, ws.h_out_cap, bi + bd));
+    PX_HIP(hipMemcpyAsync(ws.h_out, ws.out_ids.p, bi, hipMemcpyDeviceToHost, s));
+    PX_HIP(hipMemcpyAsync(ws.h_out + bi, ws.out_d.p, bd, hipMemcpyDeviceToHost, s));
+    PX_HIP(hipStreamSynchronize(s));
+    std::memcpy(out_ids, ws.h_out, bi);
+    std::memcpy(out_d, ws.h_out + bi, bd);
+    return PX_OK;
+}
 
 // Compacts a device keep-mask into ascending row ids; returns the kept count in *n_eff.
 int compact_mask(Workspace& ws, const uint8_t* d_mask, int64_t n, hipStream_t s, int64_t* n_eff,
@@ -866,10 +918,8 @@ int flat_search_host(px_flat* f, const float* queries, int64_t nq, int64_t k, co
     PX_TRY(flat_sync(f));
     Workspace& ws = f->ws;
     hipStream_t s = f->stream;
-    PX_TRY(ws.q.reserve(sizeof(float) * nq * f->dp));
-    if (f->dp != f->dim) PX_HIP(hipMemsetAsync(ws.q.p, 0, sizeof(float) * nq * f->dp, s));
-    PX_HIP(hipMemcpy2DAsync(ws.q.p, sizeof(float) * f->dp, queries, sizeof(float) * f->dim,
-                            sizeof(float) * f->dim, nq, hipMemcpyHostToDevice, s));
+    const float* d_q = nullptr;
+    PX_TRY(upload_queries(ws, queries, nq, f->dim, f->dp, s, &d_q));
     const uint8_t* d_mask = nullptr;
     if (mask) {
         PX_TRY(ws.mask.reserve(f->d_rows));
@@ -878,12 +928,9 @@ int flat_search_host(px_flat* f, const float* queries, int64_t nq, int64_t k, co
     }
     PX_TRY(ws.out_ids.reserve(sizeof(int64_t) * nq * k));
     PX_TRY(ws.out_d.reserve(sizeof(float) * nq * k));
-    PX_TRY(flat_run(f, ws.q.as<float>(), nq, k, d_mask, ws.out_ids.as<int64_t>(),
-                    ws.out_d.as<float>(), raw_keys));
-    PX_HIP(hipMemcpyAsync(out_ids, ws.out_ids.p, sizeof(int64_t) * nq * k, hipMemcpyDeviceToHost, s));
-    PX_HIP(hipMemcpyAsync(out_d, ws.out_d.p, sizeof(float) * nq * k, hipMemcpyDeviceToHost, s));
-    PX_HIP(hipStreamSynchronize(s));
-    return PX_OK;
+    PX_TRY(flat_run(f, d_q, nq, k, d_mask, ws.out_ids.as<int64_t>(), ws.out_d.as<float>(),
+                    raw_keys));
+    return download_results(ws, nq, k, s, out_ids, out_d);
 }
 
 // ---- PQ ----------------------------------------------------------------------------
@@ -1503,8 +1550,8 @@ int px_pq_search(const px_pq* cp, const float* queries, int64_t nq, int64_t k,
     PX_TRY(pq_sync(p));
     Workspace& ws = p->ws;
     hipStream_t s = p->stream;
-    PX_TRY(ws.q.reserve(sizeof(float) * nq * p->dim));
-    PX_HIP(hipMemcpyAsync(ws.q.p, queries, sizeof(float) * nq * p->dim, hipMemcpyHostToDevice, s));
+    const float* d_q = nullptr;
+    PX_TRY(upload_queries(ws, queries, nq, p->dim, p->dim, s, &d_q));
     const uint8_t* d_mask = nullptr;
     if (mask) {
         PX_TRY(ws.mask.reserve(p->d_rows));
@@ -1513,11 +1560,8 @@ int px_pq_search(const px_pq* cp, const float* queries, int64_t nq, int64_t k,
     }
     PX_TRY(ws.out_ids.reserve(sizeof(int64_t) * nq * k));
     PX_TRY(ws.out_d.reserve(sizeof(float) * nq * k));
-    PX_TRY(pq_run(p, ws.q.as<float>(), nq, k, d_mask, ws.out_ids.as<int64_t>(), ws.out_d.as<float>()));
-    PX_HIP(hipMemcpyAsync(out_ids, ws.out_ids.p, sizeof(int64_t) * nq * k, hipMemcpyDeviceToHost, s));
-    PX_HIP(hipMemcpyAsync(out_dists, ws.out_d.p, sizeof(float) * nq * k, hipMemcpyDeviceToHost, s));
-    PX_HIP(hipStreamSynchronize(s));
-    return PX_OK;
+    PX_TRY(pq_run(p, d_q, nq, k, d_mask, ws.out_ids.as<int64_t>(), ws.out_d.as<float>()));
+    return download_results(ws, nq, k, s, out_ids, out_dists);
 }
 
 int px_pq_search_device(const px_pq* cp, const float* d_queries, int64_t nq, int64_t k,
