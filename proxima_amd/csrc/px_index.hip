@@ -385,10 +385,23 @@ int flat_sync(px_flat* f) {
         f->d_cap = cap;
     }
     float* dst = f->d_x + f->d_rows * f->dp;
-    if (f->dp != f->dim)
-        PX_HIP(hipMemsetAsync(dst, 0, sizeof(float) * add * f->dp, f->stream));
-    PX_HIP(hipMemcpy2DAsync(dst, sizeof(float) * f->dp, f->pending.data(), sizeof(float) * f->dim,
-                            sizeof(float) * f->dim, add, hipMemcpyHostToDevice, f->stream));
+    if (f->dp == f->dim) {
+        PX_HIP(hipMemcpyAsync(dst, f->pending.data(), sizeof(float) * add * f->dim,
+                              hipMemcpyHostToDevice, f->stream));
+    } else {
+        // rows go up contiguously (a pitched host copy is staged row by row) in chunks of
+        // 64 MB, and are padded to dp on the device
+        const int64_t chunk =
+            std::max<int64_t>(1, ((int64_t)64 << 20) / ((int64_t)sizeof(float) * f->dim));
+        PX_TRY(f->ws.qraw.reserve(sizeof(float) * std::min(add, chunk) * f->dim));
+        for (int64_t r = 0; r < add; r += chunk) {
+            const int64_t nr = std::min(chunk, add - r);
+            PX_HIP(hipMemcpyAsync(f->ws.qraw.p, f->pending.data() + r * f->dim,
+                                  sizeof(float) * nr * f->dim, hipMemcpyHostToDevice, f->stream));
+            PX_HIP(px::launch_pad_rows(f->ws.qraw.as<float>(), nr, (int)f->dim, (int)f->dp,
+                                       dst + r * f->dp, f->stream));
+        }
+    }
     PX_HIP(px::launch_row_norms(dst, add, (int)f->dp, f->d_norm + f->d_rows, f->stream));
     PX_HIP(hipStreamSynchronize(f->stream));
     f->d_rows = need;
@@ -1332,10 +1345,26 @@ int px_flat_get_vectors(const px_flat* cf, int64_t first, int64_t n, float* out)
     const int64_t dev_hi = std::min(first + n, f->d_rows);
     if (first < dev_hi) {
         PX_TRY(flat_bind(f));
-        PX_HIP(hipMemcpy2DAsync(out, sizeof(float) * f->dim, f->d_x + first * f->dp,
-                                sizeof(float) * f->dp, sizeof(float) * f->dim, dev_hi - first,
-                                hipMemcpyDeviceToHost, f->stream));
-        PX_HIP(hipStreamSynchronize(f->stream));
+        if (f->dp == f->dim) {
+            PX_HIP(hipMemcpyAsync(out, f->d_x + first * f->dp, sizeof(float) * (dev_hi - first) * f->dp,
+                                  hipMemcpyDeviceToHost, f->stream));
+            PX_HIP(hipStreamSynchronize(f->stream));
+        } else {
+            // padded rows come down contiguously in 64 MB chunks (a pitched copy to host
+            // memory is staged row by row) and drop their pad columns on the host
+            const int64_t chunk =
+                std::max<int64_t>(1, ((int64_t)64 << 20) / ((int64_t)sizeof(float) * f->dp));
+            std::vector<float> stage((size_t)(std::min(chunk, dev_hi - first) * f->dp));
+            for (int64_t r = first; r < dev_hi; r += chunk) {
+                const int64_t nr = std::min(chunk, dev_hi - r);
+                PX_HIP(hipMemcpyAsync(stage.data(), f->d_x + r * f->dp, sizeof(float) * nr * f->dp,
+                                      hipMemcpyDeviceToHost, f->stream));
+                PX_HIP(hipStreamSynchronize(f->stream));
+                for (int64_t i = 0; i < nr; ++i)
+                    std::memcpy(out + (r - first + i) * f->dim, stage.data() + i * f->dp,
+                                sizeof(float) * f->dim);
+            }
+        }
     }
     for (int64_t r = std::max(first, f->d_rows); r < first + n; ++r)
         std::memcpy(out + (r - first) * f->dim, f->pending.data() + (r - f->d_rows) * f->dim,
