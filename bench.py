@@ -214,9 +214,15 @@ def bench_flat(args, dev):
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
                      "traffic": read_traffic("flat_scan_kernel_l2_1Mx128_q10k_k10.md", headline),
-                     "kernel": ("flat_scan_kernel (per-split lists)" if info["collect_rounds"] == 0
-                                else "flat_scan_kernel (threshold-collect: sample scan, ladder "
-                                     "and collect scan)"),
+                     "kernel": {"lists": "flat_scan_kernel (per-split lists)",
+                                "collect-sampled": "flat_scan_kernel (threshold-collect: sample "
+                                                   "scan, ladder and collect scan)",
+                                "collect-bounded": "flat_scan_kernel (threshold-collect: "
+                                                   "collect scan bounded by the splits' shared "
+                                                   "bound, no sample)",
+                                "vector": "flat_vcollect_kernel (vector-ALU collect: sample "
+                                          "and collect scans)"}[info["path"]],
+                     "collect_rounds": info["collect_rounds"],
                      "kernel_ms": float(np.mean(scan_ms)),
                      "algorithmic_flop_per_launch": flops},
         "pipeline_ms": float(np.mean(total_ms)),

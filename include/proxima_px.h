@@ -163,11 +163,20 @@ int px_hip_versions(int* runtime_version, int* driver_version);
 int px_flat_set_timing(px_flat* idx, int enable);
 int px_flat_last_timing(const px_flat* idx, float* scan_ms, float* total_ms, int* splits,
                         int* blocks);
-/* Collect rounds of the handle's last search: 0 when it used per-split candidate lists
- * (k < 16, or batches under 256 queries, with k + 8 <= 128), else the rounds of the
- * threshold-collect path (1 when every query finished in the first). Diagnostic; no
- * counterpart in the reference. */
+/* Collect rounds of the handle's last search: 0 when it used per-split candidate lists,
+ * else the rounds of the threshold-collect path (1 when every query finished in the
+ * first). Diagnostic; no counterpart in the reference. */
 int px_flat_last_rounds(const px_flat* idx, int* rounds);
+/* Selection path of the handle's last search: PX_PATH_LISTS (per-split candidate lists),
+ * PX_PATH_COLLECT_SAMPLED (threshold-collect whose first round takes its thresholds from a
+ * strided row sample), PX_PATH_COLLECT_BOUNDED (threshold-collect whose first round is
+ * bounded by the splits' shared bound alone, no sample), PX_PATH_VECTOR (the vector-ALU
+ * collect scan of a few queries). Diagnostic; no counterpart in the reference. */
+#define PX_PATH_LISTS 0
+#define PX_PATH_COLLECT_SAMPLED 1
+#define PX_PATH_COLLECT_BOUNDED 2
+#define PX_PATH_VECTOR 3
+int px_flat_last_path(const px_flat* idx, int* path);
 /* The same for PqIndex searches (k <= 128: per-wave lists; above: threshold-collect). */
 int px_pq_last_rounds(const px_pq* idx, int* rounds);
 int px_pq_set_timing(px_pq* idx, int enable);

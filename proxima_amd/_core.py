@@ -271,10 +271,12 @@ class FlatIndex:
         splits, blocks = ctypes.c_int(), ctypes.c_int()
         _check(self._lib.px_flat_last_timing(self._h, ctypes.byref(scan), ctypes.byref(total),
                                              ctypes.byref(splits), ctypes.byref(blocks)))
-        rounds = ctypes.c_int()
+        rounds, path = ctypes.c_int(), ctypes.c_int()
         _check(self._lib.px_flat_last_rounds(self._h, ctypes.byref(rounds)))
+        _check(self._lib.px_flat_last_path(self._h, ctypes.byref(path)))
         return {"scan_ms": scan.value, "total_ms": total.value, "splits": splits.value,
-                "blocks": blocks.value, "collect_rounds": rounds.value}
+                "blocks": blocks.value, "collect_rounds": rounds.value,
+                "path": ("lists", "collect-sampled", "collect-bounded", "vector")[path.value]}
 
 
 class PqIndex:

@@ -158,6 +158,40 @@ __device__ __forceinline__ int kth_smallest32(int (&v)[16], int rank) {
     return r;
 }
 
+// kl-th smallest (kl <= 64) key of the 64 rows a lane pair holds for query j in the first
+// tile of a split (key[x] is row 32 (x / 16) + mfma_row(x % 16, h)); rows at or past rem,
+// and padding queries, do not count. +inf when fewer than kl rows count. kl rounds of
+// "smallest remaining" over the pair, as in first_tile_lists, keeping only the value.
+__device__ __forceinline__ float first_tile_kth(const float (&key)[32], int rem, bool qvalid,
+                                                int kl) {
+    constexpr int kNoKey = 0x7fffffff;
+    const int h = lane_id() >> 5;
+    int tk[32];
+#pragma unroll
+    for (int x = 0; x < 32; ++x) {
+        const int off = (x >> 4) * 32 + mfma_row(x & 15, h);
+        tk[x] = (qvalid && off < rem) ? total_key(key[x]) : kNoKey;
+    }
+    int last = kNoKey;
+    for (int r = 0; r < kl; ++r) {
+        int bt = kNoKey, bx = 0;
+#pragma unroll
+        for (int x = 0; x < 32; ++x) {
+            const bool lt = tk[x] < bt;
+            bt = lt ? tk[x] : bt;
+            bx = lt ? x : bx;
+        }
+        const int pt = __shfl_xor(bt, 32);
+        // equal minima: the h == 0 lane's goes first (the partner agrees)
+        const bool mine = bt < pt || (bt == pt && h == 0);
+        last = mine ? bt : pt;
+        if (__ballot(last != kNoKey) == 0) break;  // no query has a row left
+#pragma unroll
+        for (int x = 0; x < 32; ++x) tk[x] = (mine && x == bx) ? kNoKey : tk[x];
+    }
+    return last == kNoKey ? __int_as_float(0x7f800000) : from_total_key(last);
+}
+
 // One workgroup = WAVES waves = 32 * WAVES queries x one corpus split of rows_per_split rows.
 //
 // MFMA operands: A = corpus rows (M), B = queries (N), K = dims. For the 4 sub-steps e of
@@ -242,10 +276,24 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     int64_t next_refresh = 1;                                // tile index of the next refresh
     const float* qrow = a.queries + (int64_t)(qvalid ? q : 0) * a.dp;
     int* gtau = COLLECT ? nullptr : a.gtau + (qvalid ? q : 0);
-    int* gbest = COLLECT ? nullptr : a.gbest + (int64_t)(qvalid ? q : 0) * 32;
+    // collect mode with a.gbest: a shared bound as well (below)
+    int* gbest = (COLLECT && !a.gbest) ? nullptr : a.gbest + (int64_t)(qvalid ? q : 0) * 32;
     // collect mode: this query's threshold (nothing passes -inf) and region
     float cthr = -kInf;
     int cpos = -1, ccount = 0;
+    // Collect mode's shared bound (a.gbest set, a.kl <= min(splits, 32)): each lane
+    // publishes the smallest key of its rows of the split so far to the query's slot
+    // split % 32 (atomicMin; the two lanes of a pair share the slot), so every published
+    // slot has a row of its own splits at or below it, and the kl-th smallest slot bounds
+    // the query's best kl. A row passes when it is at or below both the threshold and
+    // gbound; ctest = min(cthr, gbound) pre-screens a tile's keys.
+    // The first tile of a split also bounds itself: its kl-th smallest key has kl of the
+    // split's rows at or below it (so a first round needs no threshold), and the
+    // first refresh comes right after the first tile's publication.
+    const bool dyn = COLLECT && a.gbest != nullptr && !a.dense;
+    int cpub = kTotalKeyInf;
+    float ctest = -kInf;
+    if (dyn) next_refresh = 0;
     // list mode with one query chunk: the insertions of a tile's second row block run during
     // the next tile's MFMAs (an insertion otherwise holds up the stage barrier for all eight
     // waves); the first block's run in the epilogue, as do all of them with MULTI
@@ -259,7 +307,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         if constexpr (COLLECT) {
             const int off = (x >> 4) * 32 + mfma_row(x & 15, h);
             const float kv = pkey[x];
-            const bool p = off < prem && (kv < cthr || (kv == cthr && pt0 + off <= cpos));
+            const bool p = off < prem && (kv < cthr || (kv == cthr && pt0 + off <= cpos)) &&
+                           kv <= gbound;
             if (p) {
                 if (ccount < a.cap) {
                     const int64_t at =
@@ -452,7 +501,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             if constexpr (COLLECT) {
                 // one compare per row and one uniform branch per pair of rows; the exact
                 // test and the append only where some lane has a row at or below
-                if (pend && __ballot(pkey[2 * g] <= cthr || pkey[2 * g + 1] <= cthr)) {
+                if (pend && __ballot(pkey[2 * g] <= ctest || pkey[2 * g + 1] <= ctest)) {
                     collect_x(2 * g);
                     collect_x(2 * g + 1);
                 }
@@ -519,16 +568,48 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                 // tested during the next tile's MFMAs (or after the last tile); with MULTI
                 // (several chunks per tile, and the next query chunk held in registers) the
                 // keys are tested here instead, so that they are not held across the MFMAs
+                if (dyn) {
+                    // this lane's smallest key of the split's rows so far (the last tile
+                    // of a split may end early: rows past its end do not count)
+                    float vmin = kmin;
+                    if (rem < kTileRows) {
+                        vmin = kInf;
+#pragma unroll
+                        for (int x = 0; x < 32; ++x)
+                            vmin = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? fminf(vmin, key[x])
+                                                                             : vmin;
+                    }
+                    if (t0 == row0) gbound = first_tile_kth(key, rem, qvalid, a.kl);
+                    const int tk = total_key(vmin);
+                    if (qvalid && tk < cpub) {
+                        atomicMin(gbest + (split & 31), tk);
+                        cpub = tk;
+                    }
+                    if (ti == next_refresh) {
+                        const long long* src = reinterpret_cast<const long long*>(gbest + h * 16);
+                        int v[16];
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) {
+                            const long long w = __hip_atomic_load(src + u, __ATOMIC_RELAXED,
+                                                                  __HIP_MEMORY_SCOPE_AGENT);
+                            v[2 * u] = (int)(w & 0xffffffffll);
+                            v[2 * u + 1] = (int)(w >> 32);
+                        }
+                        gbound = fminf(gbound, from_total_key(kth_smallest32(v, a.kl)));
+                        next_refresh = ti + max<int64_t>(1, ti >> 2);
+                    }
+                }
+                ctest = fminf(cthr, gbound);
 #pragma unroll
                 for (int x = 0; x < 32; ++x) pkey[x] = key[x];
                 pt0 = (int)t0;
                 prem = rem;
-                pend = __ballot(kmin <= cthr) != 0;
+                pend = __ballot(kmin <= ctest) != 0;
                 if constexpr (MULTI) {
                     if (pend) {
 #pragma unroll
                         for (int g = 0; g < 16; ++g) {
-                            if (__ballot(pkey[2 * g] <= cthr || pkey[2 * g + 1] <= cthr)) {
+                            if (__ballot(pkey[2 * g] <= ctest || pkey[2 * g + 1] <= ctest)) {
                                 collect_x(2 * g);
                                 collect_x(2 * g + 1);
                             }
@@ -1145,22 +1226,60 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
         return;
     }
 
-    int p = 1;
-    while (p < held) p <<= 1;
+    // A finishing query with the scan's shared bound sorts only the candidates at or below
+    // it: the kk-th smallest slot (every slot has a collected row of its own at or below it).
+    int bound = kTotalKeyInf;
+    if (a.gbest && finish) {
+        __shared__ int s_gb[32], s_kth;
+        if (t < 32) s_gb[t] = a.gbest[(int64_t)q * 32 + t];
+        if (t == 0) s_kth = kTotalKeyInf;
+        __syncthreads();
+        if (t < 32) {
+            // position of slot t in (key, slot) order; exactly one slot has kk - 1
+            const int v = s_gb[t];
+            int below = 0;
+            for (int u = 0; u < 32; ++u) below += s_gb[u] < v || (s_gb[u] == v && u < t);
+            if (below == a.kk - 1) s_kth = v;
+        }
+        __syncthreads();
+        bound = s_kth;
+    }
     // candidate x comes from the region r with s_off[r] <= x < s_off[r + 1] (binary search),
     // so that every thread's loads are independent of each other
-    for (int x = threadIdx.x; x < held; x += blockDim.x) {
+    auto region_of = [&](int x) {
         int lo = 0, hi = a.regions - 1;
         while (lo < hi) {
             const int mid = (lo + hi + 1) >> 1;
             if (s_off[mid] <= x) lo = mid;
             else hi = mid - 1;
         }
-        const int64_t at = (int64_t)lo * a.cap + (x - s_off[lo]);
-        sk[x] = rk[at];
-        si[x] = rp[at];
+        return (int64_t)lo * a.cap + (x - s_off[lo]);
+    };
+    int avail = held;  // candidates sorted into sk/si
+    if (bound != kTotalKeyInf) {
+        if (t == 0) s_total = 0;
+        __syncthreads();
+        for (int x = threadIdx.x; x < held; x += blockDim.x) {
+            const int64_t at = region_of(x);
+            const float kv = rk[at];
+            if (total_key(kv) <= bound) {
+                const int i = atomicAdd(&s_total, 1);
+                sk[i] = kv;
+                si[i] = rp[at];
+            }
+        }
+        __syncthreads();
+        avail = s_total;
+    } else {
+        for (int x = threadIdx.x; x < held; x += blockDim.x) {
+            const int64_t at = region_of(x);
+            sk[x] = rk[at];
+            si[x] = rp[at];
+        }
     }
-    for (int x = held + threadIdx.x; x < p; x += blockDim.x) {
+    int p = 1;
+    while (p < avail) p <<= 1;
+    for (int x = avail + threadIdx.x; x < p; x += blockDim.x) {
         sk[x] = kInf;
         si[x] = kIdNone;
     }
@@ -1176,7 +1295,7 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
         return;
     }
 
-    const int keep = min(a.kk, held);
+    const int keep = min(a.kk, avail);
     int p2 = 1;
     while (p2 < keep) p2 <<= 1;
     for (int x = threadIdx.x; x < p2; x += blockDim.x) {

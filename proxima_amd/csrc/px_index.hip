@@ -321,6 +321,7 @@ struct px_flat {
     int64_t d_rows = 0, d_cap = 0;
     Workspace ws;
     Timing timing;
+    int last_path = PX_PATH_LISTS; // selection path of the last search
     int last_rounds = 0;           // collect rounds of the last search (0: list path)
     std::mutex mu;
 };
@@ -410,10 +411,13 @@ int flat_sync(px_flat* f) {
 }
 
 // Smallest k served by the threshold-collect path for batches of at least
-// kCollectMinQueries queries. Below it the per-split lists are faster (1M x 128, 10,000
-// queries: 23.6 ms a batch at k = 10 against 24.4); from k = 16 the collect path is ahead
-// (24.8 / 23.7 ms at k = 16, 27.9 / 24.5 at k = 24, 46.5 / 25.9 at k = 64). Smaller batches keep the lists, which need no sample pass and no host round
-// trip. The PX_FLAT_COLLECT_FROM_K environment variable overrides the k (read once).
+// kCollectMinQueries queries. Below it the per-split lists are faster than a collect round
+// that samples its thresholds (1M x 128, 10,000 queries: 23.6 ms a batch at k = 10 against
+// 24.4); from k = 16 the collect path is ahead (24.8 / 23.7 ms at k = 16, 27.9 / 24.5 at
+// k = 24, 46.5 / 25.9 at k = 64). Smaller k also goes to the collect path where its first
+// round needs no sample (collect_bound_only). Smaller batches keep the lists, which need no
+// sample pass and no host round trip. The PX_FLAT_COLLECT_FROM_K environment variable
+// overrides the k (read once).
 constexpr int64_t kCollectMinQueries = 256;
 int64_t collect_from_k() {
     static const int64_t v = [] {
@@ -476,6 +480,15 @@ int64_t collect_bytes() {
     return v;
 }
 constexpr int64_t kCollectBatch = 16384;
+// Whether the MFMA collect scan also applies the splits' shared bound (default on;
+// PX_COLLECT_SHARED_BOUND=0 turns it off, for measurement; read once).
+bool shared_collect_bound() {
+    static const bool v = [] {
+        const char* e = std::getenv("PX_COLLECT_SHARED_BOUND");
+        return !(e && *e == '0');
+    }();
+    return v;
+}
 
 struct CollectJob {
     Workspace* ws = nullptr;
@@ -493,6 +506,12 @@ struct CollectJob {
                       int64_t max_bytes, int64_t* regions, int64_t* cap)>
         scan;
     px::CollectSelectArgs sel{};  // metric, corpus (null: no re-rank), dims, k, outputs
+    // The first round's scan bounds itself (the splits' shared bound): no sample, no
+    // ladder, every query's threshold +inf; bound_expect sizes its regions.
+    bool bound_only = false;
+    double bound_expect = 0.0;
+    // set by scan: the shared-bound slots of its launch (null when it applied none)
+    const int* sel_gbest = nullptr;
 };
 
 int run_collect(CollectJob& j) {
@@ -510,11 +529,12 @@ int run_collect(CollectJob& j) {
 
     // expected candidates per query in the first round
     double expect = (double)n_eff;
-    if (n_eff <= kk) {
+    if (n_eff <= kk || j.bound_only) {
         // every row is a candidate
         PX_HIP(px::launch_fill_int(ws.thr_k.as<int>(), nq, px::kTotalKeyInf, s));
         PX_HIP(px::launch_fill_int(ws.thr_p.as<int>(), nq, 0x7fffffff, s));
         PX_HIP(px::launch_fill_int(ws.rung.as<int>(), nq, px::kRungs, s));
+        if (n_eff > kk) expect = j.bound_expect;
     } else {
         const int64_t S = std::max<int64_t>(
             1, std::min<int64_t>({n_eff, (int64_t)16384, 80 * n_eff / kk}));
@@ -562,6 +582,7 @@ int run_collect(CollectJob& j) {
             c.rung = ws.rung.as<int>();
             c.status = ws.status.as<int>();
             c.kk = (int)kk;
+            c.gbest = j.sel_gbest;
             PX_HIP(px::launch_collect_select(c, (int)take, s));
             if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[2], s));
             done += take;
@@ -614,6 +635,41 @@ int64_t collect_cap(double expect, int64_t regions, int round, int64_t kk, int64
     return std::max<int64_t>(1, std::min<int64_t>((cap + 31) / 32 * 32, most));
 }
 
+// Splits and rows per split of an MFMA collect scan of `slots` query slots.
+void collect_splits(int64_t n_eff, int64_t slots, int cus, int64_t* splits, int64_t* rps) {
+    const int64_t groups = (slots + 255) / 256;
+    int64_t sp = std::min<int64_t>(choose_flat_splits(n_eff, groups, 1, cus, false),
+                                   px::kMaxCollectRegions / 2);
+    int64_t r = (n_eff + sp - 1) / sp;
+    r = std::max<int64_t>((r + 63) / 64 * 64, 64);
+    *splits = std::max<int64_t>(1, (n_eff + r - 1) / r);
+    *rps = r;
+}
+
+// Whether an MFMA collect scan over `splits` splits applies the shared bound for k'.
+bool collect_shared_bound(int64_t splits, int64_t kk) {
+    return shared_collect_bound() && std::min<int64_t>(splits, 32) >= kk;
+}
+
+// Whether a collect batch of nq query slots runs its first round on the shared bound alone
+// (no sample, no ladder). Measured on one MI355X against the per-split lists and the
+// sampled threshold (ms per batch of device-resident queries):
+//   1M x 128 SIFT-like L2, 10,000 queries: k = 10: 22.4 (lists 23.5); k = 16: 23.2 (lists
+//     24.7, sampled 24.4); k = 24 (k' = 32): 25.8 and a second round (sampled 24.5)
+//   300k x 128, 10,000 queries, k = 10: 7.6 (lists 8.3)
+//   1M x 128, 2,000 queries (96 splits), k = 10: 5.1 (lists 5.0): every split's first
+//     tile adds up to k' candidates a query
+//   100k / 1M x 384 IP, 1,000-4,000 queries, k = 10: 1-2% behind the lists (several query
+//     chunks: the keys are tested in the epilogue, not during the next tile's MFMAs)
+// so: one 128-dim chunk, at most 48 splits, k' <= 24 (the bound is the k'-th smallest of
+// at most 32 split minima; at k' = 32 it is their largest and prunes little).
+bool collect_bound_only(int64_t n_eff, int64_t nq, int64_t kk, int64_t dp, int cus) {
+    if (dp > 128 || kk > 24 || nq < kCollectMinQueries || vec_collect(nq, dp)) return false;
+    int64_t splits = 1, rps = 64;
+    collect_splits(n_eff, std::min(nq, kCollectBatch), cus, &splits, &rps);
+    return splits <= 48 && collect_shared_bound(splits, kk);
+}
+
 int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
                            const int* rowidx, int64_t* d_ids, float* d_out, int raw_keys) {
     Workspace& ws = f->ws;
@@ -624,6 +680,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     j.stream = s;
     j.timing = &f->timing;
     j.last_rounds = &f->last_rounds;
+    f->last_path = vec_collect(nq, f->dp) ? PX_PATH_VECTOR : PX_PATH_COLLECT_SAMPLED;
     j.nq = nq;
     j.kk = k + kReRankMargin;
     j.n_eff = n_eff;
@@ -746,12 +803,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             return PX_OK;
         }
         for (;;) {
-            const int64_t groups = (slots + 255) / 256;
-            splits = std::min<int64_t>(choose_flat_splits(n_eff, groups, 1, cus, false),
-                                       px::kMaxCollectRegions / 2);
-            rps = (n_eff + splits - 1) / splits;
-            rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
-            splits = std::max<int64_t>(1, (n_eff + rps - 1) / rps);
+            collect_splits(n_eff, slots, cus, &splits, &rps);
             // two regions per split (one per lane of the pair holding a query), each of
             // which receives at most half the split's rows
             *regions = 2 * splits;
@@ -782,6 +834,15 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.cand_pos = ws.cand_p.as<int>();
         a.cand_count = ws.cand_n.as<int>();
         a.cap = (int)*cap;
+        // the shared bound needs k' publishing slots (one per split, at most 32)
+        j.sel_gbest = nullptr;
+        if (collect_shared_bound(splits, j.kk)) {
+            PX_TRY(ws.gbest.reserve(sizeof(int) * j.nq * 32));
+            PX_HIP(px::launch_fill_int(ws.gbest.as<int>(), j.nq * 32, px::kTotalKeyInf, s));
+            a.gbest = ws.gbest.as<int>();
+            a.kl = (int)j.kk;
+            j.sel_gbest = a.gbest;
+        }
         PX_HIP(px::launch_flat_collect(a, s));
         if (round == 0) {
             f->timing.splits = (int)splits;
@@ -789,6 +850,18 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         }
         return PX_OK;
     };
+    if (!vec_collect(nq, f->dp)) {
+        // the first round bounds itself: per region (one lane of a split) up to k' rows of
+        // the split's first tile and a few after it, twice over (a split that starts ahead
+        // of the others of its query tile scans a few tiles before their minima arrive),
+        // and at least 2 k' + 1 (an overflowing region holds enough to tighten from)
+        j.bound_only = collect_bound_only(n_eff, nq, j.kk, f->dp, cus);
+        if (j.bound_only) f->last_path = PX_PATH_COLLECT_BOUNDED;
+        int64_t splits = 1, rps = 64;
+        collect_splits(n_eff, nq, cus, &splits, &rps);
+        j.bound_expect = (double)(2 * splits) *
+                         (double)std::max<int64_t>(2 * (j.kk + 32), 2 * j.kk + 1) / 3.0;
+    }
     j.sel.rowidx = rowidx;
     j.sel.k = (int)k;
     j.sel.metric = f->metric;
@@ -825,11 +898,13 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     const int* rowidx = nullptr;
     if (d_mask) PX_TRY(compact_mask(ws, d_mask, f->d_rows, s, &n_eff, &rowidx));
     f->last_rounds = 0;
+    f->last_path = PX_PATH_LISTS;
     // lists for batches of moderate size and small k; the collect path for large k, for
     // larger k on large batches, and for the few-query batches the vector-ALU scan serves
-    const bool collect = k + kReRankMargin > px::kMaxList ||
-                         (k >= collect_from_k() && nq >= kCollectMinQueries) ||
-                         vec_collect(nq, f->dp);
+    const bool collect =
+        k + kReRankMargin > px::kMaxList ||
+        (k >= collect_from_k() && nq >= kCollectMinQueries) || vec_collect(nq, f->dp) ||
+        collect_bound_only(n_eff, nq, k + kReRankMargin, f->dp, std::max(f->dev.cus, 1));
     if (collect && n_eff > 0)
         return flat_run_collect(f, d_q, nq, k, n_eff, rowidx, d_ids, d_out, raw_keys);
 
@@ -1398,6 +1473,12 @@ int px_flat_last_timing(const px_flat* f, float* scan_ms, float* total_ms, int* 
 int px_flat_last_rounds(const px_flat* f, int* rounds) {
     if (!f) return fail(PX_ERR_ARG, "null index handle");
     if (rounds) *rounds = f->last_rounds;
+    return PX_OK;
+}
+
+int px_flat_last_path(const px_flat* f, int* path) {
+    if (!f) return fail(PX_ERR_ARG, "null index handle");
+    if (path) *path = f->last_path;
     return PX_OK;
 }
 

@@ -28,13 +28,16 @@ struct FlatScanArgs {
     int64_t rows_per_split;
     int dp;
     int nq;
-    int kl;                // list length k' (<= kp)
+    int kl;                // list length k' (<= kp); collect mode with gbest: rank of the bound
     int splits;
     int metric;            // 0 = L2, 1 = inner product
     float* part_keys;      // [nq][splits][kl]
     int* part_ids;         // compacted positions (row ids when unfiltered)
     int* gtau;             // [nq] shared per-query bound, total-order ints; starts at +inf
-    int* gbest;            // [nq][32] per-split published list keys, total-order ints; +inf
+    int* gbest;            // [nq][32] per-split published list keys, total-order ints; +inf.
+                           // Collect mode: optional (kl <= min(splits, 32)); each split
+                           // publishes its smallest key and rows above the kl-th smallest
+                           // published key are not appended
     // Collect mode (launch_flat_collect): no lists; every row whose (key, position) is at or
     // below its query's threshold is appended to the region of (query slot, split).
     const int* qlist;      // optional: query index of each of the nq slots
@@ -97,6 +100,10 @@ struct CollectSelectArgs {
     int kk;                  // candidates re-ranked exactly (k + margin)
     int k;
     int metric;
+    // optional [queries][32]: the scan's shared-bound slots (FlatScanArgs::gbest). The
+    // kk-th smallest slot bounds the best kk, and every row at or below it was collected,
+    // so a finishing query sorts only the candidates at or below it.
+    const int* gbest;
     const float* corpus;     // nullptr: keys are exact already (PQ), no re-rank
     const float* queries;
     int dim, dp;

@@ -266,3 +266,50 @@ print("ok", r.value)
                          timeout=240, env=env)
     assert out.returncode == 0, out.stdout[-2000:] + out.stderr[-2000:]
     assert out.stdout.strip().startswith("ok")
+
+
+
+def _path(idx) -> str:
+    return idx._last_timing()["path"]
+
+
+def test_bound_only_first_round(gpu):
+    # k' <= 24 on batches of 256+ queries of at most 128 dims over at most 48 splits (here
+    # 40,000 rows and 2,048 queries: 32 splits): the first round takes no sample; each
+    # split's first tile and the splits' shared bound decide what is collected
+    data = datagen.sift_like(40_000, 64, 63)
+    q = datagen.sift_like(2048, 64, 64)
+    mask = datagen.mask(40_000, 0.5, 65)
+    for k in (1, 10, 16):
+        for m in (None, mask):
+            idx, ids, d = _search(data, q, k, oracle.L2, m)
+            assert _path(idx) == "collect-bounded", k
+            o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2, mask=m)
+            assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d), k
+    # k' = 25 is past the rule: sampled thresholds (and the shared bound) instead
+    idx, ids, d = _search(data, q, 17, oracle.L2)
+    assert _path(idx) == "collect-sampled"
+    o_ids, o_d, _ = oracle.flat_search(data, q, 17, oracle.L2)
+    assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
+    gd = datagen.unit_gaussian(40_000, 96, 66)
+    gq = datagen.unit_gaussian(2048, 96, 67)
+    _check(gd, gq, 12, oracle.IP, mask=datagen.mask(40_000, 0.6, 68))
+
+
+def test_bound_only_overflow_and_ties(gpu):
+    # Keys fall along the rows (each tile nearer than the last), so the shared bound
+    # prunes little in the last splits, their regions overflow and retry rounds tighten the
+    # threshold from the candidates; only 512 distinct keys, so ties at the bound decide
+    # by row.
+    n = 40_000
+    data = np.zeros((n, 16), dtype=np.float32)
+    data[:, 0] = 255 - (np.arange(n) * 255) // n
+    data[:, 3] = np.arange(n) % 2
+    rng = np.random.default_rng(69)
+    q = np.zeros((2048, 16), dtype=np.float32)
+    q[:, 0] = rng.integers(0, 4, size=2048)
+    idx, ids, d = _search(data, q, 16, oracle.L2)
+    assert _path(idx) == "collect-bounded"
+    o_ids, o_d, _ = oracle.flat_search(data, q, 16, oracle.L2)
+    assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
+    assert _rounds(idx) >= 2
