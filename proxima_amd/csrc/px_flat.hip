@@ -288,8 +288,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     // the query's best kl. A row passes when it is at or below both the threshold and
     // gbound; ctest = min(cthr, gbound) pre-screens a tile's keys.
     // The first tile of a split also bounds itself: its kl-th smallest key has kl of the
-    // split's rows at or below it (so a first round needs no threshold), and the
-    // first refresh comes right after the first tile's publication.
+    // split's rows at or below it (so a query needs no threshold), and the first refresh
+    // comes right after the first tile's publication.
     const bool dyn = COLLECT && a.gbest != nullptr && !a.dense;
     int cpub = kTotalKeyInf;
     float ctest = -kInf;
@@ -579,7 +579,10 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                             vmin = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? fminf(vmin, key[x])
                                                                              : vmin;
                     }
-                    if (t0 == row0) gbound = first_tile_kth(key, rem, qvalid, a.kl);
+                    // (only where some query of the wave has no threshold: a sampled one
+                    // already bounds the first tile far below its k'-th key)
+                    if (t0 == row0 && __ballot(qvalid && cthr == kInf))
+                        gbound = first_tile_kth(key, rem, qvalid, a.kl);
                     const int tk = total_key(vmin);
                     if (qvalid && tk < cpub) {
                         atomicMin(gbest + (split & 31), tk);

@@ -663,6 +663,11 @@ bool collect_shared_bound(int64_t splits, int64_t kk) {
 //     chunks: the keys are tested in the epilogue, not during the next tile's MFMAs)
 // so: one 128-dim chunk, at most 48 splits, k' <= 24 (the bound is the k'-th smallest of
 // at most 32 split minima; at k' = 32 it is their largest and prunes little).
+// Moderate k' on corpora short of 16 threshold samples' worth of rows stays on the lists:
+// there the sample scan alone adds S / n_eff of a scan (100k x 384 IP, 1,000 queries,
+// k = 16: lists 0.97 ms, sampled collect 1.08 ms; k = 32: 1.03 against 1.07).
+bool lists_beat_sample(int64_t n_eff, int64_t kk) { return kk <= 56 && n_eff < 16 * 16384; }
+
 bool collect_bound_only(int64_t n_eff, int64_t nq, int64_t kk, int64_t dp, int cus) {
     if (dp > 128 || kk > 24 || nq < kCollectMinQueries || vec_collect(nq, dp)) return false;
     int64_t splits = 1, rps = 64;
@@ -834,9 +839,11 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.cand_pos = ws.cand_p.as<int>();
         a.cand_count = ws.cand_n.as<int>();
         a.cap = (int)*cap;
-        // the shared bound needs k' publishing slots (one per split, at most 32)
+        // the shared bound needs k' publishing slots (one per split, at most 32); it is
+        // applied where the first round has no sampled thresholds (with them it measured
+        // no faster on 1M x 128 and 1M x 384, and 11% slower on 100k x 384 at k = 16)
         j.sel_gbest = nullptr;
-        if (collect_shared_bound(splits, j.kk)) {
+        if (j.bound_only && collect_shared_bound(splits, j.kk)) {
             PX_TRY(ws.gbest.reserve(sizeof(int) * j.nq * 32));
             PX_HIP(px::launch_fill_int(ws.gbest.as<int>(), j.nq * 32, px::kTotalKeyInf, s));
             a.gbest = ws.gbest.as<int>();
@@ -901,10 +908,11 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     f->last_path = PX_PATH_LISTS;
     // lists for batches of moderate size and small k; the collect path for large k, for
     // larger k on large batches, and for the few-query batches the vector-ALU scan serves
+    const int64_t kk = k + kReRankMargin;
     const bool collect =
-        k + kReRankMargin > px::kMaxList ||
-        (k >= collect_from_k() && nq >= kCollectMinQueries) || vec_collect(nq, f->dp) ||
-        collect_bound_only(n_eff, nq, k + kReRankMargin, f->dp, std::max(f->dev.cus, 1));
+        kk > px::kMaxList ||
+        (k >= collect_from_k() && nq >= kCollectMinQueries && !lists_beat_sample(n_eff, kk)) ||
+        vec_collect(nq, f->dp) || collect_bound_only(n_eff, nq, kk, f->dp, std::max(f->dev.cus, 1));
     if (collect && n_eff > 0)
         return flat_run_collect(f, d_q, nq, k, n_eff, rowidx, d_ids, d_out, raw_keys);
 

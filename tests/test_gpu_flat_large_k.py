@@ -2,11 +2,14 @@
 
 The reference's FlatIndex takes any k (flat.rs:106-148 keeps a heap of k); the library
 serves k up to PX_MAX_K. For k + 8 > 128, and for k >= 16 in batches of at least 256
-queries, it samples a strided subset of the rows for per-query thresholds, appends every
-row at or below them in one collect scan, and finishes each query whose candidate set is
-complete and large enough; the others go round again with a looser or tighter threshold. These tests compare with the oracle at the
-parity rule, bit for bit on integer-valued data (exact in fp32), and force each kind of
-extra round with data laid out against the sample.
+queries (k + 8 > 56 below 262,144 rows), it samples a strided subset of the rows for
+per-query thresholds, appends every row at or below them in one collect scan, and
+finishes each query whose candidate set is complete and large enough; the others go round
+again with a looser or tighter threshold. Batches of at least 256 queries with k + 8 <= 24
+on rows of at most 128 padded dims over at most 48 splits take no sample: their first
+round is bounded by the splits' shared bound alone. These tests compare with the oracle at
+the parity rule, bit for bit on integer-valued data (exact in fp32), and force each kind
+of extra round with data laid out against the sample or the bound.
 """
 import ctypes
 
@@ -84,10 +87,12 @@ def test_first_k_past_the_lists_and_last_list_k(gpu):
 
 
 def test_batch_routing_boundary(gpu):
-    # batches of >= 256 queries switch from the per-split lists to the collect path at k = 16
+    # batches of >= 256 queries switch from the per-split lists to the collect path at k = 16,
+    # except that k' = k + 8 <= 56 stays on the lists below 262,144 rows (16 threshold
+    # samples' worth)
     data = datagen.sift_like(30_000, 64, 49)
     q = datagen.sift_like(300, 64, 50)
-    for k, collected in ((15, False), (16, True), (100, True)):
+    for k, collected in ((15, False), (16, False), (48, False), (49, True), (100, True)):
         idx, ids, d = _search(data, q, k, oracle.L2)
         o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2)
         assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d), k
@@ -224,10 +229,11 @@ def test_k_limit(gpu):
 
 
 def test_more_queries_than_one_collect_batch(gpu):
-    # 17,000 queries: two collect batches of at most 16,384
+    # 17,000 queries: two collect batches of at most 16,384 (k' = 68 > 56: collected on
+    # 2,000 rows)
     data = datagen.sift_like(2000, 16, 58)
     q = datagen.sift_like(17_000, 16, 59)
-    rounds = _check(data, q, 20, oracle.L2, exact=True)
+    rounds = _check(data, q, 60, oracle.L2, exact=True)
     assert rounds >= 1
 
 
@@ -286,9 +292,10 @@ def test_bound_only_first_round(gpu):
             assert _path(idx) == "collect-bounded", k
             o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2, mask=m)
             assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d), k
-    # k' = 25 is past the rule: sampled thresholds (and the shared bound) instead
+    # k' = 25 is past the rule, and 40,000 rows are too few for a threshold sample to pay:
+    # the per-split lists
     idx, ids, d = _search(data, q, 17, oracle.L2)
-    assert _path(idx) == "collect-sampled"
+    assert _path(idx) == "lists"
     o_ids, o_d, _ = oracle.flat_search(data, q, 17, oracle.L2)
     assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
     gd = datagen.unit_gaussian(40_000, 96, 66)
