@@ -290,7 +290,9 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     // The first tile of a split also bounds itself: its kl-th smallest key has kl of the
     // split's rows at or below it (so a query needs no threshold), and the first refresh
     // comes right after the first tile's publication.
-    const bool dyn = COLLECT && a.gbest != nullptr && !a.dense;
+    // (one query chunk and no filter only: the host applies it to unfiltered searches of
+    // rows of at most 128 padded dims)
+    const bool dyn = COLLECT && !MULTI && !FILT && a.gbest != nullptr && !a.dense;
     int cpub = kTotalKeyInf;
     float ctest = -kInf;
     if (dyn) next_refresh = 0;

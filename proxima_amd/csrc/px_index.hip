@@ -651,25 +651,28 @@ bool collect_shared_bound(int64_t splits, int64_t kk) {
     return shared_collect_bound() && std::min<int64_t>(splits, 32) >= kk;
 }
 
+// Moderate k' on corpora short of 16 threshold samples' worth of rows stays on the lists:
+// there the sample scan alone adds S / n_eff of a scan (100k x 384 IP, 1,000 queries,
+// k = 16: lists 0.97 ms, sampled collect 1.08 ms; k = 32: 1.03 against 1.07).
+bool lists_beat_sample(int64_t n_eff, int64_t kk) { return kk <= 56 && n_eff < 16 * 16384; }
+
 // Whether a collect batch of nq query slots runs its first round on the shared bound alone
 // (no sample, no ladder). Measured on one MI355X against the per-split lists and the
 // sampled threshold (ms per batch of device-resident queries):
-//   1M x 128 SIFT-like L2, 10,000 queries: k = 10: 22.4 (lists 23.5); k = 16: 23.2 (lists
+//   1M x 128 SIFT-like L2, 10,000 queries: k = 10: 22.2 (lists 23.5); k = 16: 22.6 (lists
 //     24.7, sampled 24.4); k = 24 (k' = 32): 25.8 and a second round (sampled 24.5)
 //   300k x 128, 10,000 queries, k = 10: 7.6 (lists 8.3)
 //   1M x 128, 2,000 queries (96 splits), k = 10: 5.1 (lists 5.0): every split's first
 //     tile adds up to k' candidates a query
 //   100k / 1M x 384 IP, 1,000-4,000 queries, k = 10: 1-2% behind the lists (several query
 //     chunks: the keys are tested in the epilogue, not during the next tile's MFMAs)
-// so: one 128-dim chunk, at most 48 splits, k' <= 24 (the bound is the k'-th smallest of
-// at most 32 split minima; at k' = 32 it is their largest and prunes little).
-// Moderate k' on corpora short of 16 threshold samples' worth of rows stays on the lists:
-// there the sample scan alone adds S / n_eff of a scan (100k x 384 IP, 1,000 queries,
-// k = 16: lists 0.97 ms, sampled collect 1.08 ms; k = 32: 1.03 against 1.07).
-bool lists_beat_sample(int64_t n_eff, int64_t kk) { return kk <= 56 && n_eff < 16 * 16384; }
-
-bool collect_bound_only(int64_t n_eff, int64_t nq, int64_t kk, int64_t dp, int cus) {
-    if (dp > 128 || kk > 24 || nq < kCollectMinQueries || vec_collect(nq, dp)) return false;
+//   1M x 128 with a 50% / 10% filter, k = 10: 13.2 / 3.7 (lists 13.1 / 3.6)
+// so: unfiltered, one 128-dim chunk, at most 48 splits, k' <= 24 (the bound is the k'-th
+// smallest of at most 32 split minima; at k' = 32 it is their largest and prunes little).
+bool collect_bound_only(int64_t n_eff, int64_t nq, int64_t kk, int64_t dp, int cus,
+                        bool filtered) {
+    if (filtered || dp > 128 || kk > 24 || nq < kCollectMinQueries || vec_collect(nq, dp))
+        return false;
     int64_t splits = 1, rps = 64;
     collect_splits(n_eff, std::min(nq, kCollectBatch), cus, &splits, &rps);
     return splits <= 48 && collect_shared_bound(splits, kk);
@@ -862,7 +865,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         // the split's first tile and a few after it, twice over (a split that starts ahead
         // of the others of its query tile scans a few tiles before their minima arrive),
         // and at least 2 k' + 1 (an overflowing region holds enough to tighten from)
-        j.bound_only = collect_bound_only(n_eff, nq, j.kk, f->dp, cus);
+        j.bound_only = collect_bound_only(n_eff, nq, j.kk, f->dp, cus, rowidx != nullptr);
         if (j.bound_only) f->last_path = PX_PATH_COLLECT_BOUNDED;
         int64_t splits = 1, rps = 64;
         collect_splits(n_eff, nq, cus, &splits, &rps);
@@ -912,7 +915,8 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     const bool collect =
         kk > px::kMaxList ||
         (k >= collect_from_k() && nq >= kCollectMinQueries && !lists_beat_sample(n_eff, kk)) ||
-        vec_collect(nq, f->dp) || collect_bound_only(n_eff, nq, kk, f->dp, std::max(f->dev.cus, 1));
+        vec_collect(nq, f->dp) ||
+        collect_bound_only(n_eff, nq, kk, f->dp, std::max(f->dev.cus, 1), rowidx != nullptr);
     if (collect && n_eff > 0)
         return flat_run_collect(f, d_q, nq, k, n_eff, rowidx, d_ids, d_out, raw_keys);
 

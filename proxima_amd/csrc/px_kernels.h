@@ -35,9 +35,9 @@ struct FlatScanArgs {
     int* part_ids;         // compacted positions (row ids when unfiltered)
     int* gtau;             // [nq] shared per-query bound, total-order ints; starts at +inf
     int* gbest;            // [nq][32] per-split published list keys, total-order ints; +inf.
-                           // Collect mode: optional (kl <= min(splits, 32)); each split
-                           // publishes its smallest key and rows above the kl-th smallest
-                           // published key are not appended
+                           // Collect mode: optional (kl <= min(splits, 32), one 128-dim
+                           // chunk, no rowidx); each split publishes its smallest key and
+                           // rows above the kl-th smallest published key are not appended
     // Collect mode (launch_flat_collect): no lists; every row whose (key, position) is at or
     // below its query's threshold is appended to the region of (query slot, split).
     const int* qlist;      // optional: query index of each of the nq slots
