@@ -853,6 +853,15 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             a.kl = (int)j.kk;
             j.sel_gbest = a.gbest;
         }
+        // The stream is drained before the scan is launched. Launched right behind the small
+        // kernels before it (fills, the ladder), a collect scan on this box ran slow in one
+        // search of a handful, at the same search every time: 1M x 128, 10,000 queries,
+        // k = 10 bounded: the second search, scan 28 ms (its shared bound lost for most
+        // queries, ~60% of them a second round), 43 ms against 22.3; k = 50 sampled: the
+        // fourth, 31 ms against 24.6. With the host wait every search ran at the steady time
+        // (a slot fill with atomics, or slots that need no fill at all, did not help); the
+        // wait costs nothing measurable at these sizes.
+        PX_HIP(hipStreamSynchronize(s));
         PX_HIP(px::launch_flat_collect(a, s));
         if (round == 0) {
             f->timing.splits = (int)splits;

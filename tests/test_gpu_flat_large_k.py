@@ -321,3 +321,24 @@ def test_bound_only_overflow_and_ties(gpu):
     o_ids, o_d, _ = oracle.flat_search(data, q, 16, oracle.L2)
     assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
     assert _rounds(idx) >= 2
+
+
+def test_bound_only_consecutive_searches(gpu):
+    # The shared-bound slots are not reset between searches: each launch takes a new epoch
+    # and slots of earlier epochs read as +inf. Five searches in a row on one handle, the
+    # query sets alternating (a stale slot of the other set would drop true neighbours),
+    # each exact.
+    data = datagen.sift_like(40_000, 64, 70)
+    qa = datagen.sift_like(2048, 64, 71)
+    qb = datagen.sift_like(2048, 64, 72) // 4
+    idx = FlatIndex(64, Metric.L2)
+    idx.add(data)
+    ref = {}
+    for name, q in (("a", qa), ("b", qb)):
+        ref[name] = oracle.flat_search(data, q, 10, oracle.L2)[:2]
+    for name in "abbab":
+        q = qa if name == "a" else qb
+        print(f"case consecutive search {name}", flush=True)
+        ids, d = idx.search_batch(q, k=10)
+        assert _path(idx) == "collect-bounded"
+        assert np.array_equal(ids, ref[name][0]) and np.array_equal(d, ref[name][1]), name
