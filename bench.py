@@ -213,7 +213,10 @@ def bench_flat(args, dev):
                    "n_eff": n_eff, "queries_resident_in_hbm": True},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
-                     "traffic": read_traffic("flat_scan_kernel_l2_1Mx128_q10k_k10.md", headline),
+                     "traffic": read_traffic(
+                         {"lists": "flat_scan_kernel_l2_1Mx128_q10k_k10.md",
+                          "collect-bounded": "flat_collect_scan_bounded_l2_1Mx128_q10k_k10.md"}
+                         .get(info["path"], ""), headline),
                      "kernel": {"lists": "flat_scan_kernel (per-split lists)",
                                 "collect-sampled": "flat_scan_kernel (threshold-collect: sample "
                                                    "scan, ladder and collect scan)",
