@@ -38,7 +38,9 @@ extern "C" {
 #define PX_ERR_UNTRAINED (-6)  /* PQ index used before train (crates/py/src/lib.rs:492-504) */
 #define PX_ERR_DEVICE (-7)     /* no usable gfx950 device */
 
-/* Largest k a search accepts. */
+/* Largest k of the reference's GPU seam (knn_gpu_search). px_flat_search* and
+ * px_pq_search* take any k >= 0, as the reference's FlatIndex and PqIndex do
+ * (flat.rs:106-148, pq.rs:299-347): past PX_MAX_K every key is computed and sorted. */
 #define PX_MAX_K 4096
 
 /* Message for the calling thread's last non-zero status (empty string if none). */
@@ -171,11 +173,13 @@ int px_flat_last_rounds(const px_flat* idx, int* rounds);
  * PX_PATH_COLLECT_SAMPLED (threshold-collect whose first round takes its thresholds from a
  * strided row sample), PX_PATH_COLLECT_BOUNDED (threshold-collect whose first round is
  * bounded by the splits' shared bound alone, no sample), PX_PATH_VECTOR (the vector-ALU
- * collect scan of a few queries). Diagnostic; no counterpart in the reference. */
+ * collect scan of a few queries), PX_PATH_FULL_SORT (k past PX_MAX_K). Diagnostic; no
+ * counterpart in the reference. */
 #define PX_PATH_LISTS 0
 #define PX_PATH_COLLECT_SAMPLED 1
 #define PX_PATH_COLLECT_BOUNDED 2
 #define PX_PATH_VECTOR 3
+#define PX_PATH_FULL_SORT 4 /* k past PX_MAX_K: every key computed and sorted */
 int px_flat_last_path(const px_flat* idx, int* path);
 /* The same for PqIndex searches (k <= 128: per-wave lists; above: threshold-collect). */
 int px_pq_last_rounds(const px_pq* idx, int* rounds);

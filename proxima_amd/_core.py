@@ -276,7 +276,8 @@ class FlatIndex:
         _check(self._lib.px_flat_last_path(self._h, ctypes.byref(path)))
         return {"scan_ms": scan.value, "total_ms": total.value, "splits": splits.value,
                 "blocks": blocks.value, "collect_rounds": rounds.value,
-                "path": ("lists", "collect-sampled", "collect-bounded", "vector")[path.value]}
+                "path": ("lists", "collect-sampled", "collect-bounded", "vector",
+                         "full-sort")[path.value]}
 
 
 class PqIndex:

@@ -123,6 +123,7 @@ struct Workspace {
     // collect path (k' past the lists)
     DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
     DevBuf qraw;             // host-path queries before padding to dp
+    DevBuf sort_scratch;     // k past PX_MAX_K: sort keys, positions, radix-sort storage
     int* h_count = nullptr;  // pinned
     int* h_status = nullptr; // pinned, h_status_cap ints
     int64_t h_status_cap = 0;
@@ -158,7 +159,7 @@ struct Workspace {
     void release() {
         for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids,
                           &out_d, &gtau, &gbest, &thr_k, &thr_p, &lad_k, &lad_p, &rung, &status,
-                          &cand_k, &cand_p, &cand_n, &samp_row, &qlist})
+                          &cand_k, &cand_p, &cand_n, &samp_row, &qlist, &sort_scratch})
             b->release();
         if (h_count) (void)hipHostFree(h_count);
         h_count = nullptr;
@@ -894,6 +895,41 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     return run_collect(j);
 }
 
+// k past PX_MAX_K (px_sort.hip): every key of a chunk of queries in the reference's
+// arithmetic, one stable radix sort by (query, key), the first k of each query finished and
+// padded. Chunks of queries whose keys and sort buffers fit collect_bytes().
+int run_full_sort(Workspace& ws, hipStream_t s, Timing& timing, int64_t nq, int64_t k,
+                  int64_t n_eff, const int* rowidx, int metric, int raw_keys,
+                  const std::function<int(int64_t q0, int qc, float* keys)>& keys_of,
+                  int64_t* d_ids, float* d_out) {
+    PX_TRY(timing.ensure());
+    if (timing.enabled) PX_HIP(hipEventRecord(timing.ev[0], s));
+    const int64_t rows = std::max<int64_t>(n_eff, 1);
+    const int64_t per_query = rows * (4 + 2 * 8 + 2 * 4) + 4096;
+    const int64_t qc = std::max<int64_t>(
+        1, std::min<int64_t>({nq, collect_bytes() / per_query, 65535, INT32_MAX / rows}));
+    PX_TRY(ws.cand_k.reserve(sizeof(float) * (size_t)(qc * rows)));
+    const size_t sb = px::full_sort_scratch_bytes(n_eff, (int)qc);
+    PX_TRY(ws.sort_scratch.reserve(sb));
+    for (int64_t q0 = 0; q0 < nq; q0 += qc) {
+        const int c = (int)std::min(qc, nq - q0);
+        if (n_eff > 0) PX_TRY(keys_of(q0, c, ws.cand_k.as<float>()));
+        PX_HIP(px::launch_full_sort(ws.cand_k.as<float>(), n_eff, c, rowidx, k, metric, raw_keys,
+                                    ws.sort_scratch.p, ws.sort_scratch.cap, d_ids + q0 * k,
+                                    d_out + q0 * k, s));
+    }
+    if (timing.enabled) {
+        PX_HIP(hipEventRecord(timing.ev[1], s));
+        PX_HIP(hipEventRecord(timing.ev[2], s));
+    }
+    PX_HIP(hipStreamSynchronize(s));
+    if (timing.enabled) {
+        PX_HIP(hipEventElapsedTime(&timing.scan_ms, timing.ev[0], timing.ev[1]));
+        PX_HIP(hipEventElapsedTime(&timing.total_ms, timing.ev[0], timing.ev[2]));
+    }
+    return PX_OK;
+}
+
 // Batches of at most kCollectBatch queries, one after another.
 int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
                      const int* rowidx, int64_t* d_ids, float* d_out, int raw_keys) {
@@ -918,6 +954,17 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     if (d_mask) PX_TRY(compact_mask(ws, d_mask, f->d_rows, s, &n_eff, &rowidx));
     f->last_rounds = 0;
     f->last_path = PX_PATH_LISTS;
+    if (k > PX_MAX_K) {
+        f->last_path = PX_PATH_FULL_SORT;
+        return run_full_sort(ws, s, f->timing, nq, k, n_eff, rowidx, f->metric, raw_keys,
+                             [&](int64_t q0, int qc, float* keys) -> int {
+                                 PX_HIP(px::launch_flat_exact_keys(
+                                     f->d_x, d_q + q0 * f->dp, rowidx, n_eff, qc, (int)f->dim,
+                                     (int)f->dp, f->metric, keys, s));
+                                 return PX_OK;
+                             },
+                             d_ids, d_out);
+    }
     // lists for batches of moderate size and small k; the collect path for large k, for
     // larger k on large batches, and for the few-query batches the vector-ALU scan serves
     const int64_t kk = k + kReRankMargin;
@@ -1006,9 +1053,6 @@ int check_search_args(const void* idx, const void* queries, int64_t nq, int64_t 
     if (!idx) return fail(PX_ERR_ARG, "null index handle");
     if (nq < 0) return fail(PX_ERR_ARG, "nq must be >= 0");
     if (k < 0) return fail(PX_ERR_BAD_K, "k must be >= 0");
-    if (k > PX_MAX_K)
-        return fail(PX_ERR_BAD_K, "k=" + std::to_string(k) + " exceeds the GPU kernels' limit of " +
-                                      std::to_string(PX_MAX_K));
     if (k > 0 && nq > 0 && (!queries || !ids || !dists))
         return fail(PX_ERR_ARG, "null query or output pointer");
     return PX_OK;
@@ -1290,6 +1334,41 @@ int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_m
     if (d_mask) PX_TRY(compact_mask(ws, d_mask, p->d_rows, s, &n_eff, &rowidx));
 
     p->last_rounds = 0;
+    if (k > PX_MAX_K) {
+        const int waves = px::pq_lists_per_split();
+        const int64_t qpb = px::pq_queries_per_block((int)p->m, (int)p->ks);
+        const int cus = std::max(p->dev.cus, 1);
+        return run_full_sort(
+            ws, s, p->timing, nq, k, n_eff, rowidx, p->metric, 0,
+            [&](int64_t q0, int qc, float* keys) -> int {
+                // the ADC scan's dense mode: every key, in the reference's order
+                const int64_t groups = (qc + qpb - 1) / qpb;
+                int64_t splits = std::min<int64_t>(
+                    choose_splits(n_eff, groups, waves, 1, cus, 4096), px::kMaxCollectRegions / waves);
+                int64_t rps = (n_eff + splits - 1) / splits;
+                rps = std::max<int64_t>((rps + 255) / 256 * 256, 256);
+                splits = std::max<int64_t>(1, (n_eff + rps - 1) / rps);
+                px::PqScanArgs a{};
+                a.codes = p->d_codes;
+                a.codebooks = p->d_books;
+                a.queries = d_q + q0 * p->dim;
+                a.dim = (int)p->dim;
+                a.m = (int)p->m;
+                a.ks = (int)p->ks;
+                a.dsub = (int)p->dsub;
+                a.metric = p->metric;
+                a.rowidx = rowidx;
+                a.n_eff = n_eff;
+                a.rows_per_split = rps;
+                a.nq = qc;
+                a.splits = (int)splits;
+                a.cand_keys = keys;
+                a.dense = 1;
+                PX_HIP(px::launch_pq_collect(a, s));
+                return PX_OK;
+            },
+            d_ids, d_out);
+    }
     if (k > px::kMaxList && n_eff > 0) return pq_run_collect(p, d_q, nq, k, n_eff, rowidx, d_ids, d_out);
     const int kl = (int)std::min<int64_t>(k, px::kMaxList);
     const int lists = px::pq_lists_per_split();

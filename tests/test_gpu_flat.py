@@ -209,11 +209,16 @@ def test_empty_index_and_zero_k(gpu):
     assert ids.shape == (4, 0) and d.shape == (4, 0)
 
 
-def test_k_above_limit_raises(gpu):
+def test_k_above_seam_limit_searches(gpu):
+    # the reference's FlatIndex takes any k: every row in order, then padding
+    data = datagen.gaussian(300, 8, 1)
     idx = FlatIndex(8, Metric.L2)
-    idx.add(datagen.gaussian(300, 8, 1))
-    with pytest.raises(ValueError):
-        idx.search(np.zeros(8, dtype=np.float32), k=_lib.PX_MAX_K + 1)
+    idx.add(data)
+    q = np.zeros(8, dtype=np.float32)
+    ids, d = idx.search(q, k=_lib.PX_MAX_K + 1)
+    o_ids, o_d, _ = oracle.flat_search(data, q[None, :], _lib.PX_MAX_K + 1, oracle.L2)
+    assert np.array_equal(ids, o_ids[0]) and np.array_equal(d, o_d[0])
+    assert (ids[300:] == -1).all() and (d[300:] == np.finfo(np.float32).max).all()
 
 
 def test_knn_gpu_seam_raw_keys(gpu):

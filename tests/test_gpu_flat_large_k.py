@@ -219,13 +219,64 @@ def test_knn_seam_raw_keys(gpu):
 
 
 def test_k_limit(gpu):
+    # k = PX_MAX_K is the last k of the threshold-collect path; past it, every key is
+    # computed in the reference's arithmetic and sorted
     idx = FlatIndex(8, Metric.L2)
     idx.add(np.zeros((10, 8), dtype=np.float32))
-    with pytest.raises(ValueError):
-        idx.search(np.zeros(8, dtype=np.float32), k=_lib.PX_MAX_K + 1)
-    ids, d = idx.search(np.zeros(8, dtype=np.float32), k=_lib.PX_MAX_K)
-    assert ids.shape == (_lib.PX_MAX_K,)
-    assert np.array_equal(ids[:10], np.arange(10)) and (ids[10:] == -1).all()
+    for k in (_lib.PX_MAX_K, _lib.PX_MAX_K + 1):
+        ids, d = idx.search(np.zeros(8, dtype=np.float32), k=k)
+        assert ids.shape == (k,)
+        assert np.array_equal(ids[:10], np.arange(10)) and (ids[10:] == -1).all()
+        # (one query: the vector-ALU collect scan up to PX_MAX_K)
+        assert _path(idx) == ("vector" if k == _lib.PX_MAX_K else "full-sort")
+
+
+@pytest.mark.parametrize("metric", [oracle.L2, oracle.IP])
+def test_full_sort_past_max_k(gpu, metric):
+    # k past PX_MAX_K: the keys are the reference's own arithmetic, so ids and distances
+    # equal the oracle's bit for bit (ties to the lower row), filtered or not, k above the
+    # rows padded
+    data = datagen.gaussian(12_000, 40, 73)
+    q = datagen.gaussian(20, 40, 74)
+    mask = datagen.mask(12_000, 0.5, 75)
+    for k, m in ((5000, None), (5000, mask), (13_000, None)):
+        print(f"case full sort n=12000 k={k} metric={metric} mask={m is not None}", flush=True)
+        idx, ids, d = _search(data, q, k, metric, m)
+        assert _path(idx) == "full-sort"
+        o_ids, o_d, _ = oracle.flat_search(data, q, k, metric, mask=m)
+        assert np.array_equal(ids, o_ids)
+        assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+
+
+def test_full_sort_ties_and_chunks(gpu, tmp_path):
+    # 25 distinct rows repeated (exactly equal keys: the lower row first) with a 4 MB budget,
+    # so the queries are sorted in several chunks
+    import os
+    import subprocess
+    import sys
+    script = tmp_path / "run.py"
+    script.write_text(f"""
+import sys
+sys.path.insert(0, {repr(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))})
+import numpy as np
+import oracle
+from proxima_amd import FlatIndex, Metric, datagen
+base = datagen.sift_like(25, 32, 76)
+data = np.tile(base, (800, 1))
+q = datagen.sift_like(40, 32, 77)
+idx = FlatIndex(32, Metric.L2)
+idx.add(data)
+ids, d = idx.search_batch(q, k=6000)
+assert idx._last_timing()["path"] == "full-sort"
+o_ids, o_d, _ = oracle.flat_search(data, q, 6000, oracle.L2)
+assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
+print("ok")
+""")
+    env = dict(os.environ, PX_COLLECT_BYTES=str(4 << 20))
+    out = subprocess.run([sys.executable, str(script)], capture_output=True, text=True,
+                         timeout=240, env=env)
+    assert out.returncode == 0, out.stdout[-2000:] + out.stderr[-2000:]
+    assert out.stdout.strip().endswith("ok")
 
 
 def test_more_queries_than_one_collect_batch(gpu):

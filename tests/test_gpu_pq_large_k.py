@@ -72,6 +72,18 @@ def test_pq_k_above_rows_pads(gpu):
     _check(pq, q, 1500, oracle.L2)
 
 
+@pytest.mark.parametrize("metric", [oracle.L2, oracle.IP])
+def test_pq_full_sort_past_max_k(gpu, metric):
+    # k past PX_MAX_K (the reference's PqIndex takes any k): every ADC key, sorted; bit for
+    # bit, filtered or not, k above the rows padded
+    data = datagen.gaussian(9000, 32, 308)
+    q = datagen.gaussian(12, 32, 309)
+    pq = _index(data, 8, 8, metric)
+    _check(pq, q, 5000, metric)
+    _check(pq, q, 4500, metric, mask=datagen.mask(9000, 0.6, 310))
+    _check(pq, q, 9500, metric)
+
+
 def _stride(n_eff: int, k: int) -> int:
     """Stride of the threshold sample: S = min(n_eff, 16384, 80 * n_eff // k) rows at
     positions 0, stride, 2 * stride, ... with stride = n_eff // S (ADC keys are exact, so
