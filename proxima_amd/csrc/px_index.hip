@@ -1295,6 +1295,9 @@ int pq_run_collect_batch(px_pq* p, const float* d_q, int64_t nq, int64_t k, int6
         a.cand_pos = ws.cand_p.as<int>();
         a.cand_count = ws.cand_n.as<int>();
         a.cap = (int)*cap;
+        // drained first, as the flat collect scan (1M x 16-byte codes, 10,000 queries,
+        // k = 1000: the second search 34.1 ms against 31.1 without the wait)
+        PX_HIP(hipStreamSynchronize(s));
         PX_HIP(px::launch_pq_collect(a, s));
         if (round == 0) {
             p->timing.splits = (int)splits;
