@@ -1249,38 +1249,33 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
         __syncthreads();
         bound = s_kth;
     }
-    // candidate x comes from the region r with s_off[r] <= x < s_off[r + 1] (binary search),
-    // so that every thread's loads are independent of each other
-    auto region_of = [&](int x) {
-        int lo = 0, hi = a.regions - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (s_off[mid] <= x) lo = mid;
-            else hi = mid - 1;
-        }
-        return (int64_t)lo * a.cap + (x - s_off[lo]);
-    };
+    // Sixteen threads per region read its stored candidates in order (contiguous loads);
+    // with a bound, a position is read only for a key at or below it. The regions' LDS
+    // ranges (s_off) were clamped to lcap: entries past it are dropped (overflow).
     int avail = held;  // candidates sorted into sk/si
     if (bound != kTotalKeyInf) {
         if (t == 0) s_total = 0;
         __syncthreads();
-        for (int x = threadIdx.x; x < held; x += blockDim.x) {
-            const int64_t at = region_of(x);
-            const float kv = rk[at];
-            if (total_key(kv) <= bound) {
+    }
+    for (int r = t >> 4; r < a.regions; r += nt >> 4) {
+        const int n_r = s_off[r + 1] - s_off[r];
+        const float* rkr = rk + (int64_t)r * a.cap;
+        const int* rpr = rp + (int64_t)r * a.cap;
+        for (int c = t & 15; c < n_r; c += 16) {
+            const float kv = rkr[c];
+            if (bound == kTotalKeyInf) {
+                sk[s_off[r] + c] = kv;
+                si[s_off[r] + c] = rpr[c];
+            } else if (total_key(kv) <= bound) {
                 const int i = atomicAdd(&s_total, 1);
                 sk[i] = kv;
-                si[i] = rp[at];
+                si[i] = rpr[c];
             }
         }
+    }
+    if (bound != kTotalKeyInf) {
         __syncthreads();
         avail = s_total;
-    } else {
-        for (int x = threadIdx.x; x < held; x += blockDim.x) {
-            const int64_t at = region_of(x);
-            sk[x] = rk[at];
-            si[x] = rp[at];
-        }
     }
     int p = 1;
     while (p < avail) p <<= 1;

@@ -567,6 +567,10 @@ int run_collect(CollectJob& j) {
                                             2 * kk + 1))
                 lcap <<= 1;
             lcap = std::min<int64_t>(lcap, px::kMaxCollect);
+            // a round bounded by the shared bound holds a few hundred candidates a query and
+            // sorts only those below the final bound: 32 KB of LDS lets five selects share a
+            // CU where 64 KB let two (more than 4,096 candidates counts as an overflow)
+            if (j.sel_gbest) lcap = std::max<int64_t>(std::min<int64_t>(lcap, 4096), 2 * kk + 1);
 
             px::CollectSelectArgs c = j.sel;
             c.cand_keys = ws.cand_k.as<float>();
