@@ -524,8 +524,14 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             // Epilogue, branch-free: keys of the 32 rows this lane holds for query j.
             // L2 drops the per-query constant ||q||^2 (it does not change a query's order;
             // the merge re-ranks exactly), so key = ||x||^2 - 2 q.x; IP key = -q.x.
+            // (collect mode writes them straight into pkey, where the next tile's MFMA loop
+            // tests them: the previous tile's keys there have been tested already)
             const float* tn = tnorm[(s / nch) & 1];
-            float key[32];
+            float key_own[COLLECT ? 1 : 32];
+            auto& key = [&]() -> float(&)[32] {
+                if constexpr (COLLECT) return pkey;
+                else return key_own;
+            }();
             float kmin = kInf;
 #pragma unroll
             for (int rb = 0; rb < 2; ++rb) {
@@ -605,8 +611,6 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     }
                 }
                 ctest = fminf(cthr, gbound);
-#pragma unroll
-                for (int x = 0; x < 32; ++x) pkey[x] = key[x];
                 pt0 = (int)t0;
                 prem = rem;
                 pend = __ballot(kmin <= ctest) != 0;
