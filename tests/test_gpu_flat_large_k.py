@@ -1,15 +1,16 @@
-"""GPU parity of the threshold-collect path of FlatIndex searches.
+"""GPU parity of the threshold-collect and full-sort paths of FlatIndex searches.
 
-The reference's FlatIndex takes any k (flat.rs:106-148 keeps a heap of k); the library
-serves k up to PX_MAX_K. For k + 8 > 128, and for k >= 16 in batches of at least 256
-queries (k + 8 > 56 below 262,144 rows), it samples a strided subset of the rows for
-per-query thresholds, appends every row at or below them in one collect scan, and
-finishes each query whose candidate set is complete and large enough; the others go round
-again with a looser or tighter threshold. Unfiltered batches of at least 256 queries with
-k + 8 <= 24 on rows of at most 128 padded dims over at most 48 splits take no sample: their
-first round is bounded by the splits' shared bound alone. These tests compare with the
-oracle at the parity rule, bit for bit on integer-valued data (exact in fp32), and force each kind
-of extra round with data laid out against the sample or the bound.
+The reference's FlatIndex takes any k (flat.rs:106-148 keeps a heap of k); so does the
+library: up to PX_MAX_K on the fused scans, past it by sorting every key. For k + 8 > 128,
+and for k >= 16 in batches of at least 256 queries (k + 8 > 56 below 262,144 rows), it
+samples a strided subset of the rows for per-query thresholds, appends every row at or
+below them in one collect scan, and finishes each query whose candidate set is complete
+and large enough; the others go round again with a looser or tighter threshold.
+Unfiltered batches of at least 256 queries with k + 8 <= 24 on rows of at most 128 padded
+dims over at most 48 splits take no sample: their first round is bounded by the splits'
+shared bound alone. These tests compare with the oracle at the parity rule, bit for bit
+on integer-valued data (exact in fp32) and on the full-sort path, and force each kind of
+extra round with data laid out against the sample or the bound.
 """
 import ctypes
 
