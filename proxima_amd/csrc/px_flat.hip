@@ -554,13 +554,11 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             if constexpr (COLLECT) {
                 const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
                 if (a.dense) {
-                    // every key of the tile, +inf past the split's end: one 128-byte block
-                    // per lane, the wave's 64 blocks contiguous
+                    // every key of the tile, row-major by position (+inf past the split's
+                    // end), so that each query's keys are contiguous for the ladder: keys
+                    // 4 m .. 4 m + 3 of this lane are four consecutive rows
                     if (qvalid) {
-                        float* dst = a.cand_keys +
-                                     ((((int64_t)qt * WAVES + wave) * a.splits + split) *
-                                          (a.rows_per_split / kTileRows) + ti) * (64 * 32) +
-                                     lane * 32;
+                        float* dst = a.cand_keys + (int64_t)slot * a.dense_ld + t0;
 #pragma unroll
                         for (int m = 0; m < 8; ++m) {
                             float v[4];
@@ -569,7 +567,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                                 const int x = 4 * m + e;
                                 v[e] = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? key[x] : kInf;
                             }
-                            *reinterpret_cast<float4*>(dst + 4 * m) = make_float4(v[0], v[1], v[2], v[3]);
+                            const int lr = (m >> 2) * 32 + 8 * (m & 3) + 4 * h;
+                            *reinterpret_cast<float4*>(dst + lr) = make_float4(v[0], v[1], v[2], v[3]);
                         }
                     }
                 } else {
@@ -1337,10 +1336,10 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
 }
 
 // One workgroup of 1024 threads per query: its sampled keys in registers (up to 24 per
-// thread), three 8-bit radix passes over the top 24 bits of the order-preserving unsigned
-// form of the total-order key, both ranks at once (LDS histograms of 256 bins each); the
-// 8 bits below are taken as ones, so each threshold is the top of the bin that holds its
-// rank. Query q's keys sit in the 64-key blocks of wave group q / 32, lanes q % 32 and + 32.
+// thread, row q of the row-major keys), three 8-bit radix passes over the top 24 bits of
+// the order-preserving unsigned form of the total-order key, both ranks at once (LDS
+// histograms of 256 bins each); the 8 bits below are taken as ones, so each threshold is
+// the top of the bin that holds its rank.
 __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
     constexpr int kPer = kMaxLadderEntries / 1024;
     constexpr unsigned kNone = 0xffffffffu;
@@ -1348,20 +1347,12 @@ __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
     __shared__ unsigned s_prefix[kRungs], s_rank[kRungs];
     const int q = blockIdx.x;
     const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
-    const float* base = a.ld ? a.keys + (int64_t)q * a.ld
-                             : a.keys + (int64_t)(q >> 5) * a.blocks * (64 * 32) + (q & 31) * 32;
+    const float* base = a.keys + (int64_t)q * a.ld;
     unsigned u[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
         const int e = t + i * 1024;
-        const int b = e >> 6, hh = (e >> 5) & 1, x = e & 31;
-        // dense layout: block b holds sampled rows 64 b .. 64 b + 63 (splits are whole
-        // tiles); blocks past the sample's end were never written
-        const bool in = a.ld ? e < a.count
-                             : b * 64 + (x >> 4) * 32 + mfma_row(x & 15, hh) < a.count;
-        const float kv = !in   ? __int_as_float(0x7f800000)
-                         : a.ld ? base[e]
-                                : base[(int64_t)b * (64 * 32) + hh * (32 * 32) + x];
+        const float kv = e < a.count ? base[e] : __int_as_float(0x7f800000);
         // +inf (rows past a split's end) is left out
         u[i] = kv < __int_as_float(0x7f800000) ? (unsigned)total_key(kv) ^ 0x80000000u : kNone;
     }
@@ -1439,8 +1430,7 @@ __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
 
 hipError_t launch_ladder(const LadderArgs& a, hipStream_t s) {
     if (a.nq <= 0) return hipSuccess;
-    if ((a.ld ? (int64_t)a.count : (int64_t)a.blocks * 64) > kMaxLadderEntries)
-        return hipErrorInvalidValue;
+    if (a.count > kMaxLadderEntries || a.ld < a.count) return hipErrorInvalidValue;
     hipLaunchKernelGGL(flat_ladder_kernel, dim3((unsigned)a.nq), dim3(1024), 0, s, a);
     return hipGetLastError();
 }

@@ -736,16 +736,16 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             PX_HIP(px::launch_ladder(la, s));
             return PX_OK;
         }
-        // dense keys of the sample: [query tile][wave][split][tile][lane][32]
+        // dense keys of the sample, row-major [query][splits * rps] by position
         const int64_t groups = (nq + 255) / 256;
         int64_t splits = choose_flat_splits(S, groups, 1, cus, false);
         int64_t rps = (S + splits - 1) / splits;
         rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
         splits = std::max<int64_t>(1, (S + rps - 1) / rps);
-        const int64_t blocks = splits * (rps / 64);
-        if (blocks * 64 > px::kMaxLadderEntries)
+        const int64_t ld = splits * rps;
+        if (S > px::kMaxLadderEntries)
             return fail(PX_ERR_ARG, "internal: threshold sample too large for the ladder");
-        PX_TRY(ws.cand_k.reserve(sizeof(float) * groups * 256 * blocks * 64));
+        PX_TRY(ws.cand_k.reserve(sizeof(float) * nq * ld));
         px::FlatScanArgs a{};
         a.corpus = f->d_x;
         a.norms = f->d_norm;
@@ -759,10 +759,11 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.metric = f->metric;
         a.cand_keys = ws.cand_k.as<float>();
         a.dense = 1;
+        a.dense_ld = ld;
         PX_HIP(px::launch_flat_collect(a, s));
         px::LadderArgs la{};
         la.keys = a.cand_keys;
-        la.blocks = (int)blocks;
+        la.ld = ld;
         la.count = (int)S;
         la.nq = (int)nq;
         la.ranks[0] = r0;

@@ -47,10 +47,10 @@ struct FlatScanArgs {
     int* cand_pos;         // positions (indices into rowidx when filtered)
     int* cand_count;       // [nq slots][splits][2] rows that passed; more than cap = overflow
     int cap;
-    // dense != 0: no thresholds; every key goes to cand_keys as [query tile][wave][split]
-    // [tile of split][lane][32] (keys of rows past a split's end are +inf), cand_keys sized
-    // for whole query tiles of 32 * WAVES
+    // dense != 0: no thresholds; every key goes to cand_keys as [slot][dense_ld] by position
+    // (keys of rows past a split's end are +inf; dense_ld >= splits * rows_per_split)
     int dense;
+    int64_t dense_ld;
 };
 
 // Waves per workgroup and list capacity used for a list length kl.
@@ -117,10 +117,8 @@ hipError_t launch_collect_select(const CollectSelectArgs& a, int slots, hipStrea
 // of the 2^-24-wide bin, in total order, that holds the ranks[i]-th smallest), position
 // limit kIdNone (every row with that key passes); rung 0 also goes to thr, rung = 0.
 struct LadderArgs {
-    const float* keys;       // FlatScanArgs::dense layout of the sample scan (8 waves), or
-                             // row-major [nq][ld] when ld > 0
-    int blocks;              // dense layout: splits * tiles per split (64-key blocks a query)
-    int64_t ld;              // row-major layout: row pitch
+    const float* keys;       // row-major [nq][ld]: the sampled keys of each query
+    int64_t ld;              // row pitch (>= count)
     int count;               // sampled rows (keys a query)
     int nq;
     int ranks[kRungs];
