@@ -394,3 +394,25 @@ def test_bound_only_consecutive_searches(gpu):
         ids, d = idx.search_batch(q, k=10)
         assert _path(idx) == "collect-bounded"
         assert np.array_equal(ids, ref[name][0]) and np.array_equal(d, ref[name][1]), name
+
+
+@pytest.mark.parametrize("n,nq,dim,k,metric,dist", [
+    (40_000, 2048, 96, 16, oracle.IP, "unit"),
+    (25_000, 4096, 24, 5, oracle.L2, "gauss"),
+    (33_000, 1500, 128, 12, oracle.L2, "sift"),
+    (40_000, 2048, 8, 1, oracle.L2, "gauss"),
+    (33_000, 1500, 61, 10, oracle.IP, "gauss"),
+])
+def test_bound_only_shapes(gpu, n, nq, dim, k, metric, dist):
+    # shapes that take the bounded first round: 16-40 splits, odd and padded dims, k = 1-16
+    gen = {"unit": datagen.unit_gaussian, "gauss": datagen.gaussian, "sift": datagen.sift_like}[dist]
+    data = gen(n, dim, 80 + dim)
+    q = gen(nq, dim, 81 + dim)
+    idx, ids, d = _search(data, q, k, metric)
+    print(f"case bounded n={n} nq={nq} dim={dim} k={k} metric={metric} {dist}", flush=True)
+    assert _path(idx) == "collect-bounded"
+    o_ids, o_d, _ = oracle.flat_search(data, q, k, metric)
+    if dist == "sift":
+        assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
+    else:
+        assert_parity(ids, d, o_ids, o_d, _key_of(data, q, metric))
