@@ -416,3 +416,13 @@ def test_bound_only_shapes(gpu, n, nq, dim, k, metric, dist):
         assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
     else:
         assert_parity(ids, d, o_ids, o_d, _key_of(data, q, metric))
+
+
+def test_bound_only_batch_then_sampled_batch(gpu):
+    # 17,000 queries run as two collect batches: 16,384 over 16 splits take the bounded first
+    # round (k' = 16), the last 616 over 85 splits a sampled one; exact either way
+    data = datagen.sift_like(200_000, 16, 90)
+    q = datagen.sift_like(17_000, 16, 91)
+    print("case two batches, bounded then sampled", flush=True)
+    rounds = _check(data, q, 8, oracle.L2, exact=True)
+    assert rounds >= 1
