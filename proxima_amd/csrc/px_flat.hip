@@ -606,7 +606,10 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                             v[2 * u + 1] = (int)(w >> 32);
                         }
                         gbound = fminf(gbound, from_total_key(kth_smallest32(v, a.kl)));
-                        next_refresh = ti + max<int64_t>(1, ti >> 2);
+                        // sparser than the lists' schedule: each refresh waits for its loads
+                        // in the epilogue (t -> t + t/4: 21.73 ms a scan on 1M x 128, t + t/2:
+                        // 21.58, t -> 2t: 21.58)
+                        next_refresh = ti + max<int64_t>(1, ti >> 1);
                     }
                 }
                 ctest = fminf(cthr, gbound);

@@ -426,3 +426,16 @@ def test_bound_only_batch_then_sampled_batch(gpu):
     print("case two batches, bounded then sampled", flush=True)
     rounds = _check(data, q, 8, oracle.L2, exact=True)
     assert rounds >= 1
+
+
+def test_bound_only_ip_ties(gpu):
+    # inner product on 40 distinct unit rows repeated: exactly equal keys across every split;
+    # ties at the bound and in the result go to the lower row
+    base = datagen.unit_gaussian(40, 32, 92)
+    data = np.tile(base, (1000, 1))
+    q = datagen.unit_gaussian(2048, 32, 93)
+    idx, ids, d = _search(data, q, 12, oracle.IP)
+    print("case bounded IP ties", flush=True)
+    assert _path(idx) == "collect-bounded"
+    o_ids, o_d, _ = oracle.flat_search(data, q, 12, oracle.IP)
+    assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
