@@ -294,6 +294,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     // rows of at most 128 padded dims)
     const bool dyn = COLLECT && !MULTI && !FILT && a.gbest != nullptr && !a.dense;
     int cpub = kTotalKeyInf;
+    bool pub_now = false;  // publish cpub after this stage's commit
     float ctest = -kInf;
     if (dyn) next_refresh = 0;
     // list mode with one query chunk: the insertions of a tile's second row block run during
@@ -590,11 +591,11 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     // already bounds the first tile far below its k'-th key)
                     if (t0 == row0 && __ballot(qvalid && cthr == kInf))
                         gbound = first_tile_kth(key, rem, qvalid, a.kl);
+                    // published after the stage's commit: its waits then do not wait for the
+                    // atomic, which has the next tile's MFMAs to complete
                     const int tk = total_key(vmin);
-                    if (qvalid && tk < cpub) {
-                        atomicMin(gbest + (split & 31), tk);
-                        cpub = tk;
-                    }
+                    pub_now = qvalid && tk < cpub;
+                    cpub = pub_now ? tk : cpub;
                     if (ti == next_refresh) {
                         const long long* src = reinterpret_cast<const long long*>(gbest + h * 16);
                         int v[16];
@@ -712,6 +713,10 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         }
 
         commit(s + 1);
+        if (dyn && pub_now) {
+            atomicMin(gbest + (split & 31), cpub);
+            pub_now = false;
+        }
         __syncthreads();
     }
 
