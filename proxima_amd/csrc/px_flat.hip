@@ -646,7 +646,10 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     v[2 * u + 1] = (int)(w >> 32);
                 }
                 gbound = fminf(gbound, from_total_key(kth_smallest32(v, pub_rank)));
-                next_refresh = ti + max<int64_t>(1, ti >> 2);
+                // t -> t + t/2: each refresh stalls both waves of a SIMD for its loads (on
+                // 100k x 384 x 1,000 queries, 25 tiles a split: 0.81 -> 0.80 ms against
+                // t + t/4; t -> 2t loses 1% on 1M x 128 and on 128 queries at k = 100)
+                next_refresh = ti + max<int64_t>(1, ti >> 1);
             }
             const float thr =
                 qvalid ? fminf(fminf(tau_k, from_total_key(gt_raw)), gbound) : -kInf;
