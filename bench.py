@@ -366,7 +366,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this backend runs the whole search on a "
-              "single MI355X and has no multi-GPU path (sharding is described in DESIGN.md)",
+              "single MI355X and has no multi-GPU path (a sharded search would split the "
+              "corpus rows across GPUs and merge each shard's k best)",
               file=sys.stderr)
         sys.exit(2)
     if _lib.device_count() < 1:
