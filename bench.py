@@ -116,7 +116,7 @@ def read_traffic(name: str, default_workload: bool):
     """HBM bytes per launch (calibrated FETCH_SIZE + WRITE_SIZE) from the committed rocprofv3
     summary of this workload; None when the run is not that workload or no summary exists."""
     path = os.path.join(ROOT, "profiles", name)
-    if not default_workload or not os.path.exists(path):
+    if not name or not default_workload or not os.path.isfile(path):
         return None
     with open(path) as fh:
         for line in fh:
@@ -124,6 +124,14 @@ def read_traffic(name: str, default_workload: bool):
                 return int(float(line.split(":", 1)[1]))
     return None
 
+
+# rocprofv3 summaries whose calibrated FETCH_SIZE + WRITE_SIZE give `traffic`, by
+# (workload, rows, queries, k, path that ran); other runs report null
+TRAFFIC_PROFILES = {
+    (3, 1_000_000, 10_000, 10, "lists"): "flat_scan_kernel_l2_1Mx128_q10k_k10.md",
+    (3, 1_000_000, 10_000, 10, "collect-bounded"): "flat_collect_scan_bounded_l2_1Mx128_q10k_k10.md",
+    (2, 100_000, 1_000, 10, "lists"): "flat_scan_kernel_ip_100kx384_q1k_k10.md",
+}
 
 HEADLINE_METRIC = "exact kNN QPS (1M\u00d7128 fp32, k=10, 10k-query batch); % fp32 MFMA / HBM peak"
 
@@ -213,10 +221,8 @@ def bench_flat(args, dev):
                    "n_eff": n_eff, "queries_resident_in_hbm": True},
         "roofline": {"bound": "mfma", "achieved": achieved, "peak": FP32_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
-                     "traffic": read_traffic(
-                         {"lists": "flat_scan_kernel_l2_1Mx128_q10k_k10.md",
-                          "collect-bounded": "flat_collect_scan_bounded_l2_1Mx128_q10k_k10.md"}
-                         .get(info["path"], ""), headline),
+                     "traffic": read_traffic(TRAFFIC_PROFILES.get((c, n, nq, k, info["path"]), ""),
+                                             not args.sift),
                      "kernel": {"lists": "flat_scan_kernel (per-split lists)",
                                 "collect-sampled": "flat_scan_kernel (threshold-collect: sample "
                                                    "scan, ladder and collect scan)",
@@ -224,7 +230,9 @@ def bench_flat(args, dev):
                                                    "collect scan bounded by the splits' shared "
                                                    "bound, no sample)",
                                 "vector": "flat_vcollect_kernel (vector-ALU collect: sample "
-                                          "and collect scans)"}[info["path"]],
+                                          "and collect scans)",
+                                "full-sort": "flat_exact_keys_kernel (every key) and a radix sort "
+                                             "of them (k past the fused scans' limit)"}[info["path"]],
                      "collect_rounds": info["collect_rounds"],
                      "kernel_ms": float(np.mean(scan_ms)),
                      "algorithmic_flop_per_launch": flops},
