@@ -2,8 +2,12 @@
 
 Each summary that bench.py reads must exist, state the command that produced it and carry
 the `avg_kernel_ms:` and `hbm_bytes_per_launch:` lines; a run of another workload or path
-reports null rather than a figure measured on something else.
+reports null rather than a figure measured on something else. bench.py measures one GPU and
+refuses a multi-GPU launch with exit status 2 before it touches a device.
 """
+import os
+import subprocess
+import sys
 from pathlib import Path
 
 import pytest
@@ -34,3 +38,12 @@ def test_traffic_only_for_the_profiled_run():
     # the headline's sampled path and other workloads have no traffic summary
     assert (3, 1_000_000, 10_000, 10, "collect-sampled") not in bench.TRAFFIC_PROFILES
     assert (3, 1_000_000, 10_000, 100, "collect-sampled") not in bench.TRAFFIC_PROFILES
+
+
+@pytest.mark.parametrize("argv,env", [(["--gpus", "2"], {}), ([], {"WORLD_SIZE": "8"})])
+def test_bench_refuses_more_than_one_gpu(argv, env):
+    root = Path(bench.__file__).resolve().parent
+    run = subprocess.run([sys.executable, str(root / "bench.py"), *argv], capture_output=True,
+                         text=True, timeout=120, env={**os.environ, **env})
+    assert run.returncode == 2
+    assert "one GPU only" in run.stderr and run.stdout == ""
