@@ -656,10 +656,21 @@ bool collect_shared_bound(int64_t splits, int64_t kk) {
     return shared_collect_bound() && std::min<int64_t>(splits, 32) >= kk;
 }
 
-// Moderate k' on corpora short of 16 threshold samples' worth of rows stays on the lists:
-// there the sample scan alone adds S / n_eff of a scan (100k x 384 IP, 1,000 queries,
-// k = 16: lists 0.97 ms, sampled collect 1.08 ms; k = 32: 1.03 against 1.07).
-bool lists_beat_sample(int64_t n_eff, int64_t kk) { return kk <= 56 && n_eff < 16 * 16384; }
+// Moderate k' on short corpora stays on the lists, where the sample scan alone adds
+// S / n_eff of a scan. With several query chunks (dp > 128) the lists hold up to 16 threshold
+// samples' worth of rows (100k x 384 IP, 1,000 queries, k = 16: lists 0.97 ms, sampled
+// collect 1.08 ms; k = 32: 0.95 against 0.97). With one chunk the sampled collect scan
+// overtakes them far sooner (ms a search, lists against sampled collect, 1,000 queries,
+// N(0,1) IP and SIFT-like L2 alike): k = 16: 100k rows 0.44 against 0.44-0.46, 250k 0.84
+// against 0.79; k = 32: 20k 0.24 against 0.25, 50k 0.37 against 0.33, 100k 0.52 against
+// 0.44; k = 48: 20k 0.30 against 0.25 (4,000 queries: 0.72 against 0.76), 100k 0.61
+// against 0.45. The lists' cost grows with k' and the sample's does not: the crossover falls
+// near n_eff (k' - 16) = 1.04M rows (k' = 24: 130k rows, 40: 43k, 56: 26k).
+bool lists_beat_sample(int64_t n_eff, int64_t kk, int64_t dp) {
+    if (kk > 56) return false;
+    if (dp > 128) return n_eff < 16 * 16384;
+    return kk <= 16 || n_eff * (kk - 16) < 1040000;
+}
 
 // Whether a collect batch of nq query slots runs its first round on the shared bound alone
 // (no sample, no ladder). Measured on one MI355X against the per-split lists and the
@@ -975,7 +986,7 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     const int64_t kk = k + kReRankMargin;
     const bool collect =
         kk > px::kMaxList ||
-        (k >= collect_from_k() && nq >= kCollectMinQueries && !lists_beat_sample(n_eff, kk)) ||
+        (k >= collect_from_k() && nq >= kCollectMinQueries && !lists_beat_sample(n_eff, kk, f->dp)) ||
         vec_collect(nq, f->dp) ||
         collect_bound_only(n_eff, nq, kk, f->dp, std::max(f->dev.cus, 1), rowidx != nullptr);
     if (collect && n_eff > 0)

@@ -89,15 +89,29 @@ def test_first_k_past_the_lists_and_last_list_k(gpu):
 
 def test_batch_routing_boundary(gpu):
     # batches of >= 256 queries switch from the per-split lists to the collect path at k = 16,
-    # except that k' = k + 8 <= 56 stays on the lists below 262,144 rows (16 threshold
-    # samples' worth)
+    # except that with one 128-dim query chunk k' = k + 8 <= 56 stays on the lists while
+    # n_eff (k' - 16) < 1,040,000 (30,000 rows: k' <= 50)
     data = datagen.sift_like(30_000, 64, 49)
     q = datagen.sift_like(300, 64, 50)
-    for k, collected in ((15, False), (16, False), (48, False), (49, True), (100, True)):
+    for k, collected in ((15, False), (16, False), (42, False), (43, True), (48, True),
+                         (49, True), (100, True)):
         idx, ids, d = _search(data, q, k, oracle.L2)
         o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2)
         assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d), k
         assert (_rounds(idx) > 0) == collected, k
+
+
+@pytest.mark.parametrize("dim,k,collected", [(64, 17, False), (64, 33, False), (64, 34, True),
+                                             (64, 48, True), (200, 17, False), (200, 48, False)])
+def test_routing_by_rows_and_chunks(gpu, dim, k, collected):
+    # 40,000 rows: with one query chunk the lists keep k' while 40,000 (k' - 16) < 1,040,000
+    # (k' <= 41), with two chunks up to k' = 56
+    data = datagen.sift_like(40_000, dim, 61)
+    q = datagen.sift_like(300, dim, 62)
+    idx, ids, d = _search(data, q, k, oracle.L2)
+    o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2)
+    assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
+    assert (_rounds(idx) > 0) == collected
 
 
 @pytest.mark.parametrize("metric", [oracle.L2, oracle.IP])
