@@ -59,7 +59,8 @@ const char* px_version(void);
  * ---------------------------------------------------------------------------------- */
 typedef struct PxGpuIndex PxGpuIndex;
 
-/* knn.cu:123-141: copy n x dim row-major floats to the device; NULL on failure. */
+/* knn.cu:123-141: copy n x dim row-major floats to the device; NULL on failure. One device
+ * copy of the rows (and their squared norms) serves both metrics. */
 PxGpuIndex* knn_gpu_create(const float* base, int n, int dim);
 
 /* knn.cu:143-174: 0 ok, -1 bad k, >0 HIP error. Synchronous; outputs are host memory. */
@@ -94,7 +95,9 @@ int px_flat_search(const px_flat* idx, const float* queries, int64_t nq, int64_t
 /*
  * Same search with every pointer in device memory of the index's GPU (queries nq x dim,
  * mask px_flat_size() bytes or NULL, outputs nq * k). Synchronous. No host copies: the
- * form for callers that keep queries and results resident in HBM.
+ * form for callers that keep queries and results resident in HBM. The queries are checked
+ * on the device before any search kernel runs: NaN or infinite values return
+ * PX_ERR_NONFINITE, as the host form (flat.rs:114-117).
  */
 int px_flat_search_device(const px_flat* idx, const float* d_queries, int64_t nq, int64_t k,
                           const uint8_t* d_mask, int64_t* d_ids, float* d_dists);
@@ -133,7 +136,7 @@ int px_pq_get_codes(const px_pq* idx, int64_t first, int64_t n, uint8_t* out);
 /* PqIndex::search_batch{,_filtered}, pq.rs:349-396. Same contract as px_flat_search. */
 int px_pq_search(const px_pq* idx, const float* queries, int64_t nq, int64_t k,
                  const uint8_t* mask, int64_t* out_ids, float* out_dists);
-/* Device-pointer form, as px_flat_search_device. */
+/* Device-pointer form, as px_flat_search_device (queries checked on the device first). */
 int px_pq_search_device(const px_pq* idx, const float* d_queries, int64_t nq, int64_t k,
                         const uint8_t* d_mask, int64_t* d_ids, float* d_dists);
 

@@ -14,6 +14,8 @@
 
 #include <float.h>
 
+#include <algorithm>
+
 #include <type_traits>
 
 namespace px {
@@ -970,18 +972,18 @@ hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-__global__ void sample_rows_kernel(const int* rowidx, int64_t count, int64_t stride, int* row) {
+__global__ void sample_rows_kernel(const int* rowidx, int64_t count, int64_t n_eff, int* row) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= count) return;
-    const int64_t p = i * stride;
+    const int64_t p = i * n_eff / count;  // < n_eff; i * n_eff < 2^14 * 2^31
     row[i] = rowidx ? rowidx[p] : (int)p;
 }
 
-hipError_t launch_sample_rows(const int* rowidx, int64_t count, int64_t stride, int* row,
+hipError_t launch_sample_rows(const int* rowidx, int64_t count, int64_t n_eff, int* row,
                               hipStream_t s) {
     if (count <= 0) return hipSuccess;
     hipLaunchKernelGGL(sample_rows_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, s,
-                       rowidx, count, stride, row);
+                       rowidx, count, n_eff, row);
     return hipGetLastError();
 }
 
@@ -1502,6 +1504,23 @@ hipError_t launch_pad_rows(const float* src, int64_t rows, int dim, int dp, floa
     const int64_t blocks = (rows * dp + 255) / 256;
     hipLaunchKernelGGL(pad_rows_kernel, dim3((unsigned)blocks), dim3(256), 0, s, src, rows, dim,
                        dp, dst);
+    return hipGetLastError();
+}
+
+// *flag = 1 when any of count floats is NaN or infinite (exponent bits all ones), else 0.
+__global__ __launch_bounds__(256) void nonfinite_kernel(const float* x, int64_t count, int* flag) {
+    bool bad = false;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (int64_t)gridDim.x * blockDim.x)
+        bad |= (__float_as_uint(x[i]) & 0x7f800000u) == 0x7f800000u;
+    if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(flag, 1);
+}
+
+hipError_t launch_nonfinite_check(const float* x, int64_t count, int* flag, hipStream_t s) {
+    hipError_t e = launch_fill_int(flag, 1, 0, s);
+    if (e != hipSuccess || count <= 0) return e;
+    const int64_t blocks = std::min<int64_t>((count + 255) / 256, 2048);
+    hipLaunchKernelGGL(nonfinite_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, count, flag);
     return hipGetLastError();
 }
 

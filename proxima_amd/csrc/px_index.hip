@@ -221,6 +221,19 @@ int compact_mask(Workspace& ws, const uint8_t* d_mask, int64_t n, hipStream_t s,
     return PX_OK;
 }
 
+// Device queries (count floats) must be finite, as flat.rs:114-117 asserts of every query:
+// checked on the device, and the host waits for the answer before any search kernel runs.
+int check_device_finite(Workspace& ws, const float* d_x, int64_t count, hipStream_t s) {
+    PX_TRY(ws.count.reserve(sizeof(int)));
+    PX_TRY(ws.ensure_pinned());
+    PX_HIP(px::launch_nonfinite_check(d_x, count, ws.count.as<int>(), s));
+    PX_HIP(hipMemcpyAsync(ws.h_count, ws.count.p, sizeof(int), hipMemcpyDeviceToHost, s));
+    PX_HIP(hipStreamSynchronize(s));
+    if (*ws.h_count)
+        return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
+    return PX_OK;
+}
+
 // Number of corpus splits: enough workgroups to fill the GPU several times over, each
 // split at least min_rows long, and at most kMaxMerge candidates per query to merge.
 int choose_splits(int64_t n_eff, int64_t groups, int lists_per_split, int kl, int cus,
@@ -312,6 +325,8 @@ int choose_flat_splits(int64_t n_eff, int64_t groups, int kl, int cus, bool narr
 // ---------------------------------------------------------------------------------------
 struct px_flat {
     int metric = 0;
+    int smetric = 0;               // metric of the search in progress (set under mu): the
+                                   // index's own, or the one knn_gpu_search names per call
     int64_t dim = 0, dp = 0;
     int64_t n = 0;                 // rows held (device + pending)
     std::vector<float> pending;    // rows not yet mirrored, [rows][dim]
@@ -347,8 +362,7 @@ struct px_pq {
 };
 
 struct PxGpuIndex {
-    px_flat* flat[2] = {nullptr, nullptr};  // one handle per metric, sharing nothing
-    const float* base = nullptr;
+    px_flat* flat = nullptr;  // one corpus mirror (rows and squared norms) for both metrics
 };
 
 namespace {
@@ -458,7 +472,7 @@ int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int cus, ListPlan* out, in
 
 // The threshold-collect path (large k, and moderate k on large batches), shared by the
 // flat and PQ scans.
-//  1. Thresholds from a strided sample of S rows: an all-pass collect scan over the sample
+//  1. Thresholds from a sample of S rows spread evenly over the corpus: an all-pass collect scan over the sample
 //     and a radix select give each query the keys of (about) its r0-th and r1-th smallest
 //     sampled rows as a two-rung ladder. r0 is set so that the rows at or below it in the
 //     whole corpus are, with high probability, at least k' but not many more: about
@@ -498,8 +512,9 @@ struct CollectJob {
     int* last_rounds = nullptr;
     int64_t nq = 0, kk = 0, n_eff = 0;
     int cus = 1;
-    // keys of S rows sampled at the given stride -> ladder rungs r0, r1, thresholds, rung 0
-    std::function<int(int64_t S, int64_t stride, int r0, int r1)> sample;
+    // keys of S rows spread evenly over the n_eff positions (position floor(i n_eff / S))
+    // -> ladder rungs r0, r1, thresholds, rung 0
+    std::function<int(int64_t S, int r0, int r1)> sample;
     // collect scan over the first *slots query slots (qlist: their query indices, or null
     // for all); with a qlist it may take fewer slots so that the regions stay within
     // max_bytes, and returns how many it took, the regions per slot and their capacity
@@ -539,12 +554,12 @@ int run_collect(CollectJob& j) {
     } else {
         const int64_t S = std::max<int64_t>(
             1, std::min<int64_t>({n_eff, (int64_t)16384, 80 * n_eff / kk}));
-        const int64_t stride = n_eff / S;
         const double x = (double)kk * (double)S / (double)n_eff;
         const int r0 = (int)std::min<int64_t>(S, (int64_t)std::ceil(x + 5.0 * std::sqrt(x) + 5.0));
         const int r1 = (int)std::min<int64_t>(S, 2 * (int64_t)r0 + 8);
-        expect = std::min<double>((double)n_eff, (double)(r0 + 4) * (double)stride);
-        PX_TRY(j.sample(S, stride, r0, r1));
+        // each sampled row stands for n_eff / S rows
+        expect = std::min<double>((double)n_eff, (double)(r0 + 4) * (double)n_eff / (double)S);
+        PX_TRY(j.sample(S, r0, r1));
     }
 
     PX_TRY(ws.ensure_status(nq));
@@ -709,9 +724,9 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     j.kk = k + kReRankMargin;
     j.n_eff = n_eff;
     j.cus = cus;
-    j.sample = [&](int64_t S, int64_t stride, int r0, int r1) -> int {
+    j.sample = [&](int64_t S, int r0, int r1) -> int {
         PX_TRY(ws.samp_row.reserve(sizeof(int) * S));
-        PX_HIP(px::launch_sample_rows(rowidx, S, stride, ws.samp_row.as<int>(), s));
+        PX_HIP(px::launch_sample_rows(rowidx, S, n_eff, ws.samp_row.as<int>(), s));
         if (vec_collect(nq, f->dp)) {
             // a few queries: the sampled rows' keys from the vector-ALU scan, row-major
             const int64_t want = std::min<int64_t>(px::kMaxCollectRegions, 4 * (int64_t)cus);
@@ -728,7 +743,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             a.dp = (int)f->dp;
             a.nq = (int)nq;
             a.splits = (int)((S + rps - 1) / rps);
-            a.metric = f->metric;
+            a.metric = f->smetric;
             a.cand_keys = ws.cand_k.as<float>();
             a.dense = 1;
             PX_HIP(px::launch_flat_vcollect(a, s));
@@ -767,7 +782,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.dp = (int)f->dp;
         a.nq = (int)nq;
         a.splits = (int)splits;
-        a.metric = f->metric;
+        a.metric = f->smetric;
         a.cand_keys = ws.cand_k.as<float>();
         a.dense = 1;
         a.dense_ld = ld;
@@ -812,7 +827,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             a.dp = (int)f->dp;
             a.nq = (int)slots;
             a.splits = (int)splits;
-            a.metric = f->metric;
+            a.metric = f->smetric;
             a.qlist = qlist;
             a.thr_key = ws.thr_k.as<int>();
             a.thr_pos = ws.thr_p.as<int>();
@@ -851,7 +866,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.dp = (int)f->dp;
         a.nq = (int)slots;
         a.splits = (int)splits;
-        a.metric = f->metric;
+        a.metric = f->smetric;
         a.qlist = qlist;
         a.thr_key = ws.thr_k.as<int>();
         a.thr_pos = ws.thr_p.as<int>();
@@ -900,7 +915,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     }
     j.sel.rowidx = rowidx;
     j.sel.k = (int)k;
-    j.sel.metric = f->metric;
+    j.sel.metric = f->smetric;
     j.sel.corpus = f->d_x;
     j.sel.queries = d_q;
     j.sel.dim = (int)f->dim;
@@ -972,11 +987,11 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     f->last_path = PX_PATH_LISTS;
     if (k > PX_MAX_K) {
         f->last_path = PX_PATH_FULL_SORT;
-        return run_full_sort(ws, s, f->timing, nq, k, n_eff, rowidx, f->metric, raw_keys,
+        return run_full_sort(ws, s, f->timing, nq, k, n_eff, rowidx, f->smetric, raw_keys,
                              [&](int64_t q0, int qc, float* keys) -> int {
                                  PX_HIP(px::launch_flat_exact_keys(
                                      f->d_x, d_q + q0 * f->dp, rowidx, n_eff, qc, (int)f->dim,
-                                     (int)f->dp, f->metric, keys, s));
+                                     (int)f->dp, f->smetric, keys, s));
                                  return PX_OK;
                              },
                              d_ids, d_out);
@@ -1018,7 +1033,7 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     a.nq = (int)nq;
     a.kl = kl;
     a.splits = splits;
-    a.metric = f->metric;
+    a.metric = f->smetric;
     a.part_keys = ws.part_k.as<float>();
     a.part_ids = ws.part_i.as<int>();
     a.gtau = ws.gtau.as<int>();
@@ -1037,7 +1052,7 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     mg.nq = (int)nq;
     mg.kl = kl;
     mg.k = (int)k;
-    mg.metric = f->metric;
+    mg.metric = f->smetric;
     mg.corpus = f->d_x;
     mg.queries = d_q;
     mg.dim = (int)f->dim;
@@ -1075,13 +1090,14 @@ int check_search_args(const void* idx, const void* queries, int64_t nq, int64_t 
 }
 
 // Host-pointer search: upload, run, download.
-int flat_search_host(px_flat* f, const float* queries, int64_t nq, int64_t k, const uint8_t* mask,
-                     int64_t* out_ids, float* out_d, int raw_keys) {
+int flat_search_host(px_flat* f, int metric, const float* queries, int64_t nq, int64_t k,
+                     const uint8_t* mask, int64_t* out_ids, float* out_d, int raw_keys) {
     if (!all_finite(queries, nq * f->dim))
         return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
     std::lock_guard<std::mutex> lock(f->mu);
+    f->smetric = metric;
     if (f->n == 0) {
-        host_padding(f->metric, nq, k, out_ids, out_d, raw_keys);
+        host_padding(metric, nq, k, out_ids, out_d, raw_keys);
         return PX_OK;
     }
     PX_TRY(flat_sync(f));
@@ -1252,9 +1268,9 @@ int pq_run_collect_batch(px_pq* p, const float* d_q, int64_t nq, int64_t k, int6
     j.kk = k;
     j.n_eff = n_eff;
     j.cus = cus;
-    j.sample = [&](int64_t S, int64_t stride, int r0, int r1) -> int {
+    j.sample = [&](int64_t S, int r0, int r1) -> int {
         PX_TRY(ws.samp_row.reserve(sizeof(int) * S));
-        PX_HIP(px::launch_sample_rows(rowidx, S, stride, ws.samp_row.as<int>(), s));
+        PX_HIP(px::launch_sample_rows(rowidx, S, n_eff, ws.samp_row.as<int>(), s));
         PX_TRY(ws.cand_k.reserve(sizeof(float) * nq * S));
         int64_t splits, rps;
         plan(S, nq, &splits, &rps);
@@ -1467,6 +1483,7 @@ int px_flat_create(int metric, int64_t dim, px_flat** out) {
     px_flat* f = new (std::nothrow) px_flat();
     if (!f) return fail(PX_ERR_ARG, "out of host memory");
     f->metric = metric;
+    f->smetric = metric;
     f->dim = dim;
     f->dp = px::padded_dim(dim);
     *out = f;
@@ -1496,9 +1513,20 @@ int px_flat_add(px_flat* f, const float* vectors, int64_t n) {
     if (f->n + n > (int64_t)INT32_MAX - 1)
         return fail(PX_ERR_ARG, "index would exceed 2^31 - 2 rows");
     std::lock_guard<std::mutex> lock(f->mu);
+    // the rows count only once they are mirrored: a failed upload (e.g. out of device
+    // memory) leaves the index as it was, as the reference's add either completes or panics
+    const size_t pending0 = f->pending.size();
+    const int64_t n0 = f->n;
     f->pending.insert(f->pending.end(), vectors, vectors + n * f->dim);
     f->n += n;
-    if (px_device_count() > 0) PX_TRY(flat_sync(f));
+    if (px_device_count() > 0) {
+        const int rc = flat_sync(f);
+        if (rc != PX_OK) {
+            f->pending.resize(pending0);
+            f->n = n0;
+            return rc;
+        }
+    }
     return PX_OK;
 }
 
@@ -1509,7 +1537,8 @@ int px_flat_search(const px_flat* cf, const float* queries, int64_t nq, int64_t 
     if (queries && !all_finite(queries, nq * cf->dim))
         return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
     if (k == 0 || nq == 0) return PX_OK;
-    return flat_search_host(const_cast<px_flat*>(cf), queries, nq, k, mask, out_ids, out_dists, 0);
+    return flat_search_host(const_cast<px_flat*>(cf), cf->metric, queries, nq, k, mask, out_ids,
+                            out_dists, 0);
 }
 
 int px_flat_search_device(const px_flat* cf, const float* d_queries, int64_t nq, int64_t k,
@@ -1518,8 +1547,10 @@ int px_flat_search_device(const px_flat* cf, const float* d_queries, int64_t nq,
     if (k == 0 || nq == 0) return PX_OK;
     px_flat* f = const_cast<px_flat*>(cf);
     std::lock_guard<std::mutex> lock(f->mu);
+    f->smetric = f->metric;
     PX_TRY(flat_bind(f));
     PX_TRY(flat_sync(f));
+    PX_TRY(check_device_finite(f->ws, d_queries, nq * f->dim, f->stream));
     const float* q = d_queries;
     if (f->dp != f->dim) {
         PX_TRY(f->ws.q.reserve(sizeof(float) * nq * f->dp));
@@ -1612,14 +1643,13 @@ PxGpuIndex* knn_gpu_create(const float* base, int n, int dim) {
     if (!base || n < 0 || dim <= 0) return nullptr;
     PxGpuIndex* g = new (std::nothrow) PxGpuIndex();
     if (!g) return nullptr;
-    // knn.cu:123-141: the corpus is on the device when create returns, else NULL
-    for (int metric = 0; metric < 2; ++metric) {
-        if (px_flat_create(metric, dim, &g->flat[metric]) != PX_OK ||
-            px_flat_add(g->flat[metric], base, n) != PX_OK || flat_bind(g->flat[metric]) != PX_OK ||
-            flat_sync(g->flat[metric]) != PX_OK) {
-            knn_gpu_free(g);
-            return nullptr;
-        }
+    // knn.cu:123-141: the corpus is on the device when create returns, else NULL. One copy
+    // (rows and squared norms) serves both metrics; knn_gpu_search names the metric per
+    // call (knn.cu:143-174). The handle's own metric code is never used.
+    if (px_flat_create(0, dim, &g->flat) != PX_OK || px_flat_add(g->flat, base, n) != PX_OK ||
+        flat_bind(g->flat) != PX_OK || flat_sync(g->flat) != PX_OK) {
+        knn_gpu_free(g);
+        return nullptr;
     }
     return g;
 }
@@ -1629,16 +1659,15 @@ int knn_gpu_search(const PxGpuIndex* g, const float* queries, int nq, int k, int
     if (!g) return fail(PX_ERR_ARG, "null index handle");
     if (k < 1 || k > PX_MAX_K) return fail(PX_ERR_BAD_K, "k out of range");  // knn.cu:145
     if (nq <= 0) return PX_OK;
-    px_flat* f = g->flat[metric == 0 ? 0 : 1];
-    PX_TRY(check_search_args(f, queries, nq, k, out_ids, out_keys));
-    return flat_search_host(f, queries, nq, k, nullptr, reinterpret_cast<int64_t*>(out_ids),
-                            out_keys, 1);
+    PX_TRY(check_search_args(g->flat, queries, nq, k, out_ids, out_keys));
+    // knn.cu's kernel: metric 0 is L2, anything else the inner product
+    return flat_search_host(g->flat, metric == 0 ? 0 : 1, queries, nq, k, nullptr,
+                            reinterpret_cast<int64_t*>(out_ids), out_keys, 1);
 }
 
 void knn_gpu_free(PxGpuIndex* g) {
     if (!g) return;
-    px_flat_destroy(g->flat[0]);
-    px_flat_destroy(g->flat[1]);
+    px_flat_destroy(g->flat);
     delete g;
 }
 
@@ -1750,9 +1779,18 @@ int px_pq_add_codes(px_pq* p, const uint8_t* codes, int64_t n) {
     for (int64_t i = 0; i < n * p->m; ++i)
         if (codes[i] >= p->ks) return fail(PX_ERR_ARG, "code value out of range for nbits");
     std::lock_guard<std::mutex> lock(p->mu);
+    // as px_flat_add: the rows count only once they are on the device
+    const int64_t n0 = p->n;
     p->codes.insert(p->codes.end(), codes, codes + n * p->m);
     p->n += n;
-    if (px_device_count() > 0) PX_TRY(pq_sync(p));
+    if (px_device_count() > 0) {
+        const int rc = pq_sync(p);
+        if (rc != PX_OK) {
+            p->codes.resize((size_t)(n0 * p->m));
+            p->n = n0;
+            return rc;
+        }
+    }
     return PX_OK;
 }
 
@@ -1801,6 +1839,7 @@ int px_pq_search_device(const px_pq* cp, const float* d_queries, int64_t nq, int
     if (k == 0 || nq == 0) return PX_OK;
     std::lock_guard<std::mutex> lock(p->mu);
     PX_TRY(pq_sync(p));
+    PX_TRY(check_device_finite(p->ws, d_queries, nq * p->dim, p->stream));
     return pq_run(p, d_queries, nq, k, p->d_rows ? d_mask : nullptr, d_ids, d_dists);
 }
 

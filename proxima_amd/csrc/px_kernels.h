@@ -60,7 +60,7 @@ hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s);
 // Total-order int of +inf: the starting value of FlatScanArgs::gtau.
 constexpr int kTotalKeyInf = 0x7f800000;
 // Threshold-collect selection for k' past the lists (k' > kMaxList): thresholds from a
-// strided sample, one collect scan, per-query select; queries whose threshold proved too
+// sample of rows spread evenly over the corpus, one collect scan, per-query select; queries whose threshold proved too
 // tight or too loose go round again.
 hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s);
 // The collect scan for a few query slots (nq <= kVecQueries, dp <= kVecMaxDp) on the
@@ -131,8 +131,9 @@ struct LadderArgs {
 // Most sampled keys (64 per block) a ladder workgroup holds in registers.
 constexpr int kMaxLadderEntries = 24576;
 hipError_t launch_ladder(const LadderArgs& a, hipStream_t s);
-// Row sample of the collect path: row[i] = rowidx ? rowidx[i * stride] : i * stride.
-hipError_t launch_sample_rows(const int* rowidx, int64_t count, int64_t stride, int* row,
+// Row sample of the collect path, count rows spread evenly over n_eff positions:
+// position p_i = floor(i * n_eff / count), row[i] = rowidx ? rowidx[p_i] : p_i.
+hipError_t launch_sample_rows(const int* rowidx, int64_t count, int64_t n_eff, int* row,
                               hipStream_t s);
 hipError_t launch_fill_int(int* p, int64_t n, int v, hipStream_t s);
 
@@ -171,6 +172,9 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 hipError_t launch_row_norms(const float* x, int64_t rows, int dp, float* out, hipStream_t s);
 hipError_t launch_pad_rows(const float* src, int64_t rows, int dim, int dp, float* dst,
                            hipStream_t s);
+
+// *flag = 1 when any of x[0 .. count) is NaN or infinite, else 0 (the flag is cleared first).
+hipError_t launch_nonfinite_check(const float* x, int64_t count, int* flag, hipStream_t s);
 
 // Ordered compaction of a keep-mask (nonzero = keep) into ascending row ids.
 // scratch must hold mask_compact_scratch(n) ints; *d_count receives the kept count.

@@ -4,8 +4,9 @@
  * With a gfx950 device: the reference's known answers through both entry families --
  * flat.rs:323-338 (corpus {0^4, 1^4}, query 0^4, k = 5 -> ids [0, 1, -1, -1, -1], distances
  * [0, 2, FLT_MAX x 3]), flat.rs:370-383 (filter keeps row 0 only), the inner-product padding
- * (-FLT_MAX), the raw keys of the CUDA seam (gpu.rs:80-93 finishes them), a PQ index built
- * from explicit codebooks and codes -- and the status codes of bad arguments.
+ * (-FLT_MAX), the raw keys of the CUDA seam for both metrics on one handle (gpu.rs:80-93
+ * finishes them), a PQ index built from explicit codebooks and codes -- and the status codes
+ * of bad arguments, non-finite host and device queries among them.
  * Without a device: every search fails with PX_ERR_DEVICE and knn_gpu_create returns NULL.
  * Prints "abi_check ok (...)" and exits 0, or names the failed check and exits 1. */
 #include <float.h>
@@ -56,6 +57,32 @@ static void with_device(void) {
     const float nanq[4] = {0, NAN, 0, 0};
     CHECK(px_flat_search(f, nanq, 1, 5, NULL, ids, d) == PX_ERR_NONFINITE, "non-finite query");
     CHECK(strlen(px_last_error()) > 0, "error text");
+    {
+        /* the device-pointer form checks its queries on the device before searching */
+        void *dq = NULL, *di = NULL, *dd = NULL;
+        CHECK(px_dev_alloc(&dq, sizeof nanq) == PX_OK && px_dev_alloc(&di, 5 * 8) == PX_OK &&
+                  px_dev_alloc(&dd, 5 * 4) == PX_OK,
+              "px_dev_alloc");
+        CHECK(px_dev_upload(dq, nanq, sizeof nanq) == PX_OK, "upload NaN query");
+        CHECK(px_flat_search_device(f, (const float*)dq, 1, 5, NULL, (int64_t*)di, (float*)dd) ==
+                  PX_ERR_NONFINITE,
+              "non-finite device query");
+        const float infq[4] = {0, 0, -INFINITY, 0};
+        CHECK(px_dev_upload(dq, infq, sizeof infq) == PX_OK, "upload infinite query");
+        CHECK(px_flat_search_device(f, (const float*)dq, 1, 5, NULL, (int64_t*)di, (float*)dd) ==
+                  PX_ERR_NONFINITE,
+              "infinite device query");
+        CHECK(px_dev_upload(dq, query, sizeof query) == PX_OK, "upload finite query");
+        CHECK(px_flat_search_device(f, (const float*)dq, 1, 5, NULL, (int64_t*)di, (float*)dd) ==
+                  PX_OK,
+              "finite device query after a rejected one");
+        CHECK(px_dev_download(ids, di, sizeof ids) == PX_OK && ids[0] == 0 && ids[1] == 1 &&
+                  ids[2] == -1,
+              "device search results");
+        px_dev_free(dq);
+        px_dev_free(di);
+        px_dev_free(dd);
+    }
     px_flat_destroy(f);
 
     px_flat* g = NULL;
@@ -77,6 +104,14 @@ static void with_device(void) {
     CHECK(kid[0] == 0 && kid[1] == 1 && kid[2] == -1 && kk[0] == 0.0f && kk[1] == 4.0f &&
               kk[2] == FLT_MAX,
           "raw squared-L2 keys and padding");
+    /* the same handle (one corpus copy) serves the inner product: raw keys are -q.x */
+    const float ones[4] = {1, 1, 1, 1};
+    CHECK(knn_gpu_search(gi, ones, 1, 3, 1, kid, kk) == 0, "knn_gpu_search IP");
+    CHECK(kid[0] == 1 && kid[1] == 0 && kid[2] == -1 && kk[0] == -4.0f && kk[1] == 0.0f &&
+              kk[2] == FLT_MAX,
+          "raw inner-product keys on the shared corpus copy");
+    CHECK(knn_gpu_search(gi, query, 1, 3, 0, kid, kk) == 0 && kk[1] == 4.0f,
+          "L2 again after an inner-product search");
     CHECK(knn_gpu_search(gi, query, 1, 0, 0, kid, kk) == -1, "knn.cu:145 k < 1");
     CHECK(knn_gpu_search(gi, query, 1, PX_MAX_K + 1, 0, kid, kk) == -1, "seam k limit");
     knn_gpu_free(gi);
@@ -99,6 +134,20 @@ static void with_device(void) {
     CHECK(ids[0] == 1 && ids[1] == 2 && ids[2] == 0 && ids[3] == -1, "pq order");
     CHECK(d[0] == 0.0f && d[1] == 3.0f && fabsf(d[2] - sqrtf(27.0f)) == 0.0f && d[3] == FLT_MAX,
           "pq distances");
+    {
+        const float nanq[4] = {NAN, 0, 0, 0};
+        void *dq = NULL, *di = NULL, *dd = NULL;
+        CHECK(px_dev_alloc(&dq, sizeof nanq) == PX_OK && px_dev_alloc(&di, 4 * 8) == PX_OK &&
+                  px_dev_alloc(&dd, 4 * 4) == PX_OK,
+              "px_dev_alloc (pq)");
+        CHECK(px_dev_upload(dq, nanq, sizeof nanq) == PX_OK, "upload NaN query (pq)");
+        CHECK(px_pq_search_device(p, (const float*)dq, 1, 4, NULL, (int64_t*)di, (float*)dd) ==
+                  PX_ERR_NONFINITE,
+              "non-finite device query (pq)");
+        px_dev_free(dq);
+        px_dev_free(di);
+        px_dev_free(dd);
+    }
     px_pq_destroy(p);
 }
 

@@ -29,6 +29,14 @@ def gpu():
     return True
 
 
+def sample_positions(n_eff: int, kk: int) -> np.ndarray:
+    """Positions of the collect path's threshold sample: S = min(n_eff, 16384,
+    80 * n_eff // kk) rows spread evenly, position floor(i * n_eff / S) for i < S. kk is
+    the number of candidates the search keeps (k + 8 on the flat path, k for PQ)."""
+    s = max(1, min(n_eff, 16384, 80 * n_eff // kk))
+    return np.arange(s, dtype=np.int64) * n_eff // s
+
+
 def rel(a, b):
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)

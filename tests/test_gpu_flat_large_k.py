@@ -1,9 +1,11 @@
 """GPU parity of the threshold-collect and full-sort paths of FlatIndex searches.
 
 The reference's FlatIndex takes any k (flat.rs:106-148 keeps a heap of k); so does the
-library: up to PX_MAX_K on the fused scans, past it by sorting every key. For k + 8 > 128,
-and for k >= 16 in batches of at least 256 queries (k + 8 > 56 below 262,144 rows), it
-samples a strided subset of the rows for per-query thresholds, appends every row at or
+library: up to PX_MAX_K on the fused scans, past it by sorting every key. For k' = k + 8
+past 128, and for k >= 16 in batches of at least 256 queries where the lists do not win
+(the lists keep k' <= 56 on rows of more than 128 padded dims below 262,144 rows, and on
+rows of at most 128 padded dims while n_eff * (k' - 16) < 1.04M), it samples a subset of
+the rows spread evenly over the corpus for per-query thresholds, appends every row at or
 below them in one collect scan, and finishes each query whose candidate set is complete
 and large enough; the others go round again with a looser or tighter threshold.
 Unfiltered batches of at least 256 queries with k + 8 <= 24 on rows of at most 128 padded
@@ -18,7 +20,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import assert_parity
+from conftest import assert_parity, sample_positions
 from proxima_amd import FlatIndex, Metric, _lib, datagen
 
 pytestmark = pytest.mark.gpu
@@ -58,14 +60,6 @@ def _check(data, queries, k, metric, mask=None, exact=False):
         assert np.array_equal(ids, o_ids)
         assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
     return _rounds(idx)
-
-
-def _sample_stride(n_eff: int, k: int) -> int:
-    """Stride of the threshold sample: S = min(n_eff, 16384, 80 * n_eff // k') rows taken
-    at positions 0, stride, 2 * stride, ... with stride = n_eff // S and k' = k + 8."""
-    kk = k + 8
-    s = max(1, min(n_eff, 16384, 80 * n_eff // kk))
-    return n_eff // s
 
 
 @pytest.mark.parametrize("k", [121, 300, 1000, 4096])
@@ -166,10 +160,10 @@ def test_sample_far_overflow_round(gpu):
     # threshold lets nearly every row through, the select overflows, and later rounds
     # tighten the threshold from the candidates.
     n, k = 40_000, 992
-    stride = _sample_stride(n, k)
+    sampled = sample_positions(n, k + 8)
     rng = np.random.default_rng(45)
     data = rng.integers(0, 4, size=(n, 48)).astype(np.float32)
-    data[::stride] = 255.0
+    data[sampled] = 255.0
     q = rng.integers(0, 3, size=(12, 48)).astype(np.float32)
     rounds = _check(data, q, k, oracle.L2, exact=True)
     assert rounds >= 2
@@ -179,10 +173,10 @@ def test_sample_near_underflow_rounds(gpu):
     # The sampled rows are the near ones: the sample's thresholds admit too few rows, the
     # ladder runs out, and the query finishes from an unbounded round.
     n, k = 40_000, 992
-    stride = _sample_stride(n, k)
+    sampled = sample_positions(n, k + 8)
     rng = np.random.default_rng(46)
     data = rng.integers(200, 256, size=(n, 48)).astype(np.float32)
-    data[::stride] = rng.integers(0, 4, size=(data[::stride].shape[0], 48))
+    data[sampled] = rng.integers(0, 4, size=(sampled.size, 48))
     q = rng.integers(0, 3, size=(12, 48)).astype(np.float32)
     rounds = _check(data, q, k, oracle.L2, exact=True)
     assert rounds >= 3
@@ -321,7 +315,7 @@ n, k = 40_000, 992
 s = max(1, min(n, 16384, 80 * n // (k + 8)))
 rng = np.random.default_rng(45)
 data = rng.integers(0, 4, size=(n, 48)).astype(np.float32)
-data[::n // s] = 255.0
+data[np.arange(s) * n // s] = 255.0  # the sampled positions, floor(i * n / s)
 q = rng.integers(0, 3, size=(300, 48)).astype(np.float32)
 idx = FlatIndex(48, Metric.L2)
 idx.add(data)

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
-from conftest import assert_parity
+from conftest import assert_parity, sample_positions
 from proxima_amd import FlatIndex, Metric, datagen
 
 pytestmark = pytest.mark.gpu
@@ -142,11 +142,8 @@ def test_sample_far_retry_rounds(gpu):
     # the sampled rows are far from every query and the rest are near: the first round's
     # threshold lets too many rows through and later rounds tighten it; exact on integers
     n, k = 40_000, 300
-    kk = k + 8
-    S = max(1, min(n, 16384, 80 * n // kk))
-    stride = n // S
     rng = np.random.default_rng(91)
     data = rng.integers(0, 4, size=(n, 48)).astype(np.float32)
-    data[::stride] = 255.0
+    data[sample_positions(n, k + 8)] = 255.0
     q = rng.integers(0, 3, size=(4, 48)).astype(np.float32)
     assert _check(data, q, k, oracle.L2, exact=True) >= 2

@@ -1,7 +1,7 @@
 """GPU parity of PqIndex searches with k > 128: the threshold-collect path.
 
 The reference's PqIndex takes any k (pq.rs:299-347 keeps a heap of k). Past the per-wave
-candidate lists the library samples a strided subset of the code rows for per-query
+candidate lists the library samples a subset of the code rows spread evenly for per-query
 thresholds, appends every row at or below them in one collect scan, and finishes each query
 whose candidate set is complete and large enough; ADC keys are the reference's own sums
 (pq.rs:320-323), so ids and distances are bit-identical to the oracle's with no re-rank.
@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 
 import oracle
+from conftest import sample_positions
 from proxima_amd import Metric, PqIndex, datagen
 
 pytestmark = pytest.mark.gpu
@@ -84,14 +85,6 @@ def test_pq_full_sort_past_max_k(gpu, metric):
     _check(pq, q, 9500, metric)
 
 
-def _stride(n_eff: int, k: int) -> int:
-    """Stride of the threshold sample: S = min(n_eff, 16384, 80 * n_eff // k) rows at
-    positions 0, stride, 2 * stride, ... with stride = n_eff // S (ADC keys are exact, so
-    the collect path keeps k' = k)."""
-    s = max(1, min(n_eff, 16384, 80 * n_eff // k))
-    return n_eff // s
-
-
 def _laid_out(near_on_sample: bool, seed: int):
     """4 x 16-centroid codebooks; codes near the query on the sampled rows and far from it
     elsewhere (or the other way round)."""
@@ -107,7 +100,10 @@ def _laid_out(near_on_sample: bool, seed: int):
     near, far = order[:, :4], order[:, -4:]
     rng = np.random.default_rng(seed + 2)
     pick = rng.integers(0, 4, size=(n, m))
-    codes = np.where(np.arange(n)[:, None] % _stride(n, k) == 0,
+    # ADC keys are exact, so the collect path keeps k candidates (no re-rank margin)
+    on_sample = np.zeros(n, dtype=bool)
+    on_sample[sample_positions(n, k)] = True
+    codes = np.where(on_sample[:, None],
                      np.take_along_axis(near if near_on_sample else far, pick.T, 1).T,
                      np.take_along_axis(far if near_on_sample else near, pick.T, 1).T)
     pq.add_codes(codes.astype(np.uint8))

@@ -63,3 +63,17 @@ def test_encode_more_than_one_chunk(gpu):
     pq.add(vecs)
     assert len(pq) == vecs.shape[0]
     assert np.array_equal(pq.codes(), oracle.pq_encode(pq.codebooks(), vecs))
+
+
+def test_known_answers_on_gpu(gpu):
+    # the k-means known answers of test_oracle.py through the GPU trainer: the mean is the
+    # sum times the rounded reciprocal (pq.rs:185-188), and an empty cluster is re-seeded
+    # from the k-means generator's next draw (pq.rs:180-183)
+    from test_oracle import EMPTY_ROWS, EMPTY_SEED, MEAN_ROWS
+
+    pq = _train(MEAN_ROWS, 1, 1, 10, 0)
+    by_reciprocal = np.float32(5.0) * (np.float32(1.0) / np.float32(3.0))
+    assert sorted(pq.codebooks().reshape(-1).tolist()) == [float(by_reciprocal), 1000.0]
+    pq = _train(EMPTY_ROWS, 1, 1, 1, 0, seed=EMPTY_SEED)
+    expect = [float(np.float32(39.0) * (np.float32(1.0) / np.float32(7.0))), 9.0]
+    assert pq.codebooks().reshape(-1).tolist() == expect

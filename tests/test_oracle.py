@@ -394,6 +394,57 @@ def test_train_sample_with_replacement_uses_splitmix_draws():
         assert (drawn == c).all(1).any()
 
 
+# Known answers for the two k-means steps of pq.rs:179-190 that a Lloyd invariant at a
+# tolerance cannot see. m = 1 subspace of 1 dim, 2 centroids (nbits = 1), every row used
+# (train_sample = 0: no sampling draws), so the k-means generator is SplitMix(seed).
+MEAN_ROWS = np.array([[1.0], [2.0], [2.0], [1000.0]], dtype=np.float32)
+EMPTY_ROWS = np.array([[5.0]] * 6 + [[9.0]], dtype=np.float32)
+EMPTY_SEED = 3
+
+
+def _train_both(rows, iters, seed):
+    """Codebooks of the oracle and of the product's own trainer (on the host here)."""
+    from proxima_amd import Metric, PqIndex
+
+    pq = PqIndex(1, Metric.L2, m=1, nbits=1, train_iters=iters, train_sample=0, seed=seed)
+    pq.train(rows)
+    return oracle.pq_train(rows, 1, 1, iters, 0, seed), pq.codebooks()
+
+
+def test_kmeans_mean_is_reciprocal_multiply_known_answer():
+    # Clusters {1, 2, 2} and {1000} whatever the start (10 Lloyd steps). The first mean is
+    # the sum 5 times the rounded reciprocal 1/3 (pq.rs:185-188): 5 * fl(1/3) =
+    # 1.66666675 in fp32, where a divide 5 / 3 rounds to 1.66666663.
+    by_reciprocal = np.float32(5.0) * (np.float32(1.0) / np.float32(3.0))
+    by_divide = np.float32(5.0) / np.float32(3.0)
+    assert by_reciprocal != by_divide and by_reciprocal == np.float32(1.66666675)
+    for books in _train_both(MEAN_ROWS, 10, 24301):
+        assert sorted(books.reshape(-1).tolist()) == [float(by_reciprocal), 1000.0]
+
+
+def test_kmeans_empty_cluster_reseed_known_answer():
+    # Six rows of 5 and one of 9, seed 3. Published SplitMix64 draws z0..z3 of seed 3 (the
+    # generator is pinned to Vigna's outputs above) give the start: centroid 0 = row
+    # z0 % 7, centroid 1 = row order[1 + z1 % 6] after the partial Fisher-Yates swap
+    # (pq.rs:142-148) -- rows 2 and 4, both 5. Every row is then nearest to centroid 0
+    # (strict <, ties to the lower centroid), so cluster 1 is empty and is re-seeded from
+    # row z2 % 7 = 6, the 9 (pq.rs:180-183); centroid 0 becomes 39 * fl(1/7).
+    z = oracle.splitmix(EMPTY_SEED, 4)
+    n = len(EMPTY_ROWS)
+    order = list(range(n))
+    j0 = z[0] % n
+    order[0], order[j0] = order[j0], order[0]
+    j1 = 1 + z[1] % (n - 1)
+    order[1], order[j1] = order[j1], order[1]
+    assert (order[0], order[1]) == (2, 4)
+    assert z[2] % n == 6
+    # a re-seed from a fresh generator's first draw, or one draw late, picks a 5 instead
+    assert z[0] % n != 6 and z[3] % n != 6
+    expect = [float(np.float32(39.0) * (np.float32(1.0) / np.float32(7.0))), 9.0]
+    for books in _train_both(EMPTY_ROWS, 1, EMPTY_SEED):
+        assert books.reshape(-1).tolist() == expect
+
+
 def test_product_training_equals_oracle():
     # libproxima_px.so trains with its own code (on the host here, where no device is
     # visible; its GPU kernels are checked the same way in test_gpu_pq_train.py); it must
