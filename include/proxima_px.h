@@ -102,6 +102,25 @@ int px_flat_search(const px_flat* idx, const float* queries, int64_t nq, int64_t
 int px_flat_search_device(const px_flat* idx, const float* d_queries, int64_t nq, int64_t k,
                           const uint8_t* d_mask, int64_t* d_ids, float* d_dists);
 
+/*
+ * No counterpart in the reference: px_flat_search_device for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, results and checks as px_flat_search_device, but it calls no
+ * hipMalloc, hipFree or other allocating routine: its work buffers (split candidate lists,
+ * shared bounds, padded queries, a filter's compacted row ids) live in a fixed 64 MiB
+ * device array that the library holds on each GPU it runs on until the process ends.
+ * Limits: k <= 120 (every search takes the per-split list path); the buffers for nq queries
+ * must fit the array (about nq * (k + 8) * 8 bytes per corpus split, plus nq * 132 bytes,
+ * nq * padded dim * 4 when dim is not a multiple of 8, and 4 bytes per row with a mask);
+ * larger calls return PX_ERR_ARG or PX_ERR_BAD_K naming the limit. The index's rows must
+ * already be on the device (px_flat_add with the GPU present). Every call on one GPU uses
+ * that GPU's one array: calls that overlap on the same GPU (from several threads or
+ * handles) race and must be serialised by the caller. px_flat_last_timing is not updated.
+ */
+int px_flat_search_device_noalloc(const px_flat* idx, const float* d_queries, int64_t nq,
+                                  int64_t k, const uint8_t* d_mask, int64_t* d_ids,
+                                  float* d_dists);
+
 /* Copy rows [first, first + n) out as row-major n x dim floats (FlatIndex::save needs the
  * data, flat.rs:64-66 -> lib.rs:19-30). */
 int px_flat_get_vectors(const px_flat* idx, int64_t first, int64_t n, float* out);

@@ -42,6 +42,8 @@ SIGNATURES = {
     "px_flat_search": (c_int, [c_void_p, _f32p, c_int64, c_int64, _u8p, _i64p, _f32p]),
     "px_flat_search_device": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p,
                                       c_void_p]),
+    "px_flat_search_device_noalloc": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p,
+                                              c_void_p, c_void_p]),
     "px_flat_get_vectors": (c_int, [c_void_p, c_int64, c_int64, _f32p]),
     "px_flat_size": (c_int64, [c_void_p]),
     "px_flat_dim": (c_int64, [c_void_p]),

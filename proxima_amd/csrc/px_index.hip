@@ -206,32 +206,46 @@ int download_results(Workspace& ws, int64_t nq, int64_t k, hipStream_t s, int64_
 }
 
 // Compacts a device keep-mask into ascending row ids; returns the kept count in *n_eff.
+// Compacts a device keep-mask of n rows into ascending row ids (rowidx, n ints; cscr,
+// mask_compact_scratch(n) ints; d_count one int) and reads the kept count back through
+// h_count (host memory: pinned, or the caller's own).
+int compact_mask_into(const uint8_t* d_mask, int64_t n, int* rowidx, int* cscr, int* d_count,
+                      int* h_count, hipStream_t s, int64_t* n_eff) {
+    PX_HIP(px::launch_mask_compact(d_mask, n, rowidx, cscr, d_count, s));
+    PX_HIP(hipMemcpyAsync(h_count, d_count, sizeof(int), hipMemcpyDeviceToHost, s));
+    PX_HIP(hipStreamSynchronize(s));
+    *n_eff = *h_count;
+    return PX_OK;
+}
+
 int compact_mask(Workspace& ws, const uint8_t* d_mask, int64_t n, hipStream_t s, int64_t* n_eff,
                  const int** rowidx) {
     PX_TRY(ws.rowidx.reserve(sizeof(int) * std::max<int64_t>(n, 1)));
     PX_TRY(ws.scratch.reserve(sizeof(int) * px::mask_compact_scratch(n)));
     PX_TRY(ws.count.reserve(sizeof(int)));
     PX_TRY(ws.ensure_pinned());
-    PX_HIP(px::launch_mask_compact(d_mask, n, ws.rowidx.as<int>(), ws.scratch.as<int>(),
-                                   ws.count.as<int>(), s));
-    PX_HIP(hipMemcpyAsync(ws.h_count, ws.count.p, sizeof(int), hipMemcpyDeviceToHost, s));
-    PX_HIP(hipStreamSynchronize(s));
-    *n_eff = *ws.h_count;
+    PX_TRY(compact_mask_into(d_mask, n, ws.rowidx.as<int>(), ws.scratch.as<int>(),
+                             ws.count.as<int>(), ws.h_count, s, n_eff));
     *rowidx = ws.rowidx.as<int>();
     return PX_OK;
 }
 
 // Device queries (count floats) must be finite, as flat.rs:114-117 asserts of every query:
-// checked on the device, and the host waits for the answer before any search kernel runs.
+// checked on the device (d_flag, one int), and the host waits for the answer (read through
+// h_flag) before any search kernel runs.
+int check_finite_into(const float* d_x, int64_t count, int* d_flag, int* h_flag, hipStream_t s) {
+    PX_HIP(px::launch_nonfinite_check(d_x, count, d_flag, s));
+    PX_HIP(hipMemcpyAsync(h_flag, d_flag, sizeof(int), hipMemcpyDeviceToHost, s));
+    PX_HIP(hipStreamSynchronize(s));
+    if (*h_flag)
+        return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
+    return PX_OK;
+}
+
 int check_device_finite(Workspace& ws, const float* d_x, int64_t count, hipStream_t s) {
     PX_TRY(ws.count.reserve(sizeof(int)));
     PX_TRY(ws.ensure_pinned());
-    PX_HIP(px::launch_nonfinite_check(d_x, count, ws.count.as<int>(), s));
-    PX_HIP(hipMemcpyAsync(ws.h_count, ws.count.p, sizeof(int), hipMemcpyDeviceToHost, s));
-    PX_HIP(hipStreamSynchronize(s));
-    if (*ws.h_count)
-        return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
-    return PX_OK;
+    return check_finite_into(d_x, count, ws.count.as<int>(), ws.h_count, s);
 }
 
 // Number of corpus splits: enough workgroups to fill the GPU several times over, each
@@ -451,12 +465,15 @@ struct ListPlan {
     int splits = 1;
     int64_t rps = 64, groups = 1;
 };
-int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int cus, ListPlan* out, int64_t k) {
+// max_splits (>= 1) caps the split count (the no-allocation entry point's fixed scratch).
+int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int cus, ListPlan* out, int64_t k,
+                   int64_t max_splits = INT32_MAX) {
     const int kp = px::flat_list_capacity(kl);
     const int64_t qpb = px::flat_queries_per_block(kp);
     const int64_t groups = (nq + qpb - 1) / qpb;
     const bool narrow = px::flat_list_narrow_ids(kp);
-    int splits = choose_flat_splits(n_eff, groups, kl, cus, narrow);
+    int splits = (int)std::min<int64_t>(choose_flat_splits(n_eff, groups, kl, cus, narrow),
+                                        std::max<int64_t>(1, max_splits));
     int64_t rps = (n_eff + splits - 1) / splits;
     rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
     if (narrow) rps = std::min<int64_t>(rps, px::kMaxNarrowSplitRows);
@@ -464,6 +481,9 @@ int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int cus, ListPlan* out, in
     if ((int64_t)splits * kl > px::kMaxMerge)
         return fail(PX_ERR_BAD_K, "k=" + std::to_string(k) + " over " + std::to_string(n_eff) +
                                       " rows needs more split lists than the merge holds");
+    if (splits > max_splits)
+        return fail(PX_ERR_ARG, "k=" + std::to_string(k) + " over " + std::to_string(n_eff) +
+                                    " rows needs more splits than the scratch holds lists for");
     out->splits = splits;
     out->rps = rps;
     out->groups = groups;
@@ -975,6 +995,78 @@ int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_
     return PX_OK;
 }
 
+// Device buffers of a list scan: split lists [nq][splits][kl] (key, position), the shared
+// bounds gtau [nq] and gbest [nq][32] (cleared here by fill kernels).
+struct ListBufs {
+    float* part_k;
+    int* part_i;
+    int* gtau;
+    int* gbest;
+};
+
+// The per-split list path: fused MFMA scan with per-split lists, then the merge (re-rank in
+// the reference's arithmetic, finish, pad). Waits for the stream. timed: record the
+// handle's HIP events (created beforehand).
+int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
+                   const int* rowidx, const ListPlan& lp, int kl, const ListBufs& b,
+                   int64_t* d_ids, float* d_out, int raw_keys, bool timed) {
+    hipStream_t s = f->stream;
+    const int splits = lp.splits;
+    const int64_t rps = lp.rps, groups = lp.groups;
+    PX_HIP(px::launch_fill_int(b.gtau, nq, px::kTotalKeyInf, s));
+    PX_HIP(px::launch_fill_int(b.gbest, nq * 32, px::kTotalKeyInf, s));
+    if (timed) PX_HIP(hipEventRecord(f->timing.ev[0], s));
+
+    px::FlatScanArgs a{};
+    a.corpus = f->d_x;
+    a.norms = f->d_norm;
+    a.queries = d_q;
+    a.rowidx = rowidx;
+    a.n_eff = n_eff;
+    a.rows_per_split = rps;
+    a.dp = (int)f->dp;
+    a.nq = (int)nq;
+    a.kl = kl;
+    a.splits = splits;
+    a.metric = f->smetric;
+    a.part_keys = b.part_k;
+    a.part_ids = b.part_i;
+    a.gtau = b.gtau;
+    a.gbest = b.gbest;
+    if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
+    if (timed) PX_HIP(hipEventRecord(f->timing.ev[1], s));
+
+    px::MergeArgs mg{};
+    mg.part_keys = a.part_keys;
+    mg.part_ids = a.part_ids;
+    mg.rowidx = rowidx;
+    mg.width = n_eff > 0 ? splits * kl : 0;
+    mg.bound = b.gtau;
+    mg.gbest = b.gbest;
+    mg.splits = splits;
+    mg.nq = (int)nq;
+    mg.kl = kl;
+    mg.k = (int)k;
+    mg.metric = f->smetric;
+    mg.corpus = f->d_x;
+    mg.queries = d_q;
+    mg.dim = (int)f->dim;
+    mg.dp = (int)f->dp;
+    mg.out_ids = d_ids;
+    mg.out_dists = d_out;
+    mg.raw_keys = raw_keys;
+    PX_HIP(px::launch_merge(mg, s));
+    if (timed) PX_HIP(hipEventRecord(f->timing.ev[2], s));
+    PX_HIP(hipStreamSynchronize(s));
+    if (timed) {
+        PX_HIP(hipEventElapsedTime(&f->timing.scan_ms, f->timing.ev[0], f->timing.ev[1]));
+        PX_HIP(hipEventElapsedTime(&f->timing.total_ms, f->timing.ev[0], f->timing.ev[2]));
+        f->timing.splits = splits;
+        f->timing.blocks = (int)(groups * splits);
+    }
+    return PX_OK;
+}
+
 // Runs the device pipeline. d_q: [nq][dp] on device. Outputs on device.
 int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
              int64_t* d_ids, float* d_out, int raw_keys) {
@@ -1010,66 +1102,14 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     const int kl = (int)std::min<int64_t>(px::kMaxList, k + kReRankMargin);
     ListPlan lp;
     PX_TRY(plan_list_scan(n_eff, nq, kl, f->dev.cus, &lp, k));
-    const int splits = lp.splits;
-    const int64_t rps = lp.rps, groups = lp.groups;
-
-    PX_TRY(ws.part_k.reserve(sizeof(float) * nq * splits * kl));
-    PX_TRY(ws.part_i.reserve(sizeof(int) * nq * splits * kl));
+    PX_TRY(ws.part_k.reserve(sizeof(float) * nq * lp.splits * kl));
+    PX_TRY(ws.part_i.reserve(sizeof(int) * nq * lp.splits * kl));
     PX_TRY(ws.gtau.reserve(sizeof(int) * nq));
-    PX_HIP(px::launch_fill_int(ws.gtau.as<int>(), nq, px::kTotalKeyInf, s));
     PX_TRY(ws.gbest.reserve(sizeof(int) * nq * 32));
-    PX_HIP(px::launch_fill_int(ws.gbest.as<int>(), nq * 32, px::kTotalKeyInf, s));
     PX_TRY(f->timing.ensure());
-    if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[0], s));
-
-    px::FlatScanArgs a{};
-    a.corpus = f->d_x;
-    a.norms = f->d_norm;
-    a.queries = d_q;
-    a.rowidx = rowidx;
-    a.n_eff = n_eff;
-    a.rows_per_split = rps;
-    a.dp = (int)f->dp;
-    a.nq = (int)nq;
-    a.kl = kl;
-    a.splits = splits;
-    a.metric = f->smetric;
-    a.part_keys = ws.part_k.as<float>();
-    a.part_ids = ws.part_i.as<int>();
-    a.gtau = ws.gtau.as<int>();
-    a.gbest = ws.gbest.as<int>();
-    if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
-    if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[1], s));
-
-    px::MergeArgs mg{};
-    mg.part_keys = a.part_keys;
-    mg.part_ids = a.part_ids;
-    mg.rowidx = rowidx;
-    mg.width = n_eff > 0 ? splits * kl : 0;
-    mg.bound = ws.gtau.as<int>();
-    mg.gbest = ws.gbest.as<int>();
-    mg.splits = splits;
-    mg.nq = (int)nq;
-    mg.kl = kl;
-    mg.k = (int)k;
-    mg.metric = f->smetric;
-    mg.corpus = f->d_x;
-    mg.queries = d_q;
-    mg.dim = (int)f->dim;
-    mg.dp = (int)f->dp;
-    mg.out_ids = d_ids;
-    mg.out_dists = d_out;
-    mg.raw_keys = raw_keys;
-    PX_HIP(px::launch_merge(mg, s));
-    if (f->timing.enabled) PX_HIP(hipEventRecord(f->timing.ev[2], s));
-    PX_HIP(hipStreamSynchronize(s));
-    if (f->timing.enabled) {
-        PX_HIP(hipEventElapsedTime(&f->timing.scan_ms, f->timing.ev[0], f->timing.ev[1]));
-        PX_HIP(hipEventElapsedTime(&f->timing.total_ms, f->timing.ev[0], f->timing.ev[2]));
-        f->timing.splits = splits;
-        f->timing.blocks = (int)(groups * splits);
-    }
-    return PX_OK;
+    ListBufs b{ws.part_k.as<float>(), ws.part_i.as<int>(), ws.gtau.as<int>(), ws.gbest.as<int>()};
+    return flat_run_lists(f, d_q, nq, k, n_eff, rowidx, lp, kl, b, d_ids, d_out, raw_keys,
+                          f->timing.enabled);
 }
 
 void host_padding(int metric, int64_t nq, int64_t k, int64_t* ids, float* out, int raw_keys) {
@@ -1468,6 +1508,59 @@ int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_m
 }  // namespace
 
 // ---------------------------------------------------------------------------------------
+// Fixed scratch of px_flat_search_device_noalloc: the entry point for callers that cannot
+// allocate device memory. Each GPU the library runs on holds its own copy of this array
+// from the code object's load until the process ends. In host code `scratch` names a
+// host-side stand-in, not device memory: every use goes through the device address that
+// hipGetSymbolAddress returns for the device.
+// ---------------------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+// Largest k the entry point serves (its k + 8 candidates fit the per-split lists).
+constexpr int64_t kNoAllocMaxK = px::kMaxList - kReRankMargin;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+std::mutex g_scratch_mu;
+constexpr int kMaxScratchDevices = 64;
+unsigned char* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on `device`, looked up once per device with that device
+// current (the caller has made it current).
+int scratch_of_device(int device, unsigned char** out) {
+    if (device < 0 || device >= kMaxScratchDevices)
+        return fail(PX_ERR_DEVICE, "device ordinal out of range for the fixed scratch");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(e != hipSuccess ? (int)e : PX_ERR_DEVICE,
+                        std::string("hipGetSymbolAddress of the fixed scratch failed: ") +
+                            hipGetErrorString(e));
+        g_scratch_ptr[device] = static_cast<unsigned char*>(ptr);
+    }
+    *out = g_scratch_ptr[device];
+    return PX_OK;
+}
+
+// Bump layout over the fixed scratch: 256-byte aligned pieces in order. With base ==
+// nullptr it only measures.
+struct ScratchLayout {
+    unsigned char* base = nullptr;
+    size_t used = 0;
+    template <class T>
+    T* take(size_t count) {
+        const size_t off = (used + 255) / 256 * 256;
+        used = off + count * sizeof(T);
+        return base ? reinterpret_cast<T*>(base + off) : nullptr;
+    }
+};
+
+}  // namespace
+
+
+// ---------------------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------------------
 extern "C" {
@@ -1558,6 +1651,78 @@ int px_flat_search_device(const px_flat* cf, const float* d_queries, int64_t nq,
         q = f->ws.q.as<float>();
     }
     return flat_run(f, q, nq, k, f->d_rows ? d_mask : nullptr, d_ids, d_dists, 0);
+}
+
+int px_flat_search_device_noalloc(const px_flat* cf, const float* d_queries, int64_t nq,
+                                  int64_t k, const uint8_t* d_mask, int64_t* d_ids,
+                                  float* d_dists) {
+    PX_TRY(check_search_args(cf, d_queries, nq, k, d_ids, d_dists));
+    if (k == 0 || nq == 0) return PX_OK;
+    if (k > kNoAllocMaxK)
+        return fail(PX_ERR_BAD_K, "px_flat_search_device_noalloc serves k <= " +
+                                      std::to_string(kNoAllocMaxK) + ", got " + std::to_string(k));
+    if (nq > INT32_MAX) return fail(PX_ERR_ARG, "nq must fit 32 bits");
+    px_flat* f = const_cast<px_flat*>(cf);
+    std::lock_guard<std::mutex> lock(f->mu);
+    // binding a device and uploading rows allocate: both must have happened already, in
+    // px_flat_add with the device present
+    if (f->dev.device < 0 || !f->stream || !f->pending.empty())
+        return fail(PX_ERR_DEVICE, "px_flat_search_device_noalloc needs the rows on the device "
+                                   "already (px_flat_add with the GPU present)");
+    PX_HIP(hipSetDevice(f->dev.device));
+    unsigned char* base = nullptr;
+    PX_TRY(scratch_of_device(f->dev.device, &base));
+    f->smetric = f->metric;
+    const int64_t n = f->d_rows;
+    const bool masked = d_mask != nullptr && n > 0;
+    const int kl = (int)(k + kReRankMargin);
+    const bool pad = f->dp != f->dim;
+    hipStream_t s = f->stream;
+
+    // the fixed pieces, then the split lists in what remains
+    auto fixed = [&](ScratchLayout& L, int** flag, float** q, int** rowidx, int** cscr,
+                     int** gtau, int** gbest) {
+        *flag = L.take<int>(2);
+        *q = pad ? L.take<float>((size_t)(nq * f->dp)) : nullptr;
+        *rowidx = masked ? L.take<int>((size_t)n) : nullptr;
+        *cscr = masked ? L.take<int>((size_t)px::mask_compact_scratch(n)) : nullptr;
+        *gtau = L.take<int>((size_t)nq);
+        *gbest = L.take<int>((size_t)nq * 32);
+    };
+    ScratchLayout L;
+    int *flag, *rowidx, *cscr, *gtau, *gbest;
+    float* q;
+    fixed(L, &flag, &q, &rowidx, &cscr, &gtau, &gbest);
+    const size_t per_split = (size_t)nq * kl * 8 + 512;  // both list arrays, alignment
+    if (L.used + per_split > kNoAllocScratchBytes)
+        return fail(PX_ERR_ARG, "px_flat_search_device_noalloc: nq=" + std::to_string(nq) +
+                                    ", k=" + std::to_string(k) + " need " +
+                                    std::to_string(L.used + per_split) +
+                                    " bytes of scratch, more than its " +
+                                    std::to_string(kNoAllocScratchBytes) + "-byte limit");
+    L = ScratchLayout{base, 0};
+    fixed(L, &flag, &q, &rowidx, &cscr, &gtau, &gbest);
+    const int64_t max_splits = (int64_t)((kNoAllocScratchBytes - L.used) / per_split);
+
+    int h = 0;  // read-backs land in this thread's own memory (no pinned buffer)
+    PX_TRY(check_finite_into(d_queries, nq * f->dim, flag, &h, s));
+    const float* dq = d_queries;
+    if (pad) {
+        PX_HIP(px::launch_pad_rows(d_queries, nq, (int)f->dim, (int)f->dp, q, s));
+        dq = q;
+    }
+    int64_t n_eff = n;
+    if (masked) PX_TRY(compact_mask_into(d_mask, n, rowidx, cscr, flag + 1, &h, s, &n_eff));
+    ListPlan lp;
+    PX_TRY(plan_list_scan(n_eff, nq, kl, f->dev.cus, &lp, k, max_splits));
+    ListBufs b{L.take<float>((size_t)(nq * lp.splits * kl)), nullptr, gtau, gbest};
+    b.part_i = L.take<int>((size_t)(nq * lp.splits * kl));
+    if (L.used > kNoAllocScratchBytes)
+        return fail(PX_ERR_ARG, "internal: scratch layout past its end");  // unreachable
+    f->last_rounds = 0;
+    f->last_path = PX_PATH_LISTS;
+    return flat_run_lists(f, dq, nq, k, n_eff, masked ? rowidx : nullptr, lp, kl, b, d_ids,
+                          d_dists, 0, false);
 }
 
 int px_flat_get_vectors(const px_flat* cf, int64_t first, int64_t n, float* out) {
