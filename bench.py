@@ -25,6 +25,7 @@ import argparse
 import ctypes
 import json
 import os
+import platform
 import sys
 import time
 
@@ -78,38 +79,89 @@ class Dev:
         self.ptrs = []
 
 
+def host_cpu() -> dict:
+    """The host the CPU baseline ran on: usable CPUs (affinity) and the CPU model."""
+    model = platform.processor() or "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        nproc = os.cpu_count() or 1
+    return {"nproc": nproc, "cpu_model": model}
+
+
 def cpu_baseline(data, queries, k, metric, gpu_ids, gpu_d, budget_s, mask=None, pq=None):
-    """Time the oracle on growing query batches until ~budget_s of CPU work; check parity
-    of the same sample against the GPU results."""
+    """The oracle (the reference's per-query scan restated in C, one query per OpenMP task
+    as rayon's par_chunks_mut in flat.rs:173-181) timed as bench/harness.py:256-265 times
+    the reference: a 64-query warmup, then the median of 7 timed batches. Done twice, on all
+    the host's OpenMP threads and on one thread, each within about budget_s / 2 of CPU
+    time: the batch size comes from the warmup's rate. The 7 batches of each mode are
+    consecutive, distinct query chunks, and every query timed is also checked against the
+    GPU's results (ids exact, distances relative)."""
     import oracle
 
-    threads = oracle.max_threads()
-    done, spent = 0, 0.0
-    batch = 64
-    mism = 0
-    max_rel = 0.0
-    while done < len(queries) and spent < budget_s:
-        b = min(batch, len(queries) - done)
-        qs = queries[done:done + b]
+    nq = len(queries)
+
+    def run(qs, threads):
         t0 = time.perf_counter()
         if pq is None:
-            o_ids, o_d, _ = oracle.flat_search(data, qs, k, metric, mask=mask)
+            r = oracle.flat_search(data, qs, k, metric, mask=mask, nthreads=threads)
         else:
             books, codes = pq
-            o_ids, o_d, _ = oracle.pq_search(books, codes, qs, k, metric, mask=mask)
-        spent += time.perf_counter() - t0
-        g_ids, g_d = gpu_ids[done:done + b], gpu_d[done:done + b]
-        mism += int((g_ids != o_ids).sum())
+            r = oracle.pq_search(books, codes, qs, k, metric, mask=mask, nthreads=threads)
+        return time.perf_counter() - t0, r
+
+    par = {"queries_checked": 0, "id_mismatches": 0, "max_rel_dist_err": 0.0}
+
+    def check(rows, o_ids, o_d):
+        g_ids, g_d = gpu_ids[rows], gpu_d[rows]
+        par["queries_checked"] += len(rows)
+        par["id_mismatches"] += int((g_ids != o_ids).sum())
         ok = o_ids >= 0
         if ok.any():
             r = np.abs(g_d[ok] - o_d[ok]) / np.maximum(np.abs(o_d[ok]), 1e-30)
-            max_rel = max(max_rel, float(r.max()))
-        done += b
-        batch = min(batch * 2, 1024)
-    return {"value": done / spent, "unit": "queries/s", "cores": threads, "kind": "port",
-            "sample": f"first {done} of {len(queries)} queries, full corpus, {threads} threads, "
-                      f"{spent:.1f} s"}, {"queries_checked": done, "id_mismatches": mism,
-                                           "max_rel_dist_err": max_rel}
+            par["max_rel_dist_err"] = max(par["max_rel_dist_err"], float(r.max()))
+
+    nxt = 0  # next query of the batch to time (chunks wrap round a short batch)
+
+    def chunk(size):
+        nonlocal nxt
+        rows = (nxt + np.arange(size)) % nq
+        nxt = (nxt + size) % nq
+        return rows
+
+    def mode(threads, warm):
+        rows = chunk(warm)
+        t, _ = run(queries[rows], threads)
+        per_query = t / warm
+        size = int(max(8, min(nq, (budget_s / 2.0 / 7.0) / max(per_query, 1e-9))))
+        times = []
+        for _ in range(7):
+            rows = chunk(size)
+            t, (o_ids, o_d, _) = run(queries[rows], threads)
+            times.append(t)
+            check(rows, o_ids, o_d)
+        med = float(np.median(times))
+        return size / med, size, med
+
+    threads = oracle.max_threads()
+    mt_qps, mt_size, mt_med = mode(threads, min(64, nq))
+    st_qps, st_size, st_med = mode(1, min(8, nq))
+    host = host_cpu()
+    return {"value": mt_qps, "unit": "queries/s", "cores": threads, "kind": "port",
+            "sample": f"median of 7 batches of {mt_size} queries ({mt_med:.2f} s each) after "
+                      f"a 64-query warmup, full corpus, {threads} OpenMP threads",
+            "single_thread": {"value": st_qps, "unit": "queries/s", "cores": 1,
+                              "sample": f"median of 7 batches of {st_size} queries "
+                                        f"({st_med:.2f} s each) after an 8-query warmup"},
+            "host": {**host, "omp_threads": threads}}, par
 
 
 def read_traffic(name: str, default_workload: bool):
@@ -123,6 +175,53 @@ def read_traffic(name: str, default_workload: bool):
             if line.startswith("hbm_bytes_per_launch:"):
                 return int(float(line.split(":", 1)[1]))
     return None
+
+
+def read_counters(name: str, default_workload: bool):
+    """The `key: value` figures (mfma_busy_frac, lds_busy_frac, shader_clock_ghz, ...) of a
+    committed rocprofv3 counter summary of this workload; None when the run is not that
+    workload or no summary exists."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not name or not default_workload or not os.path.isfile(path):
+        return None
+    out = {}
+    with open(path) as fh:
+        for line in fh:
+            key, sep, val = line.partition(":")
+            if sep and key.replace("_", "").isalnum() and key == key.lower() and " " not in key:
+                try:
+                    out[key] = float(val)
+                except ValueError:
+                    pass
+    out["source"] = f"profiles/{name}"
+    return out
+
+
+# rocprofv3 counter summaries (MFMA busy of the scan; LDS busy of the PQ scan), by the same
+# keys as TRAFFIC_PROFILES
+COUNTER_PROFILES = {
+    (3, 1_000_000, 10_000, 10, "collect-bounded"):
+        "flat_collect_scan_bounded_l2_1Mx128_q10k_k10_mfma_counters.md",
+    (2, 100_000, 1_000, 10, "lists"): "flat_scan_kernel_ip_100kx384_q1k_k10_mfma_counters.md",
+    (5, 10_000_000, 16_384, 100, "collect-sampled"):
+        "flat_collect_scan_ip_10Mx384_q16k_k100_mask10_mfma_counters.md",
+}
+PQ_COUNTER_PROFILE = "pq_scan_kernel_l2_1Mx16_q10k_k10_lds_counters.md"
+
+
+def host_buffer_qps(search, nq, reps=7):
+    """Median of `reps` timed calls of a search from host (numpy) arrays after one warmup:
+    query upload, the device pipeline, result download and the Python surface's checks,
+    as the reference's harness times search_batch (bench/harness.py:256-265)."""
+    out = search()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        out = search()
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": nq / med, "unit": "queries/s", "ms_median": med * 1e3, "reps": reps,
+            "warmup": 1}, out
 
 
 # rocprofv3 summaries whose calibrated FETCH_SIZE + WRITE_SIZE give `traffic`, by
@@ -203,6 +302,16 @@ def bench_flat(args, dev):
         f"pipeline {np.mean(total_ms):.3f} ms, splits {info['splits']}, blocks {info['blocks']}")
     ids = dev.get(di, np.empty((nq, k), dtype=np.int64))
     dists = dev.get(dd, np.empty((nq, k), dtype=np.float32))
+    # the same batch from host arrays through the Python surface (FlatIndex.search_batch)
+    if mask is not None:
+        hb, (h_ids, h_d) = host_buffer_qps(lambda: idx.search_batch_filtered(queries, mask, k=k), nq)
+    else:
+        hb, (h_ids, h_d) = host_buffer_qps(lambda: idx.search_batch(queries, k=k), nq)
+    hb["same_results_as_device_form"] = bool(np.array_equal(h_ids, ids) and
+                                              np.array_equal(h_d.view(np.uint32),
+                                                             dists.view(np.uint32)))
+    log(f"[bench] host-buffer search_batch: {hb['ms_median']:.3f} ms median of 7, "
+        f"{hb['value']:.0f} QPS")
 
     flops = 2.0 * nq * n_eff * dim
     achieved = flops / (np.mean(scan_ms) * 1e-3) / 1e12
@@ -237,7 +346,16 @@ def bench_flat(args, dev):
                      "kernel_ms": float(np.mean(scan_ms)),
                      "algorithmic_flop_per_launch": flops},
         "pipeline_ms": float(np.mean(total_ms)),
+        "host_buffer": hb,
     }
+    ctr = read_counters(COUNTER_PROFILES.get((c, n, nq, k, info["path"]), ""), not args.sift)
+    if ctr and "mfma_busy_frac" in ctr:
+        result["roofline"]["mfma_busy"] = {
+            "frac": ctr["mfma_busy_frac"],
+            "counter": "SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs)",
+            "mfma_flop_per_launch": ctr.get("mfma_flop_per_launch"),
+            "shader_clock_ghz": ctr.get("shader_clock_ghz"),
+            "source": ctr["source"]}
     if args.sift:
         from proxima_amd import datasets
 
@@ -296,6 +414,13 @@ def bench_pq(args, dev):
     elapsed = time.perf_counter() - t0
     ids = dev.get(di, np.empty((nq, k), dtype=np.int64))
     dists = dev.get(dd, np.empty((nq, k), dtype=np.float32))
+    if mask is not None:
+        hb, (h_ids, h_d) = host_buffer_qps(lambda: pq.search_batch_filtered(queries, mask, k=k), nq)
+    else:
+        hb, (h_ids, h_d) = host_buffer_qps(lambda: pq.search_batch(queries, k=k), nq)
+    hb["same_results_as_device_form"] = bool(np.array_equal(h_ids, ids) and
+                                              np.array_equal(h_d.view(np.uint32),
+                                                             dists.view(np.uint32)))
     n_eff = int(mask.sum()) if mask is not None else n
     algo_bytes = nq * (n_eff * m + ((n + 7) // 8 if mask is not None else 0)) + nq * m * 256 * 4
     achieved = algo_bytes / (np.mean(scan_ms) * 1e-3) / 1e9
@@ -316,7 +441,15 @@ def bench_pq(args, dev):
                                              mask is None and (n, nq, k) == (1_000_000, 10_000, 10)),
                      "kernel": "pq_scan_kernel", "kernel_ms": float(np.mean(scan_ms)),
                      "algorithmic_bytes_per_launch": algo_bytes},
+        "host_buffer": hb,
     }
+    ctr = read_counters(PQ_COUNTER_PROFILE,
+                        mask is None and (n, nq, k) == (1_000_000, 10_000, 10))
+    if ctr:
+        result["roofline"]["lds"] = {
+            "busy_frac": ctr.get("lds_busy_frac"),
+            "bank_conflict_cycles_per_lds_cycle": ctr.get("lds_bank_conflict_per_cycle"),
+            "valu_busy_frac": ctr.get("valu_busy_frac"), "source": ctr["source"]}
     if args.cpu_seconds > 0:
         import oracle
 

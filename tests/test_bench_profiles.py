@@ -47,3 +47,25 @@ def test_bench_refuses_more_than_one_gpu(argv, env):
                          text=True, timeout=120, env={**os.environ, **env})
     assert run.returncode == 2
     assert "one GPU only" in run.stderr and run.stdout == ""
+
+
+@pytest.mark.parametrize("name", sorted(set(bench.COUNTER_PROFILES.values())))
+def test_mfma_counter_profile_is_complete(name):
+    text = (PROFILES / name).read_text()
+    assert "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_VALU_MFMA_MOPS_F32" in text
+    ctr = bench.read_counters(name, True)
+    assert 0 < ctr["mfma_busy_frac"] < 1 and ctr["mfma_flop_per_launch"] > 0
+    assert 1.0 < ctr["shader_clock_ghz"] < 2.5
+    assert bench.read_counters(name, False) is None
+
+
+def test_lds_counter_profile_is_complete():
+    text = (PROFILES / bench.PQ_COUNTER_PROFILE).read_text()
+    assert "rocprofv3 --pmc SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT" in text
+    ctr = bench.read_counters(bench.PQ_COUNTER_PROFILE, True)
+    assert 0 < ctr["lds_busy_frac"] < 1 and ctr["lds_bank_conflict_per_cycle"] > 0
+
+
+def test_host_cpu_names_the_host():
+    h = bench.host_cpu()
+    assert h["nproc"] >= 1 and isinstance(h["cpu_model"], str) and h["cpu_model"]
