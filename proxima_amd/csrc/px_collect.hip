@@ -1,0 +1,428 @@
+// px_collect.hip -- the threshold-collect scan of FlatIndex searches for gfx950.
+//
+// Replaces the per-query full scan of crates/core/src/flat.rs:106-148 on the collect path
+// (large k, moderate k on large batches, and the bounded first round of the 1M x 128
+// workload): every row whose MFMA key (||x||^2 - 2 q.x for L2, -q.x for IP) is at or below
+// its query's threshold is appended to a candidate region; flat_collect_select_kernel
+// re-ranks the best k + 8 in the reference's arithmetic (distance.rs:3-39) and finishes.
+//
+// One workgroup = 8 waves = 256 queries (each wave: 32 queries' fragments in registers as
+// the MFMA B operand) x one corpus split. The corpus streams through LDS in stages of 64
+// rows x 128 dims (one tile is ceil(dp / 128) stages).
+//
+// Pipeline. Three LDS stage buffers: stage s reads buffer s % 3 while the global loads of
+// stage s + 2 are in flight in registers; they are written to buffer (s + 2) % 3 after the
+// stage's MFMAs, and one barrier per stage publishes them. Stage s + 1's buffer was
+// therefore complete one barrier earlier, so each wave reads the A operands of stage
+// s + 1's first dim group before it waits at stage s's barrier and issues its first MFMAs
+// straight after it. Two accumulator sets alternate between tiles: while the MFMAs of
+// tile t accumulate into one set, the keys of tile t - 1 are computed from the other, in
+// place, and tested against the thresholds two rows per dim group, between the MFMAs of
+// tile t's first stage; so no wave leaves the matrix unit idle for an epilogue. Each
+// tile's row norms (L2) sit in one of four small LDS buffers, kept until its keys are
+// computed a tile later.
+//
+// Appends go to one of two regions per (query slot, split), one per lane of the pair that
+// holds the query (lanes l and l ^ 32 hold the two halves of the query's 64 rows of a
+// tile), each with its own counter, so appends need no cross-lane step. dense: no
+// thresholds; every key of the split is written to cand_keys [slot][dense_ld] by position
+// (the threshold sample of the sampled path).
+//
+// DYN (unfiltered one-chunk scans with FlatScanArgs::gbest): the splits' shared bound.
+// After each tile a lane publishes the smallest key of its rows of the split so far to
+// slot split % 32 of its query (device-scope atomicMin: a plain store would stay in this
+// XCD's L2); every published slot then has a row of its own splits at or below it, so the
+// kl-th smallest slot bounds the query's best kl, and rows above it are not appended.
+// The bound is refreshed on a geometric schedule of tiles (t -> t + t/2); the refresh's
+// loads are issued at the start of a stage and consumed after its MFMAs. A split's first
+// tile also bounds itself by its own kl-th smallest key (so a query needs no threshold).
+#include "px_device.h"
+#include "px_kernels.h"
+#include "px_scan_common.h"
+
+#include <float.h>
+
+#include <type_traits>
+
+namespace px {
+
+namespace {
+
+constexpr int kStageBufs = 3;  // LDS stage buffers
+constexpr int kNormBufs = 4;   // LDS norm buffers (tile t + 2 is staged while t - 1 is tested)
+
+template <bool L2, bool MULTI, bool FILT, bool DYN, bool FULL>
+__global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
+    constexpr int NT = 512;
+    constexpr int kF4PerRow = kChunk / 4;        // 32 float4 per staged row
+    constexpr int kRowStep = NT / kF4PerRow;     // 16 rows between a thread's loads
+    constexpr int kPF = kTileRows / kRowStep;    // 4 float4 per thread per stage
+    static_assert(NT % kF4PerRow == 0 && kTileRows % kRowStep == 0, "uneven stage split");
+    static_assert(!(DYN && (MULTI || FILT)), "the shared bound serves one-chunk unfiltered scans");
+    __shared__ __attribute__((aligned(16))) float tile[kStageBufs][kTileRows * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float tnorm[kNormBufs][kTileRows];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
+    const int qt = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+    const int slot = qt * 256 + wave * 32 + j;
+    const bool qvalid = slot < a.nq;
+    const int q = a.qlist ? a.qlist[qvalid ? slot : 0] : slot;
+    // positions, tiles and stages fit 32 bits (at most 2^31 - 2 rows; host-checked)
+    const int row0 = (int)((int64_t)split * a.rows_per_split);
+    const int row1 = (int)min(a.n_eff, (int64_t)row0 + a.rows_per_split);
+    const float kInf = __int_as_float(0x7f800000);
+    const int nch = MULTI ? (a.dp + kChunk - 1) / kChunk : 1;
+    const int ntiles = (row1 - row0 + kTileRows - 1) / kTileRows;  // >= 1
+    const int nstages = ntiles * nch;
+    const int cc = tid % kF4PerRow;   // this thread's float4 column of a staged row
+    const int rr0 = tid / kF4PerRow;  // its first row of a stage
+
+    // ---- staging: row ids, global loads held in registers, commit to LDS ----------------
+    // Every load is unconditional with a clamped address (rows past the split's end read
+    // row 0, columns past a chunk's end repeat its last float4): such rows' keys are never
+    // tested or are written as +inf, and such columns are never multiplied (dim groups
+    // past the chunk's end are skipped).
+    int rid[kPF], pid;
+    // (positions past the split's end are formed in 64 bits: near 2^31 rows they overflow)
+    auto tile_ids = [&](int t) __attribute__((always_inline)) {
+        const int64_t t0 = (int64_t)row0 + (int64_t)t * kTileRows;
+#pragma unroll
+        for (int u = 0; u < kPF; ++u) {
+            const int64_t pos = t0 + rr0 + u * kRowStep;
+            const int v = FILT ? a.rowidx[min(pos, (int64_t)row1 - 1)] : (int)pos;
+            rid[u] = pos < row1 ? v : -1;
+        }
+        const int64_t pos = t0 + tid;
+        const int v = FILT ? a.rowidx[min(pos, (int64_t)row1 - 1)] : (int)pos;
+        pid = (tid < kTileRows && pos < row1) ? v : -1;
+    };
+    static_assert(kPF == 4, "four staged float4 per thread");
+    float4 pf0, pf1, pf2, pf3;  // separate variables: an array of them ended up in memory
+    float pn = 0.f;
+    auto fetch = [&](int s) __attribute__((always_inline)) {
+        const int c = MULTI ? (int)(s % nch) : 0;
+        const int f4r = min(kChunk, a.dp - c * kChunk) >> 2;
+        const float* base = a.corpus + c * kChunk + min(cc, f4r - 1) * 4;
+        pf0 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[0], 0) * a.dp);
+        pf1 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[1], 0) * a.dp);
+        pf2 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[2], 0) * a.dp);
+        pf3 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[3], 0) * a.dp);
+        if (L2 && c == 0) pn = a.norms[max(pid, 0)];
+    };
+    auto commit = [&](int s, int buf) __attribute__((always_inline)) {
+        float* tb = tile[buf] + rr0 * kLdsStride + cc * 4;
+        *reinterpret_cast<float4*>(tb) = pf0;
+        *reinterpret_cast<float4*>(tb + kRowStep * kLdsStride) = pf1;
+        *reinterpret_cast<float4*>(tb + 2 * kRowStep * kLdsStride) = pf2;
+        *reinterpret_cast<float4*>(tb + 3 * kRowStep * kLdsStride) = pf3;
+        const int c = MULTI ? (int)(s % nch) : 0;
+        if (L2 && c == 0 && tid < kTileRows) tnorm[(s / nch) & (kNormBufs - 1)][tid] = pn;
+    };
+
+    // prologue: stages 0 and 1 in LDS, ids of the tile of stage 2
+    tile_ids(0);
+    fetch(0);
+    commit(0, 0);
+    tile_ids(1 / nch);
+    fetch(1);
+    commit(1, 1);
+    tile_ids(2 / nch);
+    __syncthreads();
+
+    // A wave whose 32 queries are all padding (last query tile) only helps stage the
+    // corpus: same loads, same barriers.
+    if (qt * 256 + wave * 32 >= a.nq) {
+        int wb = 2;
+        for (int s = 0; s < nstages; ++s) {
+            fetch(s + 2);
+            tile_ids((s + 3) / nch);
+            commit(s + 2, wb);
+            wb = wb == kStageBufs - 1 ? 0 : wb + 1;
+            __syncthreads();
+        }
+        return;
+    }
+
+    // ---- per-query state ----------------------------------------------------------------
+    float cthr = -kInf;  // threshold key (nothing passes -inf: padding slots, dense mode)
+    int cpos = -1;       // threshold position (equal keys pass at positions <= cpos)
+    if (qvalid && !a.dense) {
+        cthr = from_total_key(a.thr_key[q]);
+        cpos = a.thr_pos[q];
+    }
+    float gbound = kInf;  // DYN: the shared bound as last refreshed
+    float ctest = cthr;   // min(cthr, gbound): pre-screen of the key tests
+    int ccount = 0;       // rows appended (or counted past the region's capacity)
+    int* gbest = DYN ? a.gbest + (int64_t)(qvalid ? q : 0) * 32 : nullptr;
+    int cpub = kTotalKeyInf;     // DYN: this lane's published running minimum
+    int next_refresh = 0;        // DYN: tile index of the next refresh
+    float* const creg_k = a.cand_keys + ((int64_t)slot * a.splits + split) * 2 * a.cap +
+                          (int64_t)h * a.cap;
+    int* const creg_p = a.cand_pos + ((int64_t)slot * a.splits + split) * 2 * a.cap +
+                        (int64_t)h * a.cap;
+
+    // one row of the previous tile at or below the pre-screen: the exact test and append.
+    // Past the region's capacity the count still grows (the select sees the overflow) and
+    // the last slot is rewritten, so the region keeps holding cap real candidates.
+    auto test_row = [&](float kv, int pos) __attribute__((always_inline)) {
+        if (((kv < cthr) | ((kv == cthr) & (pos <= cpos))) & (kv <= gbound)) {
+            const int at = min(ccount, a.cap - 1);
+            creg_k[at] = kv;
+            creg_p[at] = pos;
+            ++ccount;
+        }
+    };
+    // keys of a tile from its accumulators, in place: key[x] is row
+    // 32 (x / 16) + mfma_row(x % 16, h) of the tile; L2 drops the per-query ||q||^2 (it does
+    // not change a query's order, and the select re-ranks exactly), IP negates
+    auto key_of = [&](float dot, float nrm) __attribute__((always_inline)) {
+        return L2 ? __builtin_fmaf(-2.0f, dot, nrm) : -dot;
+    };
+    auto all_keys = [&](f32x16 (&acc)[2], const float* tn) __attribute__((always_inline)) {
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+            for (int m4 = 0; m4 < 4; ++m4) {
+                float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (L2) nv = *reinterpret_cast<const float4*>(tn + rb * 32 + 8 * m4 + 4 * h);
+                acc[rb][4 * m4 + 0] = key_of(acc[rb][4 * m4 + 0], nv.x);
+                acc[rb][4 * m4 + 1] = key_of(acc[rb][4 * m4 + 1], nv.y);
+                acc[rb][4 * m4 + 2] = key_of(acc[rb][4 * m4 + 2], nv.z);
+                acc[rb][4 * m4 + 3] = key_of(acc[rb][4 * m4 + 3], nv.w);
+            }
+    };
+    auto as_keys = [](f32x16 (&acc)[2], float (&k)[32]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int x = 0; x < 32; ++x) k[x] = acc[x >> 4][x & 15];
+    };
+    // every key of a tile, row-major by position (+inf past the split's end), so that each
+    // query's keys are contiguous for the ladder: keys 4 m .. 4 m + 3 of a lane are four
+    // consecutive rows
+    auto dense_write = [&](f32x16 (&acc)[2], int t0, int rem) __attribute__((always_inline)) {
+        if (!qvalid) return;
+        float* dst = a.cand_keys + (int64_t)slot * a.dense_ld + t0;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+            float v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int x = 4 * m + e;
+                v[e] = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? acc[x >> 4][x & 15] : kInf;
+            }
+            const int lr = (m >> 2) * 32 + 8 * (m & 3) + 4 * h;
+            *reinterpret_cast<float4*>(dst + lr) = make_float4(v[0], v[1], v[2], v[3]);
+        }
+    };
+    // DYN, a split's first tile (keys in place): its kl-th smallest key bounds the split,
+    // taken where some query of the wave has no threshold (a sampled one already bounds the
+    // first tile far below)
+    auto first_tile_bound = [&](f32x16 (&acc)[2], int rem) __attribute__((always_inline)) {
+        if (__ballot(qvalid && cthr == kInf)) {
+            float k[32];
+            as_keys(acc, k);
+            gbound = fminf(gbound, first_tile_kth(k, rem, qvalid, a.kl));
+        }
+    };
+
+    // query chunk 0 (MFMA B operand): dims past the chunk's end are loaded clamped and never
+    // multiplied; padding query slots load query 0's row and are never tested
+    const float* qrow = a.queries + (int64_t)(qvalid ? q : 0) * a.dp;
+    float4 b[16];
+    {
+        const int dc = min(kChunk, a.dp);
+#pragma unroll
+        for (int g = 0; g < 16; ++g)
+            b[g] = *reinterpret_cast<const float4*>(qrow + min(g * 8 + h * 4, dc - 4));
+    }
+
+    f32x16 accA[2], accB[2];
+    // A operands of the next stage's first dim group (read before each stage's barrier)
+    float4 an0 = *reinterpret_cast<const float4*>(tile[0] + j * kLdsStride + h * 4);
+    float4 an1 = *reinterpret_cast<const float4*>(tile[0] + (32 + j) * kLdsStride + h * 4);
+    int rb_cur = 0;  // LDS buffer of the current stage
+    int s = 0;       // stage index
+
+    // One stage: the MFMAs of chunk c of tile t into cur. TEST (the first stage of tiles
+    // t > 0): the keys of tile t - 1, in prev, computed and tested between them.
+    auto stage = [&](auto test_tag, auto first_tag, int t, int c, f32x16 (&cur)[2],
+                     f32x16 (&prev)[2]) __attribute__((always_inline)) {
+        constexpr bool TEST = decltype(test_tag)::value;
+        const bool first = !MULTI || c == 0;
+        const int rb_nxt = rb_cur == kStageBufs - 1 ? 0 : rb_cur + 1;
+        const int rb_wr = rb_nxt == kStageBufs - 1 ? 0 : rb_nxt + 1;
+        fetch(s + 2);
+        tile_ids((s + 3) / nch);
+        // DYN, the split's first tile (FIRST: t == 1): all its keys and its own bound before
+        // its tests
+        constexpr bool keys_ready = DYN && TEST && decltype(first_tag)::value;
+        const float* tn = tnorm[(t - 1) & (kNormBufs - 1)];
+        if constexpr (keys_ready) {
+            all_keys(prev, tn);
+            first_tile_bound(prev, kTileRows);
+            ctest = fminf(cthr, gbound);
+        }
+        const int pt0 = row0 + (t - 1) * kTileRows;  // first position of tile t - 1
+        float vmin = kInf;  // DYN: smallest key of tile t - 1
+        // dim groups of this chunk (FULL: dp is a multiple of 128, every chunk has 16)
+        const int ng = FULL ? 16 : min(kChunk, a.dp - c * kChunk) >> 3;
+        const int cn = MULTI ? (c + 1 == nch ? 0 : c + 1) : 0;
+        const int dcn = min(kChunk, a.dp - cn * kChunk);
+        const float* ta0 = tile[rb_cur] + j * kLdsStride + h * 4;
+        const float* ta1 = tile[rb_cur] + (32 + j) * kLdsStride + h * 4;
+        float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int g = 0; g < 16; ++g) {
+            if (g < ng) {
+                const float4 x0 = g == 0 ? an0 : *reinterpret_cast<const float4*>(ta0 + g * 8);
+                const float4 x1 = g == 0 ? an1 : *reinterpret_cast<const float4*>(ta1 + g * 8);
+                if (g == 0 && first) {
+                    cur[0] = mfma4z(x0, b[0]);
+                    cur[1] = mfma4z(x1, b[0]);
+                } else {
+                    cur[0] = mfma4(x0, b[g], cur[0]);
+                    cur[1] = mfma4(x1, b[g], cur[1]);
+                }
+            }
+            if constexpr (MULTI)
+                b[g] = *reinterpret_cast<const float4*>(qrow + cn * kChunk +
+                                                        min(g * 8 + h * 4, dcn - 4));
+            if constexpr (TEST) {
+                // rows x = 2g, 2g + 1 of tile t - 1: block rb = g / 8, MFMA rows r, r + 1
+                const int rb = g >> 3, r = (2 * g) & 15;
+                if (!keys_ready) {
+                    if (L2 && (g & 1) == 0)
+                        nv = *reinterpret_cast<const float4*>(tn + rb * 32 + 8 * (r >> 2) + 4 * h);
+                    const float n0 = (g & 1) ? nv.z : nv.x, n1 = (g & 1) ? nv.w : nv.y;
+                    prev[rb][r] = key_of(prev[rb][r], n0);
+                    prev[rb][r + 1] = key_of(prev[rb][r + 1], n1);
+                }
+                const float k0 = prev[rb][r], k1 = prev[rb][r + 1];
+                if constexpr (DYN) vmin = fminf(vmin, fminf(k0, k1));
+                if (__ballot(k0 <= ctest || k1 <= ctest)) {
+                    test_row(k0, pt0 + rb * 32 + mfma_row(r, h));
+                    test_row(k1, pt0 + rb * 32 + mfma_row(r + 1, h));
+                }
+            }
+        }
+        // the stage's LDS commit stays after its MFMAs: the scheduler would otherwise hoist it
+        // (to shorten the prefetch registers' lives) and wait for the global loads there
+        __builtin_amdgcn_sched_barrier(0);
+        bool pub_now = false;
+        if constexpr (TEST) {
+            if constexpr (DYN) {
+                const int tk = total_key(vmin);
+                pub_now = qvalid && tk < cpub;
+                cpub = pub_now ? tk : cpub;
+                if (t - 1 == next_refresh) {
+                    // the query's 32 published slots; their kl-th smallest bounds its best kl
+                    const long long* src = reinterpret_cast<const long long*>(gbest + h * 16);
+                    int v[16];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const long long w =
+                            __hip_atomic_load(src + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        v[2 * u] = (int)(w & 0xffffffffll);
+                        v[2 * u + 1] = (int)(w >> 32);
+                    }
+                    gbound = fminf(gbound, from_total_key(kth_smallest32(v, a.kl)));
+                    next_refresh = (t - 1) + max(1, (t - 1) >> 1);
+                }
+                ctest = fminf(cthr, gbound);
+            }
+            if (a.dense) dense_write(prev, row0 + (t - 1) * kTileRows, kTileRows);
+        }
+        // the next stage's first A operands: its buffer was complete at the last barrier
+        if (s + 1 < nstages) {
+            an0 = *reinterpret_cast<const float4*>(tile[rb_nxt] + j * kLdsStride + h * 4);
+            an1 = *reinterpret_cast<const float4*>(tile[rb_nxt] + (32 + j) * kLdsStride + h * 4);
+        }
+        commit(s + 2, rb_wr);
+        if constexpr (DYN) {
+            // published after the commit, whose waits then do not wait for the atomic
+            if (pub_now) atomicMin(gbest + (split & 31), cpub);
+        }
+        __syncthreads();
+        rb_cur = rb_nxt;
+        ++s;
+    };
+    // a tile: its first stage tests the previous tile (TEST), its other chunks do not
+    auto run_tile = [&](auto test_tag, auto first_tag, int t, f32x16 (&cur)[2],
+                        f32x16 (&prev)[2]) __attribute__((always_inline)) {
+        stage(test_tag, first_tag, t, 0, cur, prev);
+        for (int c = 1; c < nch; ++c) stage(std::false_type{}, std::false_type{}, t, c, cur, prev);
+    };
+    // tile 0; tile 1 (its first stage tests tile 0, the split's first); then pairs
+    run_tile(std::false_type{}, std::false_type{}, 0, accA, accB);
+    if (ntiles > 1) run_tile(std::true_type{}, std::true_type{}, 1, accB, accA);
+    for (int t = 2; t < ntiles; t += 2) {
+        run_tile(std::true_type{}, std::false_type{}, t, accA, accB);
+        if (t + 1 < ntiles) run_tile(std::true_type{}, std::false_type{}, t + 1, accB, accA);
+    }
+
+    // the last tile's keys: all at once, with no MFMAs to hide behind
+    auto finish = [&](f32x16 (&acc)[2]) __attribute__((always_inline)) {
+        const int tl = ntiles - 1;
+        const int t0 = row0 + tl * kTileRows;
+        const int rem = min(row1 - t0, kTileRows);
+        all_keys(acc, tnorm[tl & (kNormBufs - 1)]);
+        if (a.dense) {
+            dense_write(acc, t0, rem);
+            return;
+        }
+        if constexpr (DYN) {
+            if (tl == 0) {
+                first_tile_bound(acc, rem);
+                ctest = fminf(cthr, gbound);
+            }
+            float vmin = kInf;
+#pragma unroll
+            for (int x = 0; x < 32; ++x)
+                vmin = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? fminf(vmin, acc[x >> 4][x & 15])
+                                                                 : vmin;
+            const int tk = total_key(vmin);
+            if (qvalid && tk < cpub) atomicMin(gbest + (split & 31), tk);
+        }
+        const int pt0 = t0;
+#pragma unroll
+        for (int x = 0; x < 32; x += 2) {
+            const float k0 = acc[x >> 4][x & 15], k1 = acc[x >> 4][(x & 15) + 1];
+            const int o0 = (x >> 4) * 32 + mfma_row(x & 15, h);
+            const int o1 = (x >> 4) * 32 + mfma_row((x & 15) + 1, h);
+            if (__ballot((o0 < rem && k0 <= ctest) || (o1 < rem && k1 <= ctest))) {
+                if (o0 < rem) test_row(k0, pt0 + o0);
+                if (o1 < rem) test_row(k1, pt0 + o1);
+            }
+        }
+    };
+    if (ntiles & 1) finish(accA);
+    else finish(accB);
+    if (qvalid && !a.dense) a.cand_count[((int64_t)slot * a.splits + split) * 2 + h] = ccount;
+}
+
+}  // namespace
+
+hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s) {
+    // rows of exactly 128 padded dims (one full chunk: the 1M x 128 workload); other widths
+    // take the collect mode of flat_scan_kernel
+    if (a.dp != kChunk) return launch_flat_collect_v1(a, s);
+    const int64_t qtiles = (a.nq + 255) / 256;
+    const dim3 grid((unsigned)(qtiles * a.splits)), block(512);
+    const bool dyn = a.gbest != nullptr;
+    if (dyn && (a.rowidx || a.dense)) return hipErrorInvalidValue;
+#define PX_COLLECT(L2, FILT, DYN) \
+    hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true>), grid, block, 0, s, a)
+    if (a.metric == 0) {
+        if (a.rowidx) PX_COLLECT(true, true, false);
+        else if (dyn) PX_COLLECT(true, false, true);
+        else PX_COLLECT(true, false, false);
+    } else {
+        if (a.rowidx) PX_COLLECT(false, true, false);
+        else if (dyn) PX_COLLECT(false, false, true);
+        else PX_COLLECT(false, false, false);
+    }
+#undef PX_COLLECT
+    return hipGetLastError();
+}
+
+}  // namespace px

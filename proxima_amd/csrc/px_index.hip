@@ -924,14 +924,15 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     if (!vec_collect(nq, f->dp)) {
         // the first round bounds itself: per region (one lane of a split) up to k' rows of
         // the split's first tile and a few after it, twice over (a split that starts ahead
-        // of the others of its query tile scans a few tiles before their minima arrive),
-        // and at least 2 k' + 1 (an overflowing region holds enough to tighten from)
+        // of the others of its query tile scans a few tiles before their minima arrive, and
+        // a split publishes a tile's minimum while it scans the next), and at least
+        // 2 k' + 1 (an overflowing region holds enough to tighten from)
         j.bound_only = collect_bound_only(n_eff, nq, j.kk, f->dp, cus, rowidx != nullptr);
         if (j.bound_only) f->last_path = PX_PATH_COLLECT_BOUNDED;
         int64_t splits = 1, rps = 64;
         collect_splits(n_eff, nq, cus, &splits, &rps);
         j.bound_expect = (double)(2 * splits) *
-                         (double)std::max<int64_t>(2 * (j.kk + 32), 2 * j.kk + 1) / 3.0;
+                         (double)std::max<int64_t>(2 * (j.kk + 48), 2 * j.kk + 1) / 3.0;
     }
     j.sel.rowidx = rowidx;
     j.sel.k = (int)k;

@@ -63,6 +63,7 @@ constexpr int kTotalKeyInf = 0x7f800000;
 // sample of rows spread evenly over the corpus, one collect scan, per-query select; queries whose threshold proved too
 // tight or too loose go round again.
 hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s);
+hipError_t launch_flat_collect_v1(const FlatScanArgs& a, hipStream_t s);
 // The collect scan for a few query slots (nq <= kVecQueries, dp <= kVecMaxDp) on the
 // vector ALUs: the MFMA scan's 32-query tiles would be nearly all padding, so this one
 // streams the corpus at memory speed instead. One region per (slot, split):

@@ -1,0 +1,121 @@
+// px_scan_common.h -- device pieces shared by the MFMA scans of FlatIndex searches
+// (px_flat.hip: per-split lists; px_collect.hip: threshold collect), gfx950, wave64.
+#pragma once
+
+#include "px_device.h"
+
+namespace px {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+constexpr int kTileRows = 64;            // corpus rows per tile: two 32-row MFMA blocks
+constexpr int kChunk = 128;              // dims per staged K-chunk (16 groups of 8)
+constexpr int kLdsStride = kChunk + 4;   // row pitch in LDS; +4 floats keeps b128 reads conflict-free
+
+// v_mfma_f32_32x32x2f32 result layout: lane l, register r holds D[i][j] with
+// j = l % 32 and i = 8 * (r / 4) + 4 * (l / 32) + r % 4.
+__device__ __forceinline__ int mfma_row(int r, int h) { return 8 * (r >> 2) + 4 * h + (r & 3); }
+
+__device__ __forceinline__ f32x16 mfma4(float4 a, float4 b, f32x16 c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, c, 0, 0, 0);
+    return c;
+}
+
+// Total-order int of a key (flat.rs:30's f32::total_cmp) and back; the mapping is its own
+// inverse. Shared thresholds are published as these ints with atomicMin.
+__device__ __forceinline__ float from_total_key(int t) {
+    return __int_as_float(t ^ (int)(((unsigned)(t >> 31)) >> 1));
+}
+
+// fp32 MFMA tiles starting from zero accumulators.
+__device__ __forceinline__ f32x16 mfma4z(float4 a, float4 b) {
+    const f32x16 z = {0.f};
+    f32x16 c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, b.x, z, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, b.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, b.z, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, b.w, c, 0, 0, 0);
+    return c;
+}
+
+// rank-th smallest (1-based, rank <= 32) of the 32 ints held as v[0..15] by this lane and
+// by lane ^ 32; both lanes return it. Bitonic: sort 16 in registers, split the union into
+// its 16 smallest and 16 largest with the partner's list reversed, sort those halves.
+__device__ __forceinline__ int kth_smallest32(int (&v)[16], int rank) {
+#pragma unroll
+    for (int k = 2; k <= 16; k <<= 1)
+#pragma unroll
+        for (int s = k >> 1; s > 0; s >>= 1)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int l = i ^ s;
+                if (l > i) {
+                    const int mn = min(v[i], v[l]), mx = max(v[i], v[l]);
+                    const bool up = (i & k) == 0;
+                    v[i] = up ? mn : mx;
+                    v[l] = up ? mx : mn;
+                }
+            }
+    // only the half holding the answer is kept (rank is uniform across the wave)
+    const bool low = rank <= 16;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int p = __shfl_xor(v[15 - i], 32);
+        v[i] = low ? min(v[i], p) : max(v[i], p);
+    }
+#pragma unroll
+    for (int s = 8; s > 0; s >>= 1)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int l = i ^ s;
+            if (l > i) {
+                const int mn = min(v[i], v[l]), mx = max(v[i], v[l]);
+                v[i] = mn;
+                v[l] = mx;
+            }
+        }
+    const int want = low ? rank - 1 : rank - 17;
+    int r = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) r = i == want ? v[i] : r;
+    return r;
+}
+
+// kl-th smallest (kl <= 64) key of the 64 rows a lane pair holds for query j in the first
+// tile of a split (key[x] is row 32 (x / 16) + mfma_row(x % 16, h)); rows at or past rem,
+// and padding queries, do not count. +inf when fewer than kl rows count. kl rounds of
+// "smallest remaining" over the pair, as in first_tile_lists, keeping only the value.
+__device__ __forceinline__ float first_tile_kth(const float (&key)[32], int rem, bool qvalid,
+                                                int kl) {
+    constexpr int kNoKey = 0x7fffffff;
+    const int h = lane_id() >> 5;
+    int tk[32];
+#pragma unroll
+    for (int x = 0; x < 32; ++x) {
+        const int off = (x >> 4) * 32 + mfma_row(x & 15, h);
+        tk[x] = (qvalid && off < rem) ? total_key(key[x]) : kNoKey;
+    }
+    int last = kNoKey;
+    for (int r = 0; r < kl; ++r) {
+        int bt = kNoKey, bx = 0;
+#pragma unroll
+        for (int x = 0; x < 32; ++x) {
+            const bool lt = tk[x] < bt;
+            bt = lt ? tk[x] : bt;
+            bx = lt ? x : bx;
+        }
+        const int pt = __shfl_xor(bt, 32);
+        // equal minima: the h == 0 lane's goes first (the partner agrees)
+        const bool mine = bt < pt || (bt == pt && h == 0);
+        last = mine ? bt : pt;
+        if (__ballot(last != kNoKey) == 0) break;  // no query has a row left
+#pragma unroll
+        for (int x = 0; x < 32; ++x) tk[x] = (mine && x == bx) ? kNoKey : tk[x];
+    }
+    return last == kNoKey ? __int_as_float(0x7f800000) : from_total_key(last);
+}
+
+}  // namespace px
