@@ -314,6 +314,9 @@ def bench_flat(args, dev):
         f"{hb['value']:.0f} QPS")
 
     flops = 2.0 * nq * n_eff * dim
+    # rows of exactly 128 padded dims take flat_collect_kernel, other widths the collect mode
+    # of flat_scan_kernel
+    collect_kernel = "flat_collect_kernel" if (dim + 7) // 8 * 8 == 128 else "flat_scan_kernel"
     achieved = flops / (np.mean(scan_ms) * 1e-3) / 1e12
     headline = (c, n, nq, k) == (3, 1_000_000, 10_000, 10) and not args.sift
     desc = (f"FlatIndex exact {'L2' if l2 else 'inner product'}, corpus {n} x {dim} fp32 "
@@ -333,9 +336,9 @@ def bench_flat(args, dev):
                      "traffic": read_traffic(TRAFFIC_PROFILES.get((c, n, nq, k, info["path"]), ""),
                                              not args.sift),
                      "kernel": {"lists": "flat_scan_kernel (per-split lists)",
-                                "collect-sampled": "flat_scan_kernel (threshold-collect: sample "
+                                "collect-sampled": f"{collect_kernel} (threshold-collect: sample "
                                                    "scan, ladder and collect scan)",
-                                "collect-bounded": "flat_scan_kernel (threshold-collect: "
+                                "collect-bounded": f"{collect_kernel} (threshold-collect: "
                                                    "collect scan bounded by the splits' shared "
                                                    "bound, no sample)",
                                 "vector": "flat_vcollect_kernel (vector-ALU collect: sample "

@@ -64,7 +64,11 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
-    const int qt = blockIdx.x / a.splits, split = blockIdx.x % a.splits;
+    // query tiles in reverse launch order: the last (partial) tile, whose workgroups run
+    // fastest, starts in the first round of workgroups with all its splits together, so
+    // none of them scans far ahead of the others' shared bound
+    const int qtiles = gridDim.x / a.splits;
+    const int qt = qtiles - 1 - (int)(blockIdx.x / a.splits), split = blockIdx.x % a.splits;
     const int slot = qt * 256 + wave * 32 + j;
     const bool qvalid = slot < a.nq;
     const int q = a.qlist ? a.qlist[qvalid ? slot : 0] : slot;
