@@ -897,6 +897,20 @@ hipError_t launch_fill_int(int* p, int64_t n, int v, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Device ints to mapped pinned host memory by plain stores (a stream-ordered read-back that
+// takes no copy engine).
+__global__ void copy_to_host_kernel(const int* src, int* dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+hipError_t launch_copy_to_host(const int* src, int* host_dst, int64_t n, hipStream_t s) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(copy_to_host_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
+                       src, host_dst, n);
+    return hipGetLastError();
+}
+
 // In-LDS bitonic sort (ascending by (key total-order, id)) of p = 2^x entries.
 __device__ void bitonic_sort(float* sk, int* si, int p) {
     for (int size = 2; size <= p; size <<= 1) {

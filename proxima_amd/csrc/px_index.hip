@@ -124,8 +124,13 @@ struct Workspace {
     DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
     DevBuf qraw;             // host-path queries before padding to dp
     DevBuf sort_scratch;     // k past PX_MAX_K: sort keys, positions, radix-sort storage
-    int* h_count = nullptr;  // pinned
-    int* h_status = nullptr; // pinned, h_status_cap ints
+    // Read-backs of the search path (pinned, mapped, coherent): written by a kernel
+    // (launch_copy_to_host) through their device addresses *_dev, read by the host after
+    // the stream drains
+    int* h_count = nullptr;      // one int
+    int* h_count_dev = nullptr;
+    int* h_status = nullptr;     // h_status_cap ints
+    int* h_status_dev = nullptr;
     int64_t h_status_cap = 0;
     // pinned staging for the host-buffer entry points: queries in, results out (pageable
     // copies are staged by the runtime, and 2-D ones row by row)
@@ -142,17 +147,27 @@ struct Workspace {
         cap = want;
         return PX_OK;
     }
+    static int mapped_ints(int** host, int** dev, int64_t n) {
+        PX_HIP(hipHostMalloc(reinterpret_cast<void**>(host), sizeof(int) * std::max<int64_t>(n, 1),
+                             hipHostMallocMapped | hipHostMallocCoherent));
+        const hipError_t e = hipHostGetDevicePointer(reinterpret_cast<void**>(dev), *host, 0);
+        if (e != hipSuccess) {
+            (void)hipHostFree(*host);
+            *host = *dev = nullptr;
+            PX_HIP(e);
+        }
+        return PX_OK;
+    }
     int ensure_pinned() {
-        if (!h_count) PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_count), sizeof(int)));
+        if (!h_count) PX_TRY(mapped_ints(&h_count, &h_count_dev, 1));
         return PX_OK;
     }
     int ensure_status(int64_t n) {
         if (n <= h_status_cap) return PX_OK;
         if (h_status) (void)hipHostFree(h_status);
-        h_status = nullptr;
+        h_status = h_status_dev = nullptr;
         h_status_cap = 0;
-        PX_HIP(hipHostMalloc(reinterpret_cast<void**>(&h_status),
-                             sizeof(int) * std::max<int64_t>(n, 1)));
+        PX_TRY(mapped_ints(&h_status, &h_status_dev, n));
         h_status_cap = n;
         return PX_OK;
     }
@@ -162,9 +177,9 @@ struct Workspace {
                           &cand_k, &cand_p, &cand_n, &samp_row, &qlist, &sort_scratch})
             b->release();
         if (h_count) (void)hipHostFree(h_count);
-        h_count = nullptr;
+        h_count = h_count_dev = nullptr;
         if (h_status) (void)hipHostFree(h_status);
-        h_status = nullptr;
+        h_status = h_status_dev = nullptr;
         h_status_cap = 0;
         qraw.release();
         if (h_in) (void)hipHostFree(h_in);
@@ -205,15 +220,22 @@ int download_results(Workspace& ws, int64_t nq, int64_t k, hipStream_t s, int64_
     return PX_OK;
 }
 
-// Compacts a device keep-mask into ascending row ids; returns the kept count in *n_eff.
+// One device int read back into h: by a kernel when h is mapped pinned memory (h_dev its
+// device address), else (the caller's own memory) by a copy. Waits for the stream.
+int read_back_int(const int* d, int* h, int* h_dev, hipStream_t s) {
+    if (h_dev) PX_HIP(px::launch_copy_to_host(d, h_dev, 1, s));
+    else PX_HIP(hipMemcpyAsync(h, d, sizeof(int), hipMemcpyDeviceToHost, s));
+    PX_HIP(hipStreamSynchronize(s));
+    return PX_OK;
+}
+
 // Compacts a device keep-mask of n rows into ascending row ids (rowidx, n ints; cscr,
 // mask_compact_scratch(n) ints; d_count one int) and reads the kept count back through
-// h_count (host memory: pinned, or the caller's own).
+// h_count (read_back_int); returns it in *n_eff.
 int compact_mask_into(const uint8_t* d_mask, int64_t n, int* rowidx, int* cscr, int* d_count,
-                      int* h_count, hipStream_t s, int64_t* n_eff) {
+                      int* h_count, int* h_count_dev, hipStream_t s, int64_t* n_eff) {
     PX_HIP(px::launch_mask_compact(d_mask, n, rowidx, cscr, d_count, s));
-    PX_HIP(hipMemcpyAsync(h_count, d_count, sizeof(int), hipMemcpyDeviceToHost, s));
-    PX_HIP(hipStreamSynchronize(s));
+    PX_TRY(read_back_int(d_count, h_count, h_count_dev, s));
     *n_eff = *h_count;
     return PX_OK;
 }
@@ -225,18 +247,18 @@ int compact_mask(Workspace& ws, const uint8_t* d_mask, int64_t n, hipStream_t s,
     PX_TRY(ws.count.reserve(sizeof(int)));
     PX_TRY(ws.ensure_pinned());
     PX_TRY(compact_mask_into(d_mask, n, ws.rowidx.as<int>(), ws.scratch.as<int>(),
-                             ws.count.as<int>(), ws.h_count, s, n_eff));
+                             ws.count.as<int>(), ws.h_count, ws.h_count_dev, s, n_eff));
     *rowidx = ws.rowidx.as<int>();
     return PX_OK;
 }
 
 // Device queries (count floats) must be finite, as flat.rs:114-117 asserts of every query:
 // checked on the device (d_flag, one int), and the host waits for the answer (read through
-// h_flag) before any search kernel runs.
-int check_finite_into(const float* d_x, int64_t count, int* d_flag, int* h_flag, hipStream_t s) {
+// h_flag, read_back_int) before any search kernel runs.
+int check_finite_into(const float* d_x, int64_t count, int* d_flag, int* h_flag, int* h_flag_dev,
+                      hipStream_t s) {
     PX_HIP(px::launch_nonfinite_check(d_x, count, d_flag, s));
-    PX_HIP(hipMemcpyAsync(h_flag, d_flag, sizeof(int), hipMemcpyDeviceToHost, s));
-    PX_HIP(hipStreamSynchronize(s));
+    PX_TRY(read_back_int(d_flag, h_flag, h_flag_dev, s));
     if (*h_flag)
         return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
     return PX_OK;
@@ -245,7 +267,7 @@ int check_finite_into(const float* d_x, int64_t count, int* d_flag, int* h_flag,
 int check_device_finite(Workspace& ws, const float* d_x, int64_t count, hipStream_t s) {
     PX_TRY(ws.count.reserve(sizeof(int)));
     PX_TRY(ws.ensure_pinned());
-    return check_finite_into(d_x, count, ws.count.as<int>(), ws.h_count, s);
+    return check_finite_into(d_x, count, ws.count.as<int>(), ws.h_count, ws.h_count_dev, s);
 }
 
 // Number of corpus splits: enough workgroups to fill the GPU several times over, each
@@ -627,7 +649,7 @@ int run_collect(CollectJob& j) {
             if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[2], s));
             done += take;
         }
-        PX_HIP(hipMemcpyAsync(h_status, ws.status.p, sizeof(int) * nq, hipMemcpyDeviceToHost, s));
+        PX_HIP(px::launch_copy_to_host(ws.status.as<int>(), ws.h_status_dev, nq, s));
         PX_HIP(hipStreamSynchronize(s));
         // queries of this round still open
         std::vector<int> next;
@@ -1368,9 +1390,6 @@ int pq_run_collect_batch(px_pq* p, const float* d_q, int64_t nq, int64_t k, int6
         a.cand_pos = ws.cand_p.as<int>();
         a.cand_count = ws.cand_n.as<int>();
         a.cap = (int)*cap;
-        // drained first, as the flat collect scan (1M x 16-byte codes, 10,000 queries,
-        // k = 1000: the second search 34.1 ms against 31.1 without the wait)
-        PX_HIP(hipStreamSynchronize(s));
         PX_HIP(px::launch_pq_collect(a, s));
         if (round == 0) {
             p->timing.splits = (int)splits;
@@ -1706,14 +1725,15 @@ int px_flat_search_device_noalloc(const px_flat* cf, const float* d_queries, int
     const int64_t max_splits = (int64_t)((kNoAllocScratchBytes - L.used) / per_split);
 
     int h = 0;  // read-backs land in this thread's own memory (no pinned buffer)
-    PX_TRY(check_finite_into(d_queries, nq * f->dim, flag, &h, s));
+    PX_TRY(check_finite_into(d_queries, nq * f->dim, flag, &h, nullptr, s));
     const float* dq = d_queries;
     if (pad) {
         PX_HIP(px::launch_pad_rows(d_queries, nq, (int)f->dim, (int)f->dp, q, s));
         dq = q;
     }
     int64_t n_eff = n;
-    if (masked) PX_TRY(compact_mask_into(d_mask, n, rowidx, cscr, flag + 1, &h, s, &n_eff));
+    if (masked)
+        PX_TRY(compact_mask_into(d_mask, n, rowidx, cscr, flag + 1, &h, nullptr, s, &n_eff));
     ListPlan lp;
     PX_TRY(plan_list_scan(n_eff, nq, kl, f->dev.cus, &lp, k, max_splits));
     ListBufs b{L.take<float>((size_t)(nq * lp.splits * kl)), nullptr, gtau, gbest};

@@ -137,6 +137,12 @@ hipError_t launch_ladder(const LadderArgs& a, hipStream_t s);
 hipError_t launch_sample_rows(const int* rowidx, int64_t count, int64_t n_eff, int* row,
                               hipStream_t s);
 hipError_t launch_fill_int(int* p, int64_t n, int v, hipStream_t s);
+// n ints from device memory to host memory that is pinned and mapped for the device
+// (hipHostMallocMapped), by a kernel on stream s: the host reads them once the stream has
+// drained. A hipMemcpyAsync to the host may instead be given to a copy engine whose queue the
+// runtime creates on first use, and creating a queue preempts the kernels running on the
+// device; this read-back never does.
+hipError_t launch_copy_to_host(const int* src, int* host_dst, int64_t n, hipStream_t s);
 
 struct MergeArgs {
     const float* part_keys;  // [nq][width] candidates (key, id/position)

@@ -384,10 +384,9 @@ def test_bound_only_overflow_and_ties(gpu):
 
 
 def test_bound_only_consecutive_searches(gpu):
-    # The shared-bound slots are not reset between searches: each launch takes a new epoch
-    # and slots of earlier epochs read as +inf. Five searches in a row on one handle, the
-    # query sets alternating (a stale slot of the other set would drop true neighbours),
-    # each exact.
+    # The shared-bound slots are refilled with +inf before every launch, which no longer
+    # waits for the stream to drain. Five searches in a row on one handle, the query sets
+    # alternating (a stale slot of the other set would drop true neighbours), each exact.
     data = datagen.sift_like(40_000, 64, 70)
     qa = datagen.sift_like(2048, 64, 71)
     qb = datagen.sift_like(2048, 64, 72) // 4
