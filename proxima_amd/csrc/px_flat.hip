@@ -130,6 +130,7 @@ __device__ __forceinline__ void first_tile_lists(const float (&key)[32], int64_t
 // the epilogue together, so an epilogue of its own would leave the matrix unit idle).
 template <int KP, int WAVES, bool L2, bool MULTI, bool FILT, bool COLLECT = false>
 __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
+    if (a.abort && *a.abort == a.abort_seq) return;
     constexpr int NT = WAVES * 64;
     constexpr int kF4PerRow = kChunk / 4;                  // 32 float4 per staged row
     constexpr int kRowStep = NT / kF4PerRow;               // rows between a thread's loads
@@ -315,8 +316,9 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     float4 pf[kPF];
     float pn = 0.f;
     unsigned pvalid = 0;  // bit u: pf[u] is a real row's data; bit kPF: pn is a real norm
-    auto fetch = [&](int64_t s) {
-        const int c = MULTI ? (int)(s % nch) : 0;
+    // (stages are addressed by chunk c and tile parity, kept incrementally: a 64-bit division
+    // of the stage index by the chunk count costs dozens of scalar instructions a stage)
+    auto fetch = [&](int c) {
         const int f4r = min(kChunk, a.dp - c * kChunk) >> 2;
         pvalid = 0;
 #pragma unroll
@@ -330,15 +332,20 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             pvalid |= pid >= 0 ? 1u << kPF : 0u;
         }
     };
-    auto commit = [&](int64_t s) {
-        float* tb = tile[s & 1];
+    // stage buffer sb, chunk c, tile parity tp
+    auto commit = [&](int sb, int c, int tp) {
+        float* tb = tile[sb];
 #pragma unroll
         for (int u = 0; u < kPF; ++u)
             *reinterpret_cast<float4*>(tb + (rr0 + u * kRowStep) * kLdsStride + cc * 4) =
                 zero_unless((pvalid >> u) & 1u, pf[u]);
-        const int c = MULTI ? (int)(s % nch) : 0;
         if (L2 && c == 0 && tid < kTileRows)
-            tnorm[(s / nch) & 1][tid] = (pvalid >> kPF) & 1u ? pn : 0.f;
+            tnorm[tp][tid] = (pvalid >> kPF) & 1u ? pn : 0.f;
+    };
+    // chunk and tile of the stage after one of chunk c and tile t
+    auto next_stage = [&](int c, int64_t t, int& cn, int64_t& tn) {
+        cn = c + 1 == nch ? 0 : c + 1;
+        tn = cn == 0 ? t + 1 : t;
     };
 
     float4 b[16];
@@ -348,7 +355,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     if (nstages > 0) {
         tile_ids(0);
         fetch(0);
-        commit(0);
+        commit(0, 0, 0);
         tile_ids(nch > 1 ? 0 : 1);  // ids for the tile of stage 1
     }
     __syncthreads();
@@ -358,10 +365,18 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         // corpus: same loads, same barriers, no MFMAs, no selection. A separate loop, so
         // that the live waves' code is the one the full batches run.
         if (qt * (WAVES * 32) + wave * 32 >= a.nq) {
+            int c = 0;
+            int64_t t = 0;
             for (int64_t s = 0; s < nstages; ++s) {
-                fetch(s + 1);
-                tile_ids((s + 2) / nch);
-                commit(s + 1);
+                int c1, c2;
+                int64_t t1, t2;
+                next_stage(c, t, c1, t1);
+                next_stage(c1, t1, c2, t2);
+                fetch(c1);
+                tile_ids(t2);
+                commit((int)((s + 1) & 1), c1, (int)(t1 & 1));
+                c = c1;
+                t = t1;
                 __syncthreads();
             }
             return;
@@ -369,21 +384,25 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     }
 
     f32x16 acc0 = {0.f}, acc1 = {0.f};
+    int c = 0;        // chunk of stage s
+    int64_t ti = 0;   // its tile
     for (int64_t s = 0; s < nstages; ++s) {
-        const int c = MULTI ? (int)(s % nch) : 0;
-        const int64_t t0 = row0 + (s / nch) * kTileRows;
+        int c1, c2;
+        int64_t t1, t2;
+        next_stage(c, ti, c1, t1);
+        next_stage(c1, t1, c2, t2);
+        const int64_t t0 = row0 + ti * kTileRows;
         int gt_raw = kTotalKeyInf;
         if constexpr (!COLLECT)
             gt_raw = __hip_atomic_load(gtau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int64_t ti = s / nch;
         // MULTI: each b[g] takes the next stage's query chunk as soon as this stage's MFMAs
         // have read it. Those loads are not zeroed past the chunk's end or for padding
         // queries: the corpus tile is zero in columns past the chunk's end, every value is
         // finite, and padding queries' keys are never used.
-        const int cn = MULTI ? (c + 1) % nch : 0;
+        const int cn = c1;
         const int dcn = min(kChunk, a.dp - cn * kChunk);
-        fetch(s + 1);  // past the last stage every row is -1: harmless clamped loads
-        tile_ids((s + 2) / nch);  // ids for the tile of stage s + 2
+        fetch(c1);  // past the last stage every row is -1: harmless clamped loads
+        tile_ids(t2);  // ids for the tile of stage s + 2
         if (c == 0) {
             acc0 = (f32x16){0.f};
             acc1 = (f32x16){0.f};
@@ -428,7 +447,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             // the merge re-ranks exactly), so key = ||x||^2 - 2 q.x; IP key = -q.x.
             // (collect mode writes them straight into pkey, where the next tile's MFMA loop
             // tests them: the previous tile's keys there have been tested already)
-            const float* tn = tnorm[(s / nch) & 1];
+            const float* tn = tnorm[ti & 1];
             float key_own[COLLECT ? 1 : 32];
             auto& key = [&]() -> float(&)[32] {
                 if constexpr (COLLECT) return pkey;
@@ -616,12 +635,14 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             }  // !COLLECT
         }
 
-        commit(s + 1);
+        commit((int)((s + 1) & 1), c1, (int)(t1 & 1));
         if (dyn && pub_now) {
             atomicMin(gbest + (split & 31), cpub);
             pub_now = false;
         }
         __syncthreads();
+        c = c1;
+        ti = t1;
     }
 
     if constexpr (COLLECT) {
@@ -943,6 +964,7 @@ constexpr int kMergeFiltered = 256;
 // tail can be among the best kl. PQ lists publish no bounds; their kl-th smallest list
 // head serves instead.
 __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
+    if (a.abort && *a.abort == a.abort_seq) return;
     extern __shared__ __attribute__((aligned(16))) char msmem[];
     __shared__ int s_n;
     int p = 1;
@@ -1434,6 +1456,29 @@ hipError_t launch_nonfinite_check(const float* x, int64_t count, int* flag, hipS
     if (e != hipSuccess || count <= 0) return e;
     const int64_t blocks = std::min<int64_t>((count + 255) / 256, 2048);
     hipLaunchKernelGGL(nonfinite_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, count, flag);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void list_prologue_kernel(const float* x, int64_t count,
+                                                            int* flag, int seq, int* gtau,
+                                                            int64_t ngtau, int* gbest,
+                                                            int64_t ngbest) {
+    const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    bool bad = false;
+    for (int64_t i = i0; i < count; i += step)
+        bad |= (__float_as_uint(x[i]) & 0x7f800000u) == 0x7f800000u;
+    for (int64_t i = i0; i < ngtau; i += step) gtau[i] = kTotalKeyInf;
+    for (int64_t i = i0; i < ngbest; i += step) gbest[i] = kTotalKeyInf;
+    if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) atomicMax(flag, seq);
+}
+
+hipError_t launch_list_prologue(const float* x, int64_t count, int* flag, int seq, int* gtau,
+                                int64_t ngtau, int* gbest, int64_t ngbest, hipStream_t s) {
+    const int64_t most = std::max<int64_t>({count, ngtau, ngbest, (int64_t)1});
+    const int64_t blocks = std::min<int64_t>((most + 255) / 256, 2048);
+    hipLaunchKernelGGL(list_prologue_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, count,
+                       flag, seq, gtau, ngtau, gbest, ngbest);
     return hipGetLastError();
 }
 

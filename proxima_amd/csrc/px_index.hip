@@ -13,6 +13,7 @@
 
 #include <algorithm>
 #include <cfloat>
+#include <climits>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -122,6 +123,8 @@ struct Workspace {
     DevBuf q, qn, mask, rowidx, scratch, count, part_k, part_i, out_ids, out_d, gtau, gbest;
     // collect path (k' past the lists)
     DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
+    DevBuf fflag;            // finiteness verdicts of list-path searches (next_finite_seq)
+    int fseq = 0;
     DevBuf qraw;             // host-path queries before padding to dp
     DevBuf sort_scratch;     // k past PX_MAX_K: sort keys, positions, radix-sort storage
     // Read-backs of the search path (pinned, mapped, coherent): written by a kernel
@@ -174,8 +177,9 @@ struct Workspace {
     void release() {
         for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids,
                           &out_d, &gtau, &gbest, &thr_k, &thr_p, &lad_k, &lad_p, &rung, &status,
-                          &cand_k, &cand_p, &cand_n, &samp_row, &qlist, &sort_scratch})
+                          &cand_k, &cand_p, &cand_n, &samp_row, &qlist, &sort_scratch, &fflag})
             b->release();
+        fseq = 0;
         if (h_count) (void)hipHostFree(h_count);
         h_count = h_count_dev = nullptr;
         if (h_status) (void)hipHostFree(h_status);
@@ -261,6 +265,33 @@ int check_finite_into(const float* d_x, int64_t count, int* d_flag, int* h_flag,
     PX_TRY(read_back_int(d_flag, h_flag, h_flag_dev, s));
     if (*h_flag)
         return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
+    return PX_OK;
+}
+
+int nonfinite_error() {
+    return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
+}
+
+// The device queries of a search whose finiteness check has not run yet (x: count floats).
+// The per-split list path checks them in its first kernel, hands the verdict to its scan
+// and merge (which do nothing for a failed search) and reads it back with its last wait;
+// every other path checks them first (check_device_finite).
+struct PendingCheck {
+    const float* x;
+    int64_t count;
+};
+
+// The sequence number of a list-path search's finiteness check: its flag (ws.fflag) holds
+// the largest number of a search that failed, so no search clears it. Cleared on first use
+// and when the numbers wrap.
+int next_finite_seq(Workspace& ws, hipStream_t s, int* seq) {
+    PX_TRY(ws.fflag.reserve(sizeof(int)));
+    PX_TRY(ws.ensure_pinned());
+    if (ws.fseq <= 0 || ws.fseq == INT_MAX) {
+        PX_HIP(px::launch_fill_int(ws.fflag.as<int>(), 1, 0, s));
+        ws.fseq = 0;
+    }
+    *seq = ++ws.fseq;
     return PX_OK;
 }
 
@@ -1032,12 +1063,22 @@ struct ListBufs {
 // handle's HIP events (created beforehand).
 int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
                    const int* rowidx, const ListPlan& lp, int kl, const ListBufs& b,
-                   int64_t* d_ids, float* d_out, int raw_keys, bool timed) {
+                   int64_t* d_ids, float* d_out, int raw_keys, bool timed,
+                   const PendingCheck* chk = nullptr) {
     hipStream_t s = f->stream;
     const int splits = lp.splits;
     const int64_t rps = lp.rps, groups = lp.groups;
-    PX_HIP(px::launch_fill_int(b.gtau, nq, px::kTotalKeyInf, s));
-    PX_HIP(px::launch_fill_int(b.gbest, nq * 32, px::kTotalKeyInf, s));
+    int seq = 0;
+    const int* d_flag = nullptr;
+    if (chk) {
+        PX_TRY(next_finite_seq(f->ws, s, &seq));
+        d_flag = f->ws.fflag.as<int>();
+        PX_HIP(px::launch_list_prologue(chk->x, chk->count, f->ws.fflag.as<int>(), seq, b.gtau,
+                                        nq, b.gbest, nq * 32, s));
+    } else {
+        PX_HIP(px::launch_fill_int(b.gtau, nq, px::kTotalKeyInf, s));
+        PX_HIP(px::launch_fill_int(b.gbest, nq * 32, px::kTotalKeyInf, s));
+    }
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[0], s));
 
     px::FlatScanArgs a{};
@@ -1056,6 +1097,8 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     a.part_ids = b.part_i;
     a.gtau = b.gtau;
     a.gbest = b.gbest;
+    a.abort = d_flag;
+    a.abort_seq = seq;
     if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[1], s));
 
@@ -1078,9 +1121,13 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     mg.out_ids = d_ids;
     mg.out_dists = d_out;
     mg.raw_keys = raw_keys;
+    mg.abort = d_flag;
+    mg.abort_seq = seq;
     PX_HIP(px::launch_merge(mg, s));
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[2], s));
+    if (d_flag) PX_HIP(px::launch_copy_to_host(d_flag, f->ws.h_count_dev, 1, s));
     PX_HIP(hipStreamSynchronize(s));
+    if (d_flag && *f->ws.h_count == seq) return nonfinite_error();
     if (timed) {
         PX_HIP(hipEventElapsedTime(&f->timing.scan_ms, f->timing.ev[0], f->timing.ev[1]));
         PX_HIP(hipEventElapsedTime(&f->timing.total_ms, f->timing.ev[0], f->timing.ev[2]));
@@ -1091,16 +1138,27 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
 }
 
 // Runs the device pipeline. d_q: [nq][dp] on device. Outputs on device.
+// chk: device queries whose finiteness check has not run yet (PendingCheck), or null.
 int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
-             int64_t* d_ids, float* d_out, int raw_keys) {
+             int64_t* d_ids, float* d_out, int raw_keys, const PendingCheck* chk = nullptr) {
     Workspace& ws = f->ws;
     hipStream_t s = f->stream;
     int64_t n_eff = f->d_rows;
     const int* rowidx = nullptr;
-    if (d_mask) PX_TRY(compact_mask(ws, d_mask, f->d_rows, s, &n_eff, &rowidx));
+    auto check_now = [&]() -> int {
+        if (!chk) return PX_OK;
+        const PendingCheck c = *chk;
+        chk = nullptr;
+        return check_device_finite(ws, c.x, c.count, s);
+    };
+    if (d_mask) {
+        PX_TRY(check_now());
+        PX_TRY(compact_mask(ws, d_mask, f->d_rows, s, &n_eff, &rowidx));
+    }
     f->last_rounds = 0;
     f->last_path = PX_PATH_LISTS;
     if (k > PX_MAX_K) {
+        PX_TRY(check_now());
         f->last_path = PX_PATH_FULL_SORT;
         return run_full_sort(ws, s, f->timing, nq, k, n_eff, rowidx, f->smetric, raw_keys,
                              [&](int64_t q0, int qc, float* keys) -> int {
@@ -1119,8 +1177,10 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
         (k >= collect_from_k() && nq >= kCollectMinQueries && !lists_beat_sample(n_eff, kk, f->dp)) ||
         vec_collect(nq, f->dp) ||
         collect_bound_only(n_eff, nq, kk, f->dp, std::max(f->dev.cus, 1), rowidx != nullptr);
-    if (collect && n_eff > 0)
+    if (collect && n_eff > 0) {
+        PX_TRY(check_now());
         return flat_run_collect(f, d_q, nq, k, n_eff, rowidx, d_ids, d_out, raw_keys);
+    }
 
     const int kl = (int)std::min<int64_t>(px::kMaxList, k + kReRankMargin);
     ListPlan lp;
@@ -1132,7 +1192,7 @@ int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t*
     PX_TRY(f->timing.ensure());
     ListBufs b{ws.part_k.as<float>(), ws.part_i.as<int>(), ws.gtau.as<int>(), ws.gbest.as<int>()};
     return flat_run_lists(f, d_q, nq, k, n_eff, rowidx, lp, kl, b, d_ids, d_out, raw_keys,
-                          f->timing.enabled);
+                          f->timing.enabled, chk);
 }
 
 void host_padding(int metric, int64_t nq, int64_t k, int64_t* ids, float* out, int raw_keys) {
@@ -1663,14 +1723,14 @@ int px_flat_search_device(const px_flat* cf, const float* d_queries, int64_t nq,
     f->smetric = f->metric;
     PX_TRY(flat_bind(f));
     PX_TRY(flat_sync(f));
-    PX_TRY(check_device_finite(f->ws, d_queries, nq * f->dim, f->stream));
+    const PendingCheck chk{d_queries, nq * f->dim};
     const float* q = d_queries;
     if (f->dp != f->dim) {
         PX_TRY(f->ws.q.reserve(sizeof(float) * nq * f->dp));
         PX_HIP(px::launch_pad_rows(d_queries, nq, (int)f->dim, (int)f->dp, f->ws.q.as<float>(), f->stream));
         q = f->ws.q.as<float>();
     }
-    return flat_run(f, q, nq, k, f->d_rows ? d_mask : nullptr, d_ids, d_dists, 0);
+    return flat_run(f, q, nq, k, f->d_rows ? d_mask : nullptr, d_ids, d_dists, 0, &chk);
 }
 
 int px_flat_search_device_noalloc(const px_flat* cf, const float* d_queries, int64_t nq,

@@ -51,6 +51,10 @@ struct FlatScanArgs {
     // (keys of rows past a split's end are +inf; dense_ld >= splits * rows_per_split)
     int dense;
     int64_t dense_ld;
+    // optional: one device int; equal to abort_seq when the scan starts (a query of this
+    // search failed its finiteness check), it makes the whole launch a no-op
+    const int* abort;
+    int abort_seq;
 };
 
 // Waves per workgroup and list capacity used for a list length kl.
@@ -173,6 +177,8 @@ struct MergeArgs {
     int64_t* out_ids;        // [nq][k], -1 padding
     float* out_dists;        // [nq][k] finished (sqrt / negate) or raw keys when raw_keys
     int raw_keys;            // 1: write raw keys (FLT_MAX padding) instead of distances
+    const int* abort;        // optional, as FlatScanArgs::abort: equal to abort_seq, nothing
+    int abort_seq;           // is written
 };
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 
@@ -182,6 +188,12 @@ hipError_t launch_pad_rows(const float* src, int64_t rows, int dim, int dp, floa
 
 // *flag = 1 when any of x[0 .. count) is NaN or infinite, else 0 (the flag is cleared first).
 hipError_t launch_nonfinite_check(const float* x, int64_t count, int* flag, hipStream_t s);
+// The per-split list path's first kernel: *flag = max(*flag, seq) when any of count floats
+// of x is NaN or infinite (flag is never cleared: each search takes a larger seq), and
+// gtau[0..ngtau) and gbest[0..ngbest) filled with kTotalKeyInf. One launch where a flag
+// fill, the check and two fills took four.
+hipError_t launch_list_prologue(const float* x, int64_t count, int* flag, int seq, int* gtau,
+                                int64_t ngtau, int* gbest, int64_t ngbest, hipStream_t s);
 
 // Ordered compaction of a keep-mask (nonzero = keep) into ascending row ids.
 // scratch must hold mask_compact_scratch(n) ints; *d_count receives the kept count.

@@ -276,6 +276,62 @@ def test_device_pointer_entry(gpu):
             lib.px_dev_free(p)
 
 
+@pytest.mark.parametrize("nq,k,masked,path", [
+    (200, 10, False, "lists"),   # the check is read back with the search's last wait
+    (200, 10, True, "lists"),    # a filter: resolved before the mask is compacted
+    (2048, 10, False, "collect-bounded"),
+    (300, 200, False, "collect-sampled"),
+    (5, 10, False, "vector"),
+])
+def test_device_query_nonfinite_leaves_outputs(gpu, nq, k, masked, path):
+    # flat.rs:114-117 rejects a NaN or infinite query before searching: the device form
+    # returns PX_ERR_NONFINITE with the outputs unwritten, whichever path the batch takes,
+    # and the next, finite batch is searched normally
+    lib = _lib.load()
+    data = datagen.gaussian(40_000, 64, 44)
+    q = datagen.gaussian(nq, 64, 45)
+    mask = datagen.mask(40_000, 0.5, 46) if masked else None
+    idx = FlatIndex(64, Metric.L2)
+    idx.add(data)
+    ptrs = []
+
+    def dev(arr):
+        p = ctypes.c_void_p()
+        assert lib.px_dev_alloc(ctypes.byref(p), max(arr.nbytes, 1)) == 0
+        ptrs.append(p)
+        assert lib.px_dev_upload(p, arr.ctypes.data, arr.nbytes) == 0
+        return p
+
+    try:
+        sentinel_i = np.full((nq, k), 1234567, dtype=np.int64)
+        sentinel_d = np.full((nq, k), 7.5, dtype=np.float32)
+        di, dd = dev(sentinel_i), dev(sentinel_d)
+        dm = dev(mask.view(np.uint8)) if masked else None
+        for bad in (np.nan, np.inf, -np.inf):
+            qb = q.copy()
+            qb[nq // 2, 17] = bad
+            print(f"case nonfinite device query nq={nq} k={k} masked={masked} {bad}", flush=True)
+            rc = lib.px_flat_search_device(idx._h, dev(qb), nq, k, dm, di, dd)
+            assert rc == _lib.PX_ERR_NONFINITE, (rc, _lib.last_error())
+            got_i, got_d = np.empty_like(sentinel_i), np.empty_like(sentinel_d)
+            assert lib.px_dev_download(got_i.ctypes.data, di, got_i.nbytes) == 0
+            assert lib.px_dev_download(got_d.ctypes.data, dd, got_d.nbytes) == 0
+            assert np.array_equal(got_i, sentinel_i) and np.array_equal(got_d, sentinel_d)
+        assert lib.px_flat_search_device(idx._h, dev(q), nq, k, dm, di, dd) == 0, _lib.last_error()
+        ids, dist = np.empty_like(sentinel_i), np.empty_like(sentinel_d)
+        assert lib.px_dev_download(ids.ctypes.data, di, ids.nbytes) == 0
+        assert lib.px_dev_download(dist.ctypes.data, dd, dist.nbytes) == 0
+        if masked:
+            h_ids, h_d = idx.search_batch_filtered(q, mask, k=k)
+        else:
+            h_ids, h_d = idx.search_batch(q, k=k)
+        assert np.array_equal(ids, h_ids) and np.array_equal(dist, h_d)
+        assert idx._last_timing()["path"] == path
+    finally:
+        for p in ptrs:
+            lib.px_dev_free(p)
+
+
 @pytest.mark.parametrize("k", [24, 25, 48, 49, 112, 113, 120])
 def test_list_capacity_boundaries(gpu, k):
     # k' = k + 8 crosses the list classes (32 int ids | 56 and 120 with 16-bit offsets | 128)
