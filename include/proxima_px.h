@@ -96,8 +96,8 @@ int px_flat_search(const px_flat* idx, const float* queries, int64_t nq, int64_t
  * Same search with every pointer in device memory of the index's GPU (queries nq x dim,
  * mask px_flat_size() bytes or NULL, outputs nq * k). Synchronous. No host copies: the
  * form for callers that keep queries and results resident in HBM. The queries are checked
- * on the device before any search kernel runs: NaN or infinite values return
- * PX_ERR_NONFINITE, as the host form (flat.rs:114-117).
+ * on the device before any search work: NaN or infinite values return PX_ERR_NONFINITE with
+ * the outputs unwritten, as the host form (flat.rs:114-117).
  */
 int px_flat_search_device(const px_flat* idx, const float* d_queries, int64_t nq, int64_t k,
                           const uint8_t* d_mask, int64_t* d_ids, float* d_dists);

@@ -20,6 +20,7 @@
 #include <functional>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 namespace {
@@ -50,22 +51,66 @@ bool all_finite(const float* x, int64_t len) {
     return true;
 }
 
+// The library's own device allocations (not the caller's px_dev_* buffers, nor the static
+// array of the no-allocation entry point) go through dev_malloc / dev_free, which keep
+// their total. PX_DEVICE_BUDGET (bytes, read at every allocation) caps it: an allocation
+// that would pass the cap fails with hipErrorOutOfMemory, as on a full device -- how the
+// out-of-memory paths are tested.
+std::mutex g_alloc_mu;
+std::unordered_map<void*, size_t> g_alloc_sizes;
+int64_t g_alloc_total = 0;
+
+hipError_t dev_malloc(void** p, size_t bytes) {
+    *p = nullptr;
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    if (const char* e = std::getenv("PX_DEVICE_BUDGET")) {
+        char* end = nullptr;
+        const long long budget = std::strtoll(e, &end, 10);
+        if (end != e && g_alloc_total + (int64_t)bytes > budget) return hipErrorOutOfMemory;
+    }
+    const hipError_t r = hipMalloc(p, bytes);
+    if (r == hipSuccess) {
+        g_alloc_sizes[*p] = bytes;
+        g_alloc_total += (int64_t)bytes;
+    }
+    return r;
+}
+
+void dev_free(void* p) {
+    if (!p) return;
+    (void)hipFree(p);
+    std::lock_guard<std::mutex> lock(g_alloc_mu);
+    const auto it = g_alloc_sizes.find(p);
+    if (it != g_alloc_sizes.end()) {
+        g_alloc_total -= (int64_t)it->second;
+        g_alloc_sizes.erase(it);
+    }
+}
+
+template <class T>
+hipError_t dev_malloc(T** p, size_t bytes) {
+    void* v = nullptr;
+    const hipError_t r = dev_malloc(&v, bytes);
+    *p = static_cast<T*>(v);
+    return r;
+}
+
 // Grow-only device buffer.
 struct DevBuf {
     void* p = nullptr;
     size_t cap = 0;
     int reserve(size_t bytes) {
         if (bytes <= cap) return PX_OK;
-        if (p) (void)hipFree(p);
+        dev_free(p);
         p = nullptr;
         cap = 0;
         const size_t want = std::max<size_t>(bytes, 256);
-        PX_HIP(hipMalloc(&p, want));
+        PX_HIP(dev_malloc(&p, want));
         cap = want;
         return PX_OK;
     }
     void release() {
-        if (p) (void)hipFree(p);
+        dev_free(p);
         p = nullptr;
         cap = 0;
     }
@@ -449,10 +494,10 @@ int flat_sync(px_flat* f) {
     if (need > f->d_cap) {
         const int64_t cap = std::max<int64_t>({need, f->d_cap * 2, 1024});
         float *nx = nullptr, *nn = nullptr;
-        PX_HIP(hipMalloc(&nx, sizeof(float) * cap * f->dp));
-        if (hipMalloc(&nn, sizeof(float) * cap) != hipSuccess) {
-            (void)hipFree(nx);
-            return fail(hipErrorOutOfMemory, "hipMalloc of the corpus norms failed");
+        PX_HIP(dev_malloc(&nx, sizeof(float) * cap * f->dp));
+        if (dev_malloc(&nn, sizeof(float) * cap) != hipSuccess) {
+            dev_free(nx);
+            return fail(hipErrorOutOfMemory, "device allocation of the corpus norms failed");
         }
         if (f->d_rows) {
             PX_HIP(hipMemcpyAsync(nx, f->d_x, sizeof(float) * f->d_rows * f->dp,
@@ -461,8 +506,8 @@ int flat_sync(px_flat* f) {
                                   hipMemcpyDeviceToDevice, f->stream));
         }
         PX_HIP(hipStreamSynchronize(f->stream));
-        if (f->d_x) (void)hipFree(f->d_x);
-        if (f->d_norm) (void)hipFree(f->d_norm);
+        dev_free(f->d_x);
+        dev_free(f->d_norm);
         f->d_x = nx;
         f->d_norm = nn;
         f->d_cap = cap;
@@ -1251,7 +1296,7 @@ int pq_bind(px_pq* p) {
 int pq_sync(px_pq* p) {
     PX_TRY(pq_bind(p));
     if (!p->books_on_device) {
-        if (!p->d_books) PX_HIP(hipMalloc(&p->d_books, sizeof(float) * p->codebooks.size()));
+        if (!p->d_books) PX_HIP(dev_malloc(&p->d_books, sizeof(float) * p->codebooks.size()));
         PX_HIP(hipMemcpyAsync(p->d_books, p->codebooks.data(), sizeof(float) * p->codebooks.size(),
                               hipMemcpyHostToDevice, p->stream));
         PX_HIP(hipStreamSynchronize(p->stream));
@@ -1262,12 +1307,12 @@ int pq_sync(px_pq* p) {
     if (p->n > p->d_cap) {
         const int64_t cap = std::max<int64_t>({p->n, p->d_cap * 2, 4096});
         uint8_t* nc = nullptr;
-        PX_HIP(hipMalloc(&nc, (size_t)(cap * p->m)));
+        PX_HIP(dev_malloc(&nc, (size_t)(cap * p->m)));
         if (p->d_rows)
             PX_HIP(hipMemcpyAsync(nc, p->d_codes, (size_t)(p->d_rows * p->m),
                                   hipMemcpyDeviceToDevice, p->stream));
         PX_HIP(hipStreamSynchronize(p->stream));
-        if (p->d_codes) (void)hipFree(p->d_codes);
+        dev_free(p->d_codes);
         p->d_codes = nc;
         p->d_cap = cap;
     }
@@ -1281,11 +1326,9 @@ int pq_sync(px_pq* p) {
 // Device buffer owned by one call.
 struct TmpBuf {
     void* p = nullptr;
-    ~TmpBuf() {
-        if (p) (void)hipFree(p);
-    }
+    ~TmpBuf() { dev_free(p); }
     int alloc(size_t bytes) {
-        PX_HIP(hipMalloc(&p, std::max<size_t>(bytes, 16)));
+        PX_HIP(dev_malloc(&p, std::max<size_t>(bytes, 16)));
         return PX_OK;
     }
     template <class T>
@@ -1668,8 +1711,8 @@ void px_flat_destroy(px_flat* f) {
     if (f->dev.device >= 0) {
         (void)hipSetDevice(f->dev.device);
         if (f->stream) (void)hipStreamSynchronize(f->stream);
-        if (f->d_x) (void)hipFree(f->d_x);
-        if (f->d_norm) (void)hipFree(f->d_norm);
+        dev_free(f->d_x);
+        dev_free(f->d_norm);
         f->ws.release();
         f->timing.destroy();
         if (f->stream) (void)hipStreamDestroy(f->stream);
@@ -1942,8 +1985,8 @@ void px_pq_destroy(px_pq* p) {
     if (p->dev.device >= 0) {
         (void)hipSetDevice(p->dev.device);
         if (p->stream) (void)hipStreamSynchronize(p->stream);
-        if (p->d_books) (void)hipFree(p->d_books);
-        if (p->d_codes) (void)hipFree(p->d_codes);
+        dev_free(p->d_books);
+        dev_free(p->d_codes);
         p->ws.release();
         p->timing.destroy();
         if (p->stream) (void)hipStreamDestroy(p->stream);
