@@ -14,6 +14,9 @@ from ctypes import c_uint8, c_uint64, c_void_p
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libproxima_px.so")
+# the same library with the kernels' index checks compiled in (-DPX_DEBUG): a failed check
+# fails the search with PX_ERR_ARG naming its file and line
+DEBUG_LIB_PATH = os.path.join(_HERE, "libproxima_px_debug.so")
 
 PX_OK = 0
 PX_ERR_BAD_K = -1
@@ -98,12 +101,18 @@ def load() -> ctypes.CDLL:
         raise ImportError(
             f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
             "g.build()'` or `make -C proxima_amd/csrc` (hipcc --offload-arch=gfx950)")
-    lib = ctypes.CDLL(LIB_PATH)
+    _lib = load_path(LIB_PATH)
+    return _lib
+
+
+def load_path(path: str) -> ctypes.CDLL:
+    """A build of the library at `path` (e.g. DEBUG_LIB_PATH) with the signatures set; a
+    separate handle with its own state, loaded beside the default one."""
+    lib = ctypes.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
-    _lib = lib
     return lib
 
 

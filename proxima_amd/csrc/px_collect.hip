@@ -75,6 +75,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     // positions, tiles and stages fit 32 bits (at most 2^31 - 2 rows; host-checked)
     const int row0 = (int)((int64_t)split * a.rows_per_split);
     const int row1 = (int)min(a.n_eff, (int64_t)row0 + a.rows_per_split);
+    PX_DCHECK(a.dbg, kDbgCollect, row0 < row1 && (int64_t)qtiles * a.splits == (int64_t)gridDim.x);
     const float kInf = __int_as_float(0x7f800000);
     const int nch = MULTI ? (a.dp + kChunk - 1) / kChunk : 1;
     const int ntiles = (row1 - row0 + kTileRows - 1) / kTileRows;  // >= 1
@@ -96,6 +97,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
             const int64_t pos = t0 + rr0 + u * kRowStep;
             const int v = FILT ? a.rowidx[min(pos, (int64_t)row1 - 1)] : (int)pos;
             rid[u] = pos < row1 ? v : -1;
+            PX_DCHECK(a.dbg, kDbgCollect, pos >= row1 || (v >= 0 && v < a.rows));
         }
         const int64_t pos = t0 + tid;
         const int v = FILT ? a.rowidx[min(pos, (int64_t)row1 - 1)] : (int)pos;
@@ -172,6 +174,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     auto test_row = [&](float kv, int pos) __attribute__((always_inline)) {
         if (((kv < cthr) | ((kv == cthr) & (pos <= cpos))) & (kv <= gbound)) {
             const int at = min(ccount, a.cap - 1);
+            PX_DCHECK(a.dbg, kDbgCollect, qvalid && at >= 0 && pos >= row0 && pos < row1);
             creg_k[at] = kv;
             creg_p[at] = pos;
             ++ccount;
@@ -205,6 +208,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     // consecutive rows
     auto dense_write = [&](f32x16 (&acc)[2], int t0, int rem) __attribute__((always_inline)) {
         if (!qvalid) return;
+        PX_DCHECK(a.dbg, kDbgCollect, t0 >= 0 && (int64_t)t0 + kTileRows <= a.dense_ld);
         float* dst = a.cand_keys + (int64_t)slot * a.dense_ld + t0;
 #pragma unroll
         for (int m = 0; m < 8; ++m) {

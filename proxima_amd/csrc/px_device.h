@@ -6,6 +6,23 @@
 
 namespace px {
 
+// Index checks of the debug build (-DPX_DEBUG, libproxima_px_debug.so). A failed check does
+// not trap: the first failure's file and line (file_id * 100000 + line) are recorded in the
+// launch's debug word (dbg, one device int the host clears before a search and reads after
+// it), and the search fails with PX_ERR_ARG naming them. In the product build the checks
+// compile to nothing.
+#ifdef PX_DEBUG
+#define PX_DCHECK(dbg, file_id, cond)                                          \
+    do {                                                                       \
+        if ((dbg) != nullptr && !(cond)) atomicCAS((dbg), 0, (file_id) * 100000 + __LINE__); \
+    } while (0)
+#else
+#define PX_DCHECK(dbg, file_id, cond) \
+    do {                              \
+    } while (0)
+#endif
+constexpr int kDbgFlat = 1, kDbgCollect = 2, kDbgPq = 3;
+
 // Id sentinel for an empty list slot. Real ids (row numbers or compacted positions)
 // are < 2^31 - 1, so the sentinel sorts after every real candidate of equal key.
 constexpr int kIdNone = 0x7fffffff;

@@ -215,6 +215,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             const bool p = off < prem && (kv < cthr || (kv == cthr && pt0 + off <= cpos)) &&
                            kv <= gbound;
             if (p) {
+                PX_DCHECK(a.dbg, kDbgFlat, qvalid && pt0 + off < a.n_eff);
                 if (ccount < a.cap) {
                     const int64_t at =
                         (((int64_t)slot * a.splits + split) * 2 + h) * a.cap + ccount;
@@ -308,6 +309,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             const int64_t pos = t0 + rr0 + u * kRowStep;
             const int v = FILT ? a.rowidx[min(pos, row1 - 1)] : (int)pos;
             rid[u] = pos < row1 ? v : -1;
+            PX_DCHECK(a.dbg, kDbgFlat, pos >= row1 || (v >= 0 && v < a.rows));
         }
         const int64_t pos = t0 + tid;
         const int v = FILT ? a.rowidx[min(pos, row1 - 1)] : (int)pos;
@@ -669,6 +671,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         for (int s = lane; s < a.kl; s += 64) {
             pk[s] = lkeys[wave][ql][s];
             pi[s] = id_load(lids[wave][ql][s], (int)row0);
+            PX_DCHECK(a.dbg, kDbgFlat, pi[s] == kIdNone || (pi[s] >= row0 && pi[s] < row1));
         }
     }
 }
@@ -1019,6 +1022,7 @@ __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
             if (id != kIdNone && total_key(kv) <= bound) {
                 const int at = atomicAdd(&s_n, 1);
                 if (a.rowidx) id = a.rowidx[id];
+                PX_DCHECK(a.dbg, kDbgFlat, at < p && id >= 0);
                 sk[at] = kv;  // at < width <= p
                 si[at] = id;
             }
@@ -1210,6 +1214,7 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
     }
     for (int r = t >> 4; r < a.regions; r += nt >> 4) {
         const int n_r = s_off[r + 1] - s_off[r];
+        PX_DCHECK(a.dbg, kDbgFlat, n_r >= 0 && n_r <= a.cap && s_off[r + 1] <= a.lcap);
         const float* rkr = rk + (int64_t)r * a.cap;
         const int* rpr = rp + (int64_t)r * a.cap;
         for (int c = t & 15; c < n_r; c += 16) {

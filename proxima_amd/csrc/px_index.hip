@@ -39,6 +39,15 @@ int fail(int code, const std::string& msg) {
             return fail((int)e_, std::string(#expr) + " failed: " + hipGetErrorString(e_)); \
     } while (0)
 
+// Host-side index checks of the launch geometry (cheap, always on): a failure is a bug in
+// this library, reported as PX_ERR_ARG naming the condition and line, before any launch.
+#define PX_INTERNAL(cond)                                                                   \
+    do {                                                                                    \
+        if (!(cond))                                                                        \
+            return fail(PX_ERR_ARG, std::string("internal check failed: ") + #cond +        \
+                                        " (px_index.hip:" + std::to_string(__LINE__) + ")"); \
+    } while (0)
+
 #define PX_TRY(expr)             \
     do {                         \
         int rc_ = (expr);        \
@@ -170,6 +179,8 @@ struct Workspace {
     DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
     DevBuf fflag;            // finiteness verdicts of list-path searches (next_finite_seq)
     int fseq = 0;
+    DevBuf dbgw;             // debug build: the debug word of the kernels' index checks ...
+    int* dbg = nullptr;      // ... while a search runs (null in the product build)
     DevBuf qraw;             // host-path queries before padding to dp
     DevBuf sort_scratch;     // k past PX_MAX_K: sort keys, positions, radix-sort storage
     // Read-backs of the search path (pinned, mapped, coherent): written by a kernel
@@ -222,7 +233,8 @@ struct Workspace {
     void release() {
         for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids,
                           &out_d, &gtau, &gbest, &thr_k, &thr_p, &lad_k, &lad_p, &rung, &status,
-                          &cand_k, &cand_p, &cand_n, &samp_row, &qlist, &sort_scratch, &fflag})
+                          &cand_k, &cand_p, &cand_n, &samp_row, &qlist, &sort_scratch, &fflag,
+                          &dbgw})
             b->release();
         fseq = 0;
         if (h_count) (void)hipHostFree(h_count);
@@ -338,6 +350,41 @@ int next_finite_seq(Workspace& ws, hipStream_t s, int* seq) {
     }
     *seq = ++ws.fseq;
     return PX_OK;
+}
+
+#ifdef PX_DEBUG
+constexpr bool kDebugBuild = true;
+#else
+constexpr bool kDebugBuild = false;
+#endif
+
+// Debug build (-DPX_DEBUG): a search runs between debug_begin, which clears the debug word
+// that the kernels' index checks (PX_DCHECK) record a failure in, and debug_end, which
+// reads it and fails the search with PX_ERR_ARG naming the check's file and line.
+int debug_begin(Workspace& ws, hipStream_t s) {
+    if (!kDebugBuild) return PX_OK;
+    PX_TRY(ws.dbgw.reserve(sizeof(int)));
+    PX_TRY(ws.ensure_pinned());
+    PX_HIP(px::launch_fill_int(ws.dbgw.as<int>(), 1, 0, s));
+    ws.dbg = ws.dbgw.as<int>();
+    return PX_OK;
+}
+
+int read_back_int(const int* d, int* h, int* h_dev, hipStream_t s);
+
+int debug_end(Workspace& ws, hipStream_t s, int rc) {
+    if (!kDebugBuild || !ws.dbg) return rc;
+    int* d = ws.dbg;
+    ws.dbg = nullptr;
+    if (rc != PX_OK) return rc;
+    PX_TRY(read_back_int(d, ws.h_count, ws.h_count_dev, s));
+    const int v = *ws.h_count;
+    if (v == 0) return PX_OK;
+    static const char* const files[] = {"?", "px_flat.hip", "px_collect.hip", "px_pq.hip"};
+    const int fid = v / 100000;
+    return fail(PX_ERR_ARG, std::string("device index check failed at ") +
+                                files[fid >= 1 && fid <= 3 ? fid : 0] + ":" +
+                                std::to_string(v % 100000));
 }
 
 int check_device_finite(Workspace& ws, const float* d_x, int64_t count, hipStream_t s) {
@@ -705,7 +752,10 @@ int run_collect(CollectJob& j) {
             // CU where 64 KB let two (more than 4,096 candidates counts as an overflow)
             if (j.sel_gbest) lcap = std::max<int64_t>(std::min<int64_t>(lcap, 4096), 2 * kk + 1);
 
+            PX_INTERNAL(lcap >= 1 && lcap <= px::kMaxCollect && (lcap & (lcap - 1)) == 0);
+            PX_INTERNAL((size_t)(take * regions) * 4 <= ws.cand_n.cap);
             px::CollectSelectArgs c = j.sel;
+            c.dbg = ws.dbg;
             c.cand_keys = ws.cand_k.as<float>();
             c.cand_pos = ws.cand_p.as<int>();
             c.cand_count = ws.cand_n.as<int>();
@@ -852,6 +902,8 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             rps = std::max<int64_t>((rps + 63) / 64 * 64, 64);
             PX_TRY(ws.cand_k.reserve(sizeof(float) * nq * S));
             px::FlatScanArgs a{};
+            a.dbg = f->ws.dbg;
+            a.rows = f->d_rows;
             a.corpus = f->d_x;
             a.norms = f->d_norm;
             a.queries = d_q;
@@ -891,6 +943,8 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             return fail(PX_ERR_ARG, "internal: threshold sample too large for the ladder");
         PX_TRY(ws.cand_k.reserve(sizeof(float) * nq * ld));
         px::FlatScanArgs a{};
+        a.dbg = f->ws.dbg;
+        a.rows = f->d_rows;
         a.corpus = f->d_x;
         a.norms = f->d_norm;
         a.queries = d_q;
@@ -936,6 +990,8 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * *regions * *cap));
             PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * *regions));
             px::FlatScanArgs a{};
+            a.dbg = f->ws.dbg;
+            a.rows = f->d_rows;
             a.corpus = f->d_x;
             a.norms = f->d_norm;
             a.queries = d_q;
@@ -974,7 +1030,13 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         PX_TRY(ws.cand_k.reserve(sizeof(float) * slots * *regions * *cap));
         PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * *regions * *cap));
         PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * *regions));
+        // every split is non-empty, two regions each, and the launch's regions fit
+        PX_INTERNAL(splits * rps >= n_eff && (splits - 1) * rps < n_eff);
+        PX_INTERNAL(*regions == 2 * splits && *regions <= px::kMaxCollectRegions);
+        PX_INTERNAL(*cap >= 1 && (size_t)(slots * *regions * *cap) * 4 <= ws.cand_k.cap);
         px::FlatScanArgs a{};
+        a.dbg = f->ws.dbg;
+        a.rows = f->d_rows;
         a.corpus = f->d_x;
         a.norms = f->d_norm;
         a.queries = d_q;
@@ -1127,6 +1189,8 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[0], s));
 
     px::FlatScanArgs a{};
+    a.dbg = f->ws.dbg;
+    a.rows = f->d_rows;
     a.corpus = f->d_x;
     a.norms = f->d_norm;
     a.queries = d_q;
@@ -1147,7 +1211,9 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[1], s));
 
+    PX_INTERNAL(n_eff == 0 || ((int64_t)splits * rps >= n_eff && (int64_t)splits * kl <= px::kMaxMerge));
     px::MergeArgs mg{};
+    mg.dbg = f->ws.dbg;
     mg.part_keys = a.part_keys;
     mg.part_ids = a.part_ids;
     mg.rowidx = rowidx;
@@ -1183,9 +1249,19 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
 }
 
 // Runs the device pipeline. d_q: [nq][dp] on device. Outputs on device.
+int flat_run_paths(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
+                   int64_t* d_ids, float* d_out, int raw_keys, const PendingCheck* chk);
+
 // chk: device queries whose finiteness check has not run yet (PendingCheck), or null.
 int flat_run(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
              int64_t* d_ids, float* d_out, int raw_keys, const PendingCheck* chk = nullptr) {
+    PX_TRY(debug_begin(f->ws, f->stream));
+    return debug_end(f->ws, f->stream,
+                     flat_run_paths(f, d_q, nq, k, d_mask, d_ids, d_out, raw_keys, chk));
+}
+
+int flat_run_paths(px_flat* f, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
+                   int64_t* d_ids, float* d_out, int raw_keys, const PendingCheck* chk) {
     Workspace& ws = f->ws;
     hipStream_t s = f->stream;
     int64_t n_eff = f->d_rows;
@@ -1407,6 +1483,8 @@ int pq_run_collect_batch(px_pq* p, const float* d_q, int64_t nq, int64_t k, int6
     const int64_t qpb = px::pq_queries_per_block((int)p->m, (int)p->ks);
     auto base_args = [&]() {
         px::PqScanArgs a{};
+        a.dbg = p->ws.dbg;
+        a.rows = p->d_rows;
         a.codes = p->d_codes;
         a.codebooks = p->d_books;
         a.queries = d_q;
@@ -1523,8 +1601,17 @@ int pq_run_collect(px_pq* p, const float* d_q, int64_t nq, int64_t k, int64_t n_
     return PX_OK;
 }
 
+int pq_run_paths(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
+                 int64_t* d_ids, float* d_out);
+
 int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
            int64_t* d_ids, float* d_out) {
+    PX_TRY(debug_begin(p->ws, p->stream));
+    return debug_end(p->ws, p->stream, pq_run_paths(p, d_q, nq, k, d_mask, d_ids, d_out));
+}
+
+int pq_run_paths(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_mask,
+                 int64_t* d_ids, float* d_out) {
     Workspace& ws = p->ws;
     hipStream_t s = p->stream;
     int64_t n_eff = p->d_rows;
@@ -1547,6 +1634,8 @@ int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_m
                 rps = std::max<int64_t>((rps + 255) / 256 * 256, 256);
                 splits = std::max<int64_t>(1, (n_eff + rps - 1) / rps);
                 px::PqScanArgs a{};
+                a.dbg = p->ws.dbg;
+                a.rows = p->d_rows;
                 a.codes = p->d_codes;
                 a.codebooks = p->d_books;
                 a.queries = d_q + q0 * p->dim;
@@ -1583,6 +1672,8 @@ int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_m
     PX_TRY(p->timing.ensure());
     if (p->timing.enabled) PX_HIP(hipEventRecord(p->timing.ev[0], s));
     px::PqScanArgs a{};
+    a.dbg = p->ws.dbg;
+    a.rows = p->d_rows;
     a.codes = p->d_codes;
     a.codebooks = p->d_books;
     a.queries = d_q;
@@ -1603,6 +1694,7 @@ int pq_run(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_t* d_m
     if (p->timing.enabled) PX_HIP(hipEventRecord(p->timing.ev[1], s));
 
     px::MergeArgs mg{};
+    mg.dbg = p->ws.dbg;
     mg.part_keys = a.part_keys;
     mg.part_ids = a.part_ids;
     mg.rowidx = rowidx;

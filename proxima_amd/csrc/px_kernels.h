@@ -55,6 +55,10 @@ struct FlatScanArgs {
     // search failed its finiteness check), it makes the whole launch a no-op
     const int* abort;
     int abort_seq;
+    // debug build: the launch's debug word (null: no checks) and the corpus rows that row
+    // ids must stay below
+    int* dbg;
+    int64_t rows;
 };
 
 // Waves per workgroup and list capacity used for a list length kl.
@@ -115,6 +119,7 @@ struct CollectSelectArgs {
     int64_t* out_ids;
     float* out_dists;
     int raw_keys;
+    int* dbg;                // debug build: as FlatScanArgs::dbg
 };
 hipError_t launch_collect_select(const CollectSelectArgs& a, int slots, hipStream_t s);
 // Threshold ladder from the dense keys of a collect scan over a row sample: per query,
@@ -179,6 +184,7 @@ struct MergeArgs {
     int raw_keys;            // 1: write raw keys (FLT_MAX padding) instead of distances
     const int* abort;        // optional, as FlatScanArgs::abort: equal to abort_seq, nothing
     int abort_seq;           // is written
+    int* dbg;                // debug build: as FlatScanArgs::dbg
 };
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
 
@@ -226,6 +232,8 @@ struct PqScanArgs {
     int* cand_count;
     int cap;
     int dense;
+    int* dbg;                 // debug build: as FlatScanArgs::dbg ...
+    int64_t rows;             // ... and the code rows
 };
 int pq_list_capacity(int kl);
 int pq_lists_per_split();

@@ -136,6 +136,7 @@ __global__ __launch_bounds__(kPqThreads) void pq_scan_kernel(PqScanArgs a) {
         for (int qq = 0; qq < QPB; ++qq) key[qq] = 0.0f;
         if (valid) {
             const int64_t row = a.rowidx ? (int64_t)a.rowidx[pos] : pos;
+            PX_DCHECK(a.dbg, kDbgPq, pos < a.n_eff && row >= 0 && row < a.rows);
             if (M > 0) {
                 const CodeRow<(M > 0 ? M : 1)> cr =
                     *reinterpret_cast<const CodeRow<(M > 0 ? M : 1)>*>(a.codes + row * M);
