@@ -28,7 +28,7 @@
 // thresholds; every key of the split is written to cand_keys [slot][dense_ld] by position
 // (the threshold sample of the sampled path).
 //
-// DYN (unfiltered one-chunk scans with FlatScanArgs::gbest): the splits' shared bound.
+// DYN (one-chunk scans with FlatScanArgs::gbest, filtered or not): the splits' shared bound.
 // After each tile a lane publishes the smallest key of its rows of the split so far to
 // slot split % 32 of its query (device-scope atomicMin: a plain store would stay in this
 // XCD's L2); every published slot then has a row of its own splits at or below it, so the
@@ -58,7 +58,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     constexpr int kRowStep = NT / kF4PerRow;     // 16 rows between a thread's loads
     constexpr int kPF = kTileRows / kRowStep;    // 4 float4 per thread per stage
     static_assert(NT % kF4PerRow == 0 && kTileRows % kRowStep == 0, "uneven stage split");
-    static_assert(!(DYN && (MULTI || FILT)), "the shared bound serves one-chunk unfiltered scans");
+    static_assert(!(DYN && MULTI), "the shared bound serves one-chunk scans");
     __shared__ __attribute__((aligned(16))) float tile[kStageBufs][kTileRows * kLdsStride];
     __shared__ __attribute__((aligned(16))) float tnorm[kNormBufs][kTileRows];
 
@@ -417,16 +417,20 @@ hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s) {
     const int64_t qtiles = (a.nq + 255) / 256;
     const dim3 grid((unsigned)(qtiles * a.splits)), block(512);
     const bool dyn = a.gbest != nullptr;
-    if (dyn && (a.rowidx || a.dense)) return hipErrorInvalidValue;
+    if (dyn && a.dense) return hipErrorInvalidValue;
 #define PX_COLLECT(L2, FILT, DYN) \
     hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true>), grid, block, 0, s, a)
     if (a.metric == 0) {
-        if (a.rowidx) PX_COLLECT(true, true, false);
-        else if (dyn) PX_COLLECT(true, false, true);
+        if (a.rowidx) {
+            if (dyn) PX_COLLECT(true, true, true);
+            else PX_COLLECT(true, true, false);
+        } else if (dyn) PX_COLLECT(true, false, true);
         else PX_COLLECT(true, false, false);
     } else {
-        if (a.rowidx) PX_COLLECT(false, true, false);
-        else if (dyn) PX_COLLECT(false, false, true);
+        if (a.rowidx) {
+            if (dyn) PX_COLLECT(false, true, true);
+            else PX_COLLECT(false, true, false);
+        } else if (dyn) PX_COLLECT(false, false, true);
         else PX_COLLECT(false, false, false);
     }
 #undef PX_COLLECT

@@ -201,8 +201,11 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     if (dyn) next_refresh = 0;
     // list mode with one query chunk: the insertions of a tile's second row block run during
     // the next tile's MFMAs (an insertion otherwise holds up the stage barrier for all eight
-    // waves); the first block's run in the epilogue, as do all of them with MULTI
-    constexpr bool LDEFER = !COLLECT && !MULTI;
+    // waves); the first block's run in the epilogue, as do all of them with MULTI, and with a
+    // filter on L2 rows, where the 16 deferred keys pushed 3-4 registers to scratch
+    // (1M x 128, 10,000 queries, k = 10, without the deferral: 10% filter 3.39 -> 3.28 ms,
+    // 50% filter 12.87 -> 13.05)
+    constexpr bool LDEFER = !COLLECT && !MULTI && !(FILT && L2);
     float pkey[COLLECT ? 32 : (LDEFER ? 16 : 1)];  // keys of the previous tile tested during this one
     float pthr = -kInf;            // list mode: the previous tile's threshold ...
     bool peq = false;              // ... and whether keys equal to it may still enter

@@ -865,12 +865,17 @@ bool lists_beat_sample(int64_t n_eff, int64_t kk, int64_t dp) {
 //     tile adds up to k' candidates a query
 //   100k / 1M x 384 IP, 1,000-4,000 queries, k = 10: 1-2% behind the lists (several query
 //     chunks: the keys are tested in the epilogue, not during the next tile's MFMAs)
-//   1M x 128 with a 50% / 10% filter, k = 10: 13.2 / 3.7 (lists 13.1 / 3.6)
-// so: unfiltered, one 128-dim chunk, at most 48 splits, k' <= 24 (the bound is the k'-th
-// smallest of at most 32 split minima; at k' = 32 it is their largest and prunes little).
+//   1M x 128 with a 50% / 10% / 2% filter, k = 10: 10.8 / 2.8 / 1.1 on flat_collect_kernel
+//     (lists 13.1 / 3.5 / 1.3); on the older scan (flat_scan_kernel's collect mode, rows of
+//     other widths) 13.2 / 3.7 against 13.1 / 3.6, so filtered rows take it only at 128
+//     padded dims
+// so: one 128-dim chunk (filtered: exactly 128), at most 48 splits, k' <= 24 (the bound is
+// the k'-th smallest of at most 32 split minima; at k' = 32 it is their largest and prunes
+// little).
 bool collect_bound_only(int64_t n_eff, int64_t nq, int64_t kk, int64_t dp, int cus,
                         bool filtered) {
-    if (filtered || dp > 128 || kk > 24 || nq < kCollectMinQueries || vec_collect(nq, dp))
+    if ((filtered && dp != 128) || dp > 128 || kk > 24 || nq < kCollectMinQueries ||
+        vec_collect(nq, dp))
         return false;
     int64_t splits = 1, rps = 64;
     collect_splits(n_eff, std::min(nq, kCollectBatch), cus, &splits, &rps);

@@ -349,7 +349,8 @@ def test_bound_only_first_round(gpu):
     for k in (1, 10, 16):
         for m in (None, mask):
             idx, ids, d = _search(data, q, k, oracle.L2, m)
-            # filtered searches keep the lists at these k
+            # filtered rows of 64 dims keep the lists at these k (the shared bound of a
+            # filtered scan is compiled into the 128-dim collect scan only)
             assert _path(idx) == ("collect-bounded" if m is None else "lists"), k
             o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2, mask=m)
             assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d), k
@@ -362,6 +363,28 @@ def test_bound_only_first_round(gpu):
     gd = datagen.unit_gaussian(40_000, 96, 66)
     gq = datagen.unit_gaussian(2048, 96, 67)
     _check(gd, gq, 12, oracle.IP)
+
+
+@pytest.mark.parametrize("rows,density", [(80_000, 0.5), (400_000, 0.1)])
+def test_bound_only_filtered_128_dims(gpu, rows, density):
+    # filtered rows of exactly 128 padded dims take the bounded first round too (the shared
+    # bound over the kept rows' positions): about 40,000 kept rows and 2,048 queries, the
+    # 32 splits of the unfiltered case above
+    data = datagen.sift_like(rows, 128, 91)
+    q = datagen.sift_like(2048, 128, 92)
+    mask = datagen.mask(rows, density, 93)
+    for k in (1, 10, 16):
+        print(f"case bounded filtered rows={rows} density={density} k={k}", flush=True)
+        idx, ids, d = _search(data, q, k, oracle.L2, mask)
+        assert _path(idx) == "collect-bounded", k
+        o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2, mask=mask)
+        assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d), k
+    gd = datagen.unit_gaussian(rows, 128, 94)
+    gq = datagen.unit_gaussian(2048, 128, 95)
+    idx, ids, d = _search(gd, gq, 10, oracle.IP, mask)
+    assert _path(idx) == "collect-bounded"
+    o_ids, o_d, _ = oracle.flat_search(gd, gq, 10, oracle.IP, mask=mask)
+    assert_parity(ids, d, o_ids, o_d, _key_of(gd, gq, oracle.IP))
 
 
 def test_bound_only_overflow_and_ties(gpu):
