@@ -440,8 +440,10 @@ def bench_pq(args, dev):
                    "n": n, "m": m, "nq": nq, "k": k},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": read_traffic("pq_scan_kernel_l2_1Mx16_q10k_k10.md",
-                                             mask is None and (n, nq, k) == (1_000_000, 10_000, 10)),
+                     "traffic": read_traffic("pq_scan_kernel_l2_1Mx16_q10k_k10.md"
+                                             if mask is None else
+                                             "pq_scan_kernel_l2_1Mx16_q10k_k10_mask50.md",
+                                             (n, nq, k) == (1_000_000, 10_000, 10)),
                      "kernel": "pq_scan_kernel", "kernel_ms": float(np.mean(scan_ms)),
                      "algorithmic_bytes_per_launch": algo_bytes},
         "host_buffer": hb,

@@ -15,7 +15,8 @@ import pytest
 import bench
 
 PROFILES = Path(__file__).resolve().parent.parent / "profiles"
-NAMES = sorted(set(bench.TRAFFIC_PROFILES.values()) | {"pq_scan_kernel_l2_1Mx16_q10k_k10.md"})
+NAMES = sorted(set(bench.TRAFFIC_PROFILES.values()) | {"pq_scan_kernel_l2_1Mx16_q10k_k10.md",
+                                                        "pq_scan_kernel_l2_1Mx16_q10k_k10_mask50.md"})
 
 
 @pytest.mark.parametrize("name", NAMES)
