@@ -387,6 +387,13 @@ int debug_end(Workspace& ws, hipStream_t s, int rc) {
                                 std::to_string(v % 100000));
 }
 
+// Rows of several 128-dim chunks scanned over several rounds of workgroups take the
+// XCD-major block order (FlatScanArgs::xcd_major); qpb: query slots per workgroup.
+int xcd_major_for(const px::FlatScanArgs& a, int64_t qpb, int cus) {
+    const int64_t blocks = (a.nq + qpb - 1) / qpb * (int64_t)a.splits;
+    return a.dp > 128 && blocks > cus ? 1 : 0;
+}
+
 int check_device_finite(Workspace& ws, const float* d_x, int64_t count, hipStream_t s) {
     PX_TRY(ws.count.reserve(sizeof(int)));
     PX_TRY(ws.ensure_pinned());
@@ -963,6 +970,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.cand_keys = ws.cand_k.as<float>();
         a.dense = 1;
         a.dense_ld = ld;
+        a.xcd_major = xcd_major_for(a, 256, std::max(f->dev.cus, 1));
         PX_HIP(px::launch_flat_collect(a, s));
         px::LadderArgs la{};
         la.keys = a.cand_keys;
@@ -1070,15 +1078,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             a.kl = (int)j.kk;
             j.sel_gbest = a.gbest;
         }
-        // The stream is drained before the scan is launched. Launched right behind the small
-        // kernels before it (fills, the ladder), a collect scan on this box ran slow in one
-        // search of a handful, at the same search every time: 1M x 128, 10,000 queries,
-        // k = 10 bounded: the second search, scan 28 ms (its shared bound lost for most
-        // queries, ~60% of them a second round), 43 ms against 22.3; k = 50 sampled: the
-        // fourth, 31 ms against 24.6. With the host wait every search ran at the steady time
-        // (a slot fill with atomics, or slots that need no fill at all, did not help); the
-        // wait costs nothing measurable at these sizes.
-        PX_HIP(hipStreamSynchronize(s));
+        a.xcd_major = xcd_major_for(a, 256, std::max(f->dev.cus, 1));
         PX_HIP(px::launch_flat_collect(a, s));
         if (round == 0) {
             f->timing.splits = (int)splits;
@@ -1213,6 +1213,7 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     a.gbest = b.gbest;
     a.abort = d_flag;
     a.abort_seq = seq;
+    a.xcd_major = xcd_major_for(a, px::flat_queries_per_block(kl), std::max(f->dev.cus, 1));
     if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[1], s));
 

@@ -59,6 +59,9 @@ struct FlatScanArgs {
     // ids must stay below
     int* dbg;
     int64_t rows;
+    // rows of several 128-dim chunks over several rounds of workgroups: XCD-major block order
+    // (flat_scan_kernel), the grid padded to a multiple of 8
+    int xcd_major;
 };
 
 // Waves per workgroup and list capacity used for a list length kl.
