@@ -163,6 +163,41 @@ __device__ __forceinline__ float ref_inner_product(const float* a, const float* 
     return sum;
 }
 
+// Same arithmetic and order, spread over a group of 8 consecutive lanes (gl = lane % 8, all
+// 8 lanes of the group active and on the same a, b): lane gl accumulates the reference's
+// accumulator gl over the chunks in order -- each of its loads independent of the others,
+// so one round trip to memory instead of one per 4 chunks -- then every lane of the group
+// folds the 8 accumulators from 0.0 in order and adds the remainder, as ref_l2_sqr /
+// ref_inner_product do. Pitches a multiple of 8 floats.
+__device__ __forceinline__ float ref_key_g8(const float* a, const float* b, int n, bool l2,
+                                           int gl) {
+    float acc = 0.f;
+    const int chunks = n >> 3;
+#pragma unroll 8
+    for (int c = 0; c < chunks; ++c) {
+        const float x = a[c * 8 + gl], y = b[c * 8 + gl];
+        if (l2) {
+            const float d = x - y;
+            acc = acc + d * d;
+        } else {
+            acc = acc + x * y;
+        }
+    }
+    const int base = (int)(threadIdx.x & 63) & ~7;
+    float sum = 0.f;
+#pragma unroll
+    for (int l = 0; l < 8; ++l) sum = sum + __shfl(acc, base + l, 64);
+    for (int i = chunks * 8; i < n; ++i) {
+        if (l2) {
+            const float d = a[i] - b[i];
+            sum = sum + d * d;
+        } else {
+            sum = sum + a[i] * b[i];
+        }
+    }
+    return sum;
+}
+
 // Same arithmetic and order, for rows stored with a pitch that is a multiple of 8 floats
 // (32-byte aligned, readable up to the next multiple of 8): chunks of 8 are loaded as two
 // float4, four chunks per step so that the loads of a step are in flight together.

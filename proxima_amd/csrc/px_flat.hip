@@ -1079,7 +1079,8 @@ __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
 
     int p2 = 1;
     while (p2 < a.kl) p2 <<= 1;
-    for (int x = threadIdx.x; x < p2; x += blockDim.x) {
+    // exact keys: eight lanes per candidate (ref_key_g8)
+    for (int x = threadIdx.x >> 3; x < p2; x += blockDim.x >> 3) {
         float kv = kInf;
         int id = kIdNone;
         if (x < a.kl && x < ps) {
@@ -1088,12 +1089,16 @@ __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
             if (id != kIdNone && a.corpus) {
                 const float* qv = a.queries + (int64_t)q * a.dp;
                 const float* xv = a.corpus + (int64_t)id * a.dp;
-                kv = a.metric == 0 ? ref_key_v(qv, xv, a.dim, true) : -ref_key_v(qv, xv, a.dim, false);
+                const int gl = threadIdx.x & 7;
+                kv = a.metric == 0 ? ref_key_g8(qv, xv, a.dim, true, gl)
+                                   : -ref_key_g8(qv, xv, a.dim, false, gl);
             }
             if (id == kIdNone) kv = kInf;
         }
-        rk[x] = kv;
-        ri[x] = id;
+        if ((threadIdx.x & 7) == 0) {
+            rk[x] = kv;
+            ri[x] = id;
+        }
     }
     bitonic_sort(rk, ri, p2);
 
@@ -1276,7 +1281,9 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
     const int keep = min(a.kk, avail);
     int p2 = 1;
     while (p2 < keep) p2 <<= 1;
-    for (int x = threadIdx.x; x < p2; x += blockDim.x) {
+    // exact keys: eight lanes per candidate (ref_key_g8); each candidate's entry is read by
+    // its own group only, and written after the group has read it
+    for (int x = threadIdx.x >> 3; x < p2; x += blockDim.x >> 3) {
         float kv = kInf;
         int id = kIdNone;
         if (x < keep && si[x] != kIdNone) {
@@ -1286,12 +1293,15 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
             if (a.corpus) {
                 const float* qv = a.queries + (int64_t)q * a.dp;
                 const float* xv = a.corpus + (int64_t)id * a.dp;
-                kv = a.metric == 0 ? ref_key_v(qv, xv, a.dim, true)
-                                   : -ref_key_v(qv, xv, a.dim, false);
+                const int gl = threadIdx.x & 7;
+                kv = a.metric == 0 ? ref_key_g8(qv, xv, a.dim, true, gl)
+                                   : -ref_key_g8(qv, xv, a.dim, false, gl);
             }
         }
-        sk[x] = kv;
-        si[x] = id;
+        if ((threadIdx.x & 7) == 0) {
+            sk[x] = kv;
+            si[x] = id;
+        }
     }
     bitonic_sort(sk, si, p2);
     for (int x = threadIdx.x; x < a.k; x += blockDim.x) {
