@@ -12,10 +12,11 @@
 //
 // Pipeline. Three LDS stage buffers: stage s reads buffer s % 3 while the global loads of
 // stage s + 2 are in flight in registers; they are written to buffer (s + 2) % 3 after the
-// stage's MFMAs, and one barrier per stage publishes them. Stage s + 1's buffer was
-// therefore complete one barrier earlier, so each wave reads the A operands of stage
-// s + 1's first dim group before it waits at stage s's barrier and issues its first MFMAs
-// straight after it. Two accumulator sets alternate between tiles: while the MFMAs of
+// stage's MFMAs. There is no barrier per stage: each wave publishes in LDS the last stage
+// it has committed, and at the end of stage s waits until every wave has committed stage
+// s + 1; then it reads the A operands of stage s + 1's first dim group, writes its part of
+// stage s + 2, and issues stage s + 1's first MFMAs, at most one stage ahead of the slowest
+// wave of its workgroup. Two accumulator sets alternate between tiles: while the MFMAs of
 // tile t accumulate into one set, the keys of tile t - 1 are computed from the other, in
 // place, and tested against the thresholds two rows per dim group, between the MFMAs of
 // tile t's first stage; so no wave leaves the matrix unit idle for an epilogue. Each
@@ -50,6 +51,7 @@ namespace {
 
 constexpr int kStageBufs = 3;  // LDS stage buffers
 constexpr int kNormBufs = 4;   // LDS norm buffers (tile t + 2 is staged while t - 1 is tested)
+constexpr int kSpinLimit = 1 << 16;  // polls of a stage-sync wait (each one s_sleep 1)
 
 template <bool L2, bool MULTI, bool FILT, bool DYN, bool FULL>
 __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
@@ -61,6 +63,8 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     static_assert(!(DYN && MULTI), "the shared bound serves one-chunk scans");
     __shared__ __attribute__((aligned(16))) float tile[kStageBufs][kTileRows * kLdsStride];
     __shared__ __attribute__((aligned(16))) float tnorm[kNormBufs][kTileRows];
+    // per wave: the last stage it has committed to a stage buffer (the stage sync below)
+    __shared__ int committed[8];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
@@ -134,18 +138,63 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     fetch(1);
     commit(1, 1);
     tile_ids(2 / nch);
+    if (tid < 8) committed[tid] = 1;
     __syncthreads();
 
+    // Stage sync without a barrier per stage. The two waves of a SIMD do not finish a
+    // stage's MFMAs together (the matrix unit favours one), and at a workgroup barrier the
+    // one ahead would idle while the other finishes and commits; with three stage buffers a
+    // wave may instead run up to a stage ahead. Each wave publishes the last stage it has
+    // committed (committed[wave], an LDS store with release order), and at the end of stage
+    // s waits until every wave has committed stage s + 1 (acquire loads) before it reads
+    // stage s + 1's buffer and writes stage s + 2's. A wave commits stage s + 1 only after
+    // all its reads of stage s - 1, whose buffer and norm slot the writes of stage s + 2
+    // reuse, so the one wait covers both. A wait gives up after kSpinLimit polls (about
+    // 5 ms) and reports it (a.spin_fail), so that a wave always finishes.
+    auto publish = [&](int v) __attribute__((always_inline)) {
+        if (lane == 0)
+            __hip_atomic_store(committed + wave, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+    };
+    // Every wave has committed stage ct: each lane polls committed[lane & 7]. The poll loop
+    // is one asm block: as a loop in the compiled code it split the stage's schedule and
+    // cost register spills. Its s_waitcnt makes the load acquire (LDS at workgroup scope
+    // needs no more), and the "memory" clobber keeps the stage buffer accesses after it.
+    // The poll count is early-clobber ("+&s"): as a plain in-out operand it may share a
+    // register with an equal input (it was given ct's, and each poll then raised the target).
+    const unsigned caddr = (unsigned)(uintptr_t)(committed + (lane & 7));
+    auto wait_committed = [&](int ct) __attribute__((always_inline)) {
+        int v, spins = 0;
+        unsigned long long m;
+        asm volatile(
+            ".Lpx_poll%=:\n"
+            "  ds_read_b32 %[v], %[addr]\n"
+            "  s_waitcnt lgkmcnt(0)\n"
+            "  v_cmp_lt_i32_e64 %[m], %[v], %[ct]\n"
+            "  s_cmp_lg_u64 %[m], 0\n"
+            "  s_cbranch_scc0 .Lpx_done%=\n"
+            "  s_add_u32 %[sp], %[sp], 1\n"
+            "  s_cmp_ge_u32 %[sp], %[lim]\n"
+            "  s_cbranch_scc1 .Lpx_done%=\n"
+            "  s_sleep 1\n"
+            "  s_branch .Lpx_poll%=\n"
+            ".Lpx_done%=:\n"
+            : [v] "=&v"(v), [m] "=&s"(m), [sp] "+&s"(spins)
+            : [addr] "v"(caddr), [ct] "s"(ct), [lim] "s"(kSpinLimit)
+            : "memory", "scc");
+        if (spins >= kSpinLimit && a.spin_fail && lane == 0) atomicOr(a.spin_fail, 1);
+    };
+
     // A wave whose 32 queries are all padding (last query tile) only helps stage the
-    // corpus: same loads, same barriers.
+    // corpus: same loads, same waits.
     if (qt * 256 + wave * 32 >= a.nq) {
         int wb = 2;
         for (int s = 0; s < nstages; ++s) {
             fetch(s + 2);
             tile_ids((s + 3) / nch);
+            wait_committed(s + 1);
             commit(s + 2, wb);
+            publish(s + 2);
             wb = wb == kStageBufs - 1 ? 0 : wb + 1;
-            __syncthreads();
         }
         return;
     }
@@ -169,14 +218,21 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
                         (int64_t)h * a.cap;
 
     // one row of the previous tile at or below the pre-screen: the exact test and append.
-    // Past the region's capacity the count still grows (the select sees the overflow) and
-    // the last slot is rewritten, so the region keeps holding cap real candidates.
+    // Past the region's capacity the count still grows (the select sees the overflow). With
+    // cand_dmin the region keeps its first cap rows and dmin the smallest key of the rows
+    // it drops (the select finishes a query whose k'-th kept key is below every dropped
+    // key); without it the last slot is rewritten.
+    float dmin = kInf;
     auto test_row = [&](float kv, int pos) __attribute__((always_inline)) {
         if (((kv < cthr) | ((kv == cthr) & (pos <= cpos))) & (kv <= gbound)) {
-            const int at = min(ccount, a.cap - 1);
-            PX_DCHECK(a.dbg, kDbgCollect, qvalid && at >= 0 && pos >= row0 && pos < row1);
-            creg_k[at] = kv;
-            creg_p[at] = pos;
+            PX_DCHECK(a.dbg, kDbgCollect, qvalid && pos >= row0 && pos < row1);
+            if (ccount < a.cap || !a.cand_dmin) {
+                const int at = min(ccount, a.cap - 1);
+                creg_k[at] = kv;
+                creg_p[at] = pos;
+            } else {
+                dmin = fminf(dmin, kv);
+            }
             ++ccount;
         }
     };
@@ -245,7 +301,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     }
 
     f32x16 accA[2], accB[2];
-    // A operands of the next stage's first dim group (read before each stage's barrier)
+    // A operands of the next stage's first dim group (read at the end of each stage)
     float4 an0 = *reinterpret_cast<const float4*>(tile[0] + j * kLdsStride + h * 4);
     float4 an1 = *reinterpret_cast<const float4*>(tile[0] + (32 + j) * kLdsStride + h * 4);
     int rb_cur = 0;  // LDS buffer of the current stage
@@ -340,17 +396,19 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
             }
             if (a.dense) dense_write(prev, row0 + (t - 1) * kTileRows, kTileRows);
         }
-        // the next stage's first A operands: its buffer was complete at the last barrier
+        // the next stage's first A operands and this wave's part of stage s + 2, once every
+        // wave has committed stage s + 1
+        wait_committed(s + 1);
         if (s + 1 < nstages) {
             an0 = *reinterpret_cast<const float4*>(tile[rb_nxt] + j * kLdsStride + h * 4);
             an1 = *reinterpret_cast<const float4*>(tile[rb_nxt] + (32 + j) * kLdsStride + h * 4);
         }
         commit(s + 2, rb_wr);
+        publish(s + 2);
         if constexpr (DYN) {
             // published after the commit, whose waits then do not wait for the atomic
             if (pub_now) atomicMin(gbest + (split & 31), cpub);
         }
-        __syncthreads();
         rb_cur = rb_nxt;
         ++s;
     };
@@ -405,7 +463,11 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     };
     if (ntiles & 1) finish(accA);
     else finish(accB);
-    if (qvalid && !a.dense) a.cand_count[((int64_t)slot * a.splits + split) * 2 + h] = ccount;
+    if (qvalid && !a.dense) {
+        const int64_t r = ((int64_t)slot * a.splits + split) * 2 + h;
+        a.cand_count[r] = ccount;
+        if (a.cand_dmin && ccount > a.cap) a.cand_dmin[r] = total_key(dmin);
+    }
 }
 
 }  // namespace

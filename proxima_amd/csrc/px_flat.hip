@@ -1148,7 +1148,7 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
     float* sk = reinterpret_cast<float*>(csmem);
     int* si = reinterpret_cast<int*>(sk + a.lcap);
     __shared__ int s_off[kMaxCollectRegions + 1];
-    __shared__ int s_total, s_over;
+    __shared__ int s_total, s_over, s_dmin;
 
     const int b = blockIdx.x;
     const int q = a.qlist ? a.qlist[b] : b;
@@ -1162,15 +1162,22 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
     if (t == 0) {
         s_total = 0;
         s_over = 0;
+        s_dmin = kTotalKeyInf;
     }
     const int per = (a.regions + nt - 1) / nt;
     const int rb0 = min(t * per, a.regions), rb1 = min(rb0 + per, a.regions);
     int my_stored = 0, my_total = 0, my_over = 0;
+    // smallest dropped key of the overflowing regions (INT_MIN: unknown)
+    int my_dmin = kTotalKeyInf;
     for (int r = rb0; r < rb1; ++r) {
         const int c = cnt[r];
         my_total += c;
         my_stored += min(c, a.cap);
-        my_over |= c > a.cap;
+        if (c > a.cap) {
+            my_over = 1;
+            my_dmin = min(my_dmin, a.cand_dmin ? a.cand_dmin[(int64_t)b * a.regions + r]
+                                               : INT_MIN);
+        }
     }
     int incl = my_stored;
     for (int off = 1; off < 64; off <<= 1) {
@@ -1187,15 +1194,26 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
     }
     if (t == nt - 1) s_off[a.regions] = min(excl, a.lcap);
     if (my_total) atomicAdd(&s_total, my_total);
-    if (my_over) atomicOr(&s_over, 1);
+    if (my_over) {
+        atomicOr(&s_over, 1);
+        atomicMin(&s_dmin, my_dmin);
+    }
     __syncthreads();
-    if (t == 0 && s_total > a.lcap) s_over = 1;
+    // the kept candidates past the LDS (then some are not held)
+    const bool lds_over = excl > a.lcap && t == nt - 1;
+    if (lds_over) s_over = 2;
     __syncthreads();
     const int total = s_total;
-    const int held = s_off[a.regions];  // candidates loaded into LDS (all when !s_over)
+    const int held = s_off[a.regions];  // candidates loaded into LDS (all kept ones unless
+                                        // s_over == 2)
     const bool all_rows = a.thr_key[q] == kTotalKeyInf;
-    const bool finish = !s_over && (total >= a.kk || all_rows);
-    if (!s_over && !finish) {
+    // s_over: 0 none, 1 a region overflowed (every kept candidate held), 2 past the LDS.
+    // With 1 the query finishes if its kk-th smallest held key is below every dropped key
+    // (s_dmin), decided once they are sorted: no dropped row can be among its best kk.
+    const int over = s_over;
+    const bool may_finish = over == 0 || (over == 1 && s_dmin != INT_MIN);
+    bool finish = over == 0 && (total >= a.kk || all_rows);
+    if (over == 0 && !finish) {
         // too few: next rung
         if (threadIdx.x == 0) {
             const int r = a.rung[q] + 1;
@@ -1207,7 +1225,7 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
         }
         return;
     }
-    if (s_over && held <= a.kk) {
+    if (over && held <= a.kk) {
         // too many, but too few held to tighten: the caller collects again with a larger cap
         if (threadIdx.x == 0) a.status[q] = 1;
         return;
@@ -1267,6 +1285,8 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
         si[x] = kIdNone;
     }
     bitonic_sort(sk, si, p);
+    // a region overflowed: the kk-th smallest held key (held > kk) below every dropped one
+    if (over == 1 && may_finish) finish = total_key(sk[a.kk - 1]) < s_dmin;
 
     if (!finish) {
         // too many: tighten to the kk-th smallest held candidate

@@ -177,6 +177,7 @@ struct Workspace {
     DevBuf q, qn, mask, rowidx, scratch, count, part_k, part_i, out_ids, out_d, gtau, gbest;
     // collect path (k' past the lists)
     DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
+    DevBuf cand_d;           // smallest dropped key of each overflowing region
     DevBuf fflag;            // finiteness verdicts of list-path searches (next_finite_seq)
     int fseq = 0;
     DevBuf dbgw;             // debug build: the debug word of the kernels' index checks ...
@@ -233,7 +234,8 @@ struct Workspace {
     void release() {
         for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids,
                           &out_d, &gtau, &gbest, &thr_k, &thr_p, &lad_k, &lad_p, &rung, &status,
-                          &cand_k, &cand_p, &cand_n, &samp_row, &qlist, &sort_scratch, &fflag,
+                          &cand_k, &cand_p, &cand_n, &cand_d, &samp_row, &qlist, &sort_scratch,
+                          &fflag,
                           &dbgw})
             b->release();
         fseq = 0;
@@ -698,8 +700,10 @@ struct CollectJob {
     // ladder, every query's threshold +inf; bound_expect sizes its regions.
     bool bound_only = false;
     double bound_expect = 0.0;
-    // set by scan: the shared-bound slots of its launch (null when it applied none)
+    // set by scan: the shared-bound slots of its launch (null when it applied none) and
+    // its regions' smallest dropped keys (null when it keeps none: an overflow retries)
     const int* sel_gbest = nullptr;
+    const int* sel_dmin = nullptr;
 };
 
 int run_collect(CollectJob& j) {
@@ -711,9 +715,11 @@ int run_collect(CollectJob& j) {
     PX_TRY(ws.lad_k.reserve(sizeof(int) * nq * px::kRungs));
     PX_TRY(ws.lad_p.reserve(sizeof(int) * nq * px::kRungs));
     PX_TRY(ws.rung.reserve(sizeof(int) * nq));
-    PX_TRY(ws.status.reserve(sizeof(int) * nq));
+    // status[nq]: set by a scan whose stage sync gave up (FlatScanArgs::spin_fail)
+    PX_TRY(ws.status.reserve(sizeof(int) * (nq + 1)));
     PX_TRY(j.timing->ensure());
     if (j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[0], s));
+    PX_HIP(px::launch_fill_int(ws.status.as<int>() + nq, 1, 0, s));
 
     // expected candidates per query in the first round
     double expect = (double)n_eff;
@@ -734,7 +740,7 @@ int run_collect(CollectJob& j) {
         PX_TRY(j.sample(S, r0, r1));
     }
 
-    PX_TRY(ws.ensure_status(nq));
+    PX_TRY(ws.ensure_status(nq + 1));
     int* h_status = ws.h_status;
     std::vector<int> failing;
     int64_t slots = nq;
@@ -778,12 +784,15 @@ int run_collect(CollectJob& j) {
             c.status = ws.status.as<int>();
             c.kk = (int)kk;
             c.gbest = j.sel_gbest;
+            c.cand_dmin = j.sel_dmin;
             PX_HIP(px::launch_collect_select(c, (int)take, s));
             if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[2], s));
             done += take;
         }
-        PX_HIP(px::launch_copy_to_host(ws.status.as<int>(), ws.h_status_dev, nq, s));
+        PX_HIP(px::launch_copy_to_host(ws.status.as<int>(), ws.h_status_dev, nq + 1, s));
         PX_HIP(hipStreamSynchronize(s));
+        if (h_status[nq])
+            return fail(PX_ERR_DEVICE, "a collect scan's stage sync timed out (no results)");
         // queries of this round still open
         std::vector<int> next;
         if (qlist) {
@@ -970,6 +979,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.cand_keys = ws.cand_k.as<float>();
         a.dense = 1;
         a.dense_ld = ld;
+        a.spin_fail = ws.status.as<int>() + nq;
         a.xcd_major = xcd_major_for(a, 256, std::max(f->dev.cus, 1));
         PX_HIP(px::launch_flat_collect(a, s));
         px::LadderArgs la{};
@@ -1022,6 +1032,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             a.cand_pos = ws.cand_p.as<int>();
             a.cand_count = ws.cand_n.as<int>();
             a.cap = (int)*cap;
+            j.sel_dmin = nullptr;
             PX_HIP(px::launch_flat_vcollect(a, s));
             if (round == 0) {
                 f->timing.splits = (int)splits;
@@ -1035,7 +1046,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             // which receives at most half the split's rows
             *regions = 2 * splits;
             *cap = collect_cap(expect, *regions, round, j.kk, rps / 2);
-            const int64_t per = *regions * *cap * 8;
+            const int64_t per = *regions * (*cap * 8 + 4);
             if (!qlist || slots == 1 || slots * per <= max_bytes) break;
             slots = std::max<int64_t>(1, std::min(slots - 1, max_bytes / per));
         }
@@ -1043,6 +1054,10 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         PX_TRY(ws.cand_k.reserve(sizeof(float) * slots * *regions * *cap));
         PX_TRY(ws.cand_p.reserve(sizeof(int) * slots * *regions * *cap));
         PX_TRY(ws.cand_n.reserve(sizeof(int) * slots * *regions));
+        // rows of one 128-dim chunk (flat_collect_kernel) keep each full region's first cap
+        // rows and its smallest dropped key; the older scan rewrites the last slot
+        const bool keeps_dmin = f->dp == 128;
+        if (keeps_dmin) PX_TRY(ws.cand_d.reserve(sizeof(int) * slots * *regions));
         // every split is non-empty, two regions each, and the launch's regions fit
         PX_INTERNAL(splits * rps >= n_eff && (splits - 1) * rps < n_eff);
         PX_INTERNAL(*regions == 2 * splits && *regions <= px::kMaxCollectRegions);
@@ -1067,6 +1082,9 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.cand_pos = ws.cand_p.as<int>();
         a.cand_count = ws.cand_n.as<int>();
         a.cap = (int)*cap;
+        a.cand_dmin = keeps_dmin ? ws.cand_d.as<int>() : nullptr;
+        j.sel_dmin = a.cand_dmin;
+        a.spin_fail = ws.status.as<int>() + j.nq;
         // the shared bound needs k' publishing slots (one per split, at most 32); it is
         // applied where the first round has no sampled thresholds (with them it measured
         // no faster on 1M x 128 and 1M x 384, and 11% slower on 100k x 384 at k = 16)

@@ -47,6 +47,10 @@ struct FlatScanArgs {
     int* cand_pos;         // positions (indices into rowidx when filtered)
     int* cand_count;       // [nq slots][splits][2] rows that passed; more than cap = overflow
     int cap;
+    // optional (launch_flat_collect, 128-dim rows), [nq slots][splits][2]: where a region's
+    // count passes cap, the smallest key of the rows it dropped as a total-order int (it
+    // keeps its first cap rows); without it a full region keeps rewriting its last slot
+    int* cand_dmin;
     // dense != 0: no thresholds; every key goes to cand_keys as [slot][dense_ld] by position
     // (keys of rows past a split's end are +inf; dense_ld >= splits * rows_per_split)
     int dense;
@@ -62,6 +66,9 @@ struct FlatScanArgs {
     // rows of several 128-dim chunks over several rounds of workgroups: XCD-major block order
     // (flat_scan_kernel), the grid padded to a multiple of 8
     int xcd_major;
+    // optional (launch_flat_collect, 128-dim rows): set nonzero if a stage-sync wait of the
+    // scan gave up (a bug: the results of that launch are not to be used)
+    int* spin_fail;
 };
 
 // Waves per workgroup and list capacity used for a list length kl.
@@ -99,6 +106,10 @@ struct CollectSelectArgs {
     const float* cand_keys;  // FlatScanArgs regions of the collect scan
     const int* cand_pos;
     const int* cand_count;
+    // optional: FlatScanArgs::cand_dmin of the scan. A query whose regions overflowed but
+    // whose k'-th smallest kept key is below every dropped key finishes (the dropped rows
+    // cannot be among its best k'); without it an overflow always goes round again.
+    const int* cand_dmin;
     int regions, cap;        // regions per query slot (2 x splits), capacity of each
     int lcap;                // candidates the launch's LDS holds (power of two <= kMaxCollect)
     const int* qlist;        // optional: query index of each slot (one workgroup per slot)

@@ -182,6 +182,47 @@ def test_sample_near_underflow_rounds(gpu):
     assert rounds >= 3
 
 
+def _overflow_rows(n, kk, key_index):
+    """Rows of 128 dims whose L2 key from the origin is key_index(p) + 1 (one nonzero
+    coordinate, its square root), the threshold sample's rows far away: the sample lets
+    every other row through and every region of the first round overflows."""
+    data = np.zeros((n, 128), np.float32)
+    data[:, 0] = np.sqrt(key_index(np.arange(n)) + 1.0).astype(np.float32)
+    data[sample_positions(n, kk), 0] = 1000.0
+    return data
+
+
+def test_overflow_with_near_rows_dropped_goes_round_again(gpu):
+    # keys grow with the position: each region keeps its first rows, and the rows it drops
+    # in the first splits are nearer than the k'-th kept row of the later splits, so the
+    # query tightens and goes round again
+    n, k, nq = 40_000, 992, 64
+    data = _overflow_rows(n, k + 8, lambda p: p.astype(np.float64))
+    q = np.zeros((nq, 128), np.float32)
+    rounds = _check(data, q, k, oracle.L2, exact=True)
+    assert rounds >= 2
+
+
+def test_overflow_with_far_rows_dropped_finishes(gpu):
+    # keys grow with the position within each split of the first round's scan (a sawtooth
+    # of the split's length): each region keeps its own nearest rows and drops only rows
+    # beyond the k'-th smallest kept one, so the query finishes in the first round
+    n, k, nq = 40_000, 992, 64
+    q = np.zeros((nq, 128), np.float32)
+    # the scan's split length, from a search of the same shape
+    idx, _, _ = _search(_overflow_rows(n, k + 8, lambda p: p.astype(np.float64)), q, k,
+                        oracle.L2)
+    t = idx._last_timing()
+    assert t["path"] == "collect-sampled"
+    splits = t["splits"]
+    rps = [r for r in range(64, n + 64, 64) if -(-n // r) == splits]
+    assert len(rps) == 1, rps
+    rps = rps[0]
+    data = _overflow_rows(n, k + 8, lambda p: (p % rps) + 1e-3 * (p // rps))
+    rounds = _check(data, q, k, oracle.L2, exact=True)
+    assert rounds == 1
+
+
 def test_sample_short_of_its_last_split(gpu):
     # 10,000 rows at k = 100 sample 7,407 rows, which leave the sample scan's last split
     # four 64-row tiles short of its layout. Those key blocks are never written and must
