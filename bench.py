@@ -280,9 +280,17 @@ def bench_flat(args, dev):
     di = dev.empty(nq * k * 8)
     dd = dev.empty(nq * k * 4)
 
+    # the search and its timing read bound once: per step one library call for the search
+    # and one for the HIP-event times it recorded (kernel and pipeline)
+    search, search_args = lib.px_flat_search_device, (idx._h, dq, nq, k, dm, di, dd)
+    ev_scan, ev_total, ev_splits, ev_blocks = (ctypes.c_float(), ctypes.c_float(),
+                                               ctypes.c_int(), ctypes.c_int())
+    read_timing = lib.px_flat_last_timing
+    timing_args = (idx._h, ctypes.byref(ev_scan), ctypes.byref(ev_total),
+                   ctypes.byref(ev_splits), ctypes.byref(ev_blocks))
+
     def step():
-        rc = lib.px_flat_search_device(idx._h, dq, nq, k, dm, di, dd)
-        if rc:
+        if search(*search_args):
             raise RuntimeError(_lib.last_error())
 
     idx._timing(True)
@@ -293,9 +301,9 @@ def bench_flat(args, dev):
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
-        t = idx._last_timing()
-        scan_ms.append(t["scan_ms"])
-        total_ms.append(t["total_ms"])
+        read_timing(*timing_args)
+        scan_ms.append(ev_scan.value)
+        total_ms.append(ev_total.value)
     elapsed = time.perf_counter() - t0
     info = idx._last_timing()
     log(f"[bench] {args.steps} steps in {elapsed:.3f} s; scan {np.mean(scan_ms):.3f} ms, "
@@ -401,9 +409,16 @@ def bench_pq(args, dev):
     di = dev.empty(nq * k * 8)
     dd = dev.empty(nq * k * 4)
 
+    # as the flat loop: the search and its timing read bound once
+    search, search_args = lib.px_pq_search_device, (pq._h, dq, nq, k, dm, di, dd)
+    ev_scan, ev_total, ev_splits, ev_blocks = (ctypes.c_float(), ctypes.c_float(),
+                                               ctypes.c_int(), ctypes.c_int())
+    read_timing = lib.px_pq_last_timing
+    timing_args = (pq._h, ctypes.byref(ev_scan), ctypes.byref(ev_total),
+                   ctypes.byref(ev_splits), ctypes.byref(ev_blocks))
+
     def step():
-        rc = lib.px_pq_search_device(pq._h, dq, nq, k, dm, di, dd)
-        if rc:
+        if search(*search_args):
             raise RuntimeError(_lib.last_error())
 
     pq._timing(True)
@@ -413,7 +428,8 @@ def bench_pq(args, dev):
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
-        scan_ms.append(pq._last_timing()["scan_ms"])
+        read_timing(*timing_args)
+        scan_ms.append(ev_scan.value)
     elapsed = time.perf_counter() - t0
     ids = dev.get(di, np.empty((nq, k), dtype=np.int64))
     dists = dev.get(dd, np.empty((nq, k), dtype=np.float32))

@@ -989,7 +989,11 @@ constexpr int kMergeFiltered = 256;
 // tail can be among the best kl. PQ lists publish no bounds; their kl-th smallest list
 // head serves instead.
 __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
-    if (a.abort && *a.abort == a.abort_seq) return;
+    if (a.abort) {
+        const int v = *a.abort;
+        if (a.verdict && blockIdx.x == 0 && threadIdx.x == 0) *a.verdict = v;
+        if (v == a.abort_seq) return;
+    }
     extern __shared__ __attribute__((aligned(16))) char msmem[];
     __shared__ int s_n;
     int p = 1;
@@ -1003,6 +1007,17 @@ __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
     const float kInf = __int_as_float(0x7f800000);
     const float* pk = a.part_keys + (int64_t)q * a.width;
     const int* pi = a.part_ids + (int64_t)q * a.width;
+    // this thread's first kPre candidates, loaded while the bounds load (the filter below
+    // takes them from registers)
+    constexpr int kPre = 8;
+    float pkv[kPre];
+    int piv[kPre];
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+        const int x = threadIdx.x + u * blockDim.x;
+        pkv[u] = x < a.width ? pk[x] : kInf;
+        piv[u] = x < a.width ? pi[x] : kIdNone;
+    }
     int bound = a.bound ? a.bound[q] : kTotalKeyInf;
     if (a.gbest) {
         __shared__ int s_gb[32], s_kth;
@@ -1038,9 +1053,7 @@ __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
     if (bound != kTotalKeyInf) {
         if (threadIdx.x == 0) s_n = 0;
         __syncthreads();
-        for (int x = threadIdx.x; x < a.width; x += blockDim.x) {
-            int id = pi[x];
-            const float kv = pk[x];
+        auto keep = [&](float kv, int id) __attribute__((always_inline)) {
             if (id != kIdNone && total_key(kv) <= bound) {
                 const int at = atomicAdd(&s_n, 1);
                 if (a.rowidx) id = a.rowidx[id];
@@ -1048,7 +1061,11 @@ __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
                 sk[at] = kv;  // at < width <= p
                 si[at] = id;
             }
-        }
+        };
+#pragma unroll
+        for (int u = 0; u < kPre; ++u) keep(pkv[u], piv[u]);
+        for (int x = threadIdx.x + kPre * blockDim.x; x < a.width; x += blockDim.x)
+            keep(pk[x], pi[x]);
         __syncthreads();
         n = s_n;
         if (n > kMergeFiltered) n = -1;

@@ -1258,9 +1258,9 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     mg.raw_keys = raw_keys;
     mg.abort = d_flag;
     mg.abort_seq = seq;
+    mg.verdict = d_flag ? f->ws.h_count_dev : nullptr;
     PX_HIP(px::launch_merge(mg, s));
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[2], s));
-    if (d_flag) PX_HIP(px::launch_copy_to_host(d_flag, f->ws.h_count_dev, 1, s));
     PX_HIP(hipStreamSynchronize(s));
     if (d_flag && *f->ws.h_count == seq) return nonfinite_error();
     if (timed) {

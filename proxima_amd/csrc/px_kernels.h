@@ -198,6 +198,9 @@ struct MergeArgs {
     int raw_keys;            // 1: write raw keys (FLT_MAX padding) instead of distances
     const int* abort;        // optional, as FlatScanArgs::abort: equal to abort_seq, nothing
     int abort_seq;           // is written
+    // optional (with abort): workgroup 0 stores *abort here (a mapped host int's device
+    // address), so the host reads the search's finiteness verdict with no copy of its own
+    int* verdict;
     int* dbg;                // debug build: as FlatScanArgs::dbg
 };
 hipError_t launch_merge(const MergeArgs& a, hipStream_t s);
