@@ -399,6 +399,16 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         // the next stage's first A operands and this wave's part of stage s + 2, once every
         // wave has committed stage s + 1
         wait_committed(s + 1);
+        // Of this SIMD's pair (waves w and w ^ 4), the one behind issues first: the matrix
+        // unit otherwise favours the older wave, which runs a stage ahead and then idles at
+        // this wait while the other finishes and commits (one stage of slack is all three
+        // stage buffers allow). Partner past stage s + 1: this wave is behind.
+        {
+            const int partner = __hip_atomic_load(committed + (wave ^ 4), __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (partner > s + 1) __builtin_amdgcn_s_setprio(2);
+            else __builtin_amdgcn_s_setprio(0);
+        }
         if (s + 1 < nstages) {
             an0 = *reinterpret_cast<const float4*>(tile[rb_nxt] + j * kLdsStride + h * 4);
             an1 = *reinterpret_cast<const float4*>(tile[rb_nxt] + (32 + j) * kLdsStride + h * 4);
