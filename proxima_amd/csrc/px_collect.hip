@@ -51,7 +51,6 @@ namespace {
 
 constexpr int kStageBufs = 3;  // LDS stage buffers
 constexpr int kNormBufs = 4;   // LDS norm buffers (tile t + 2 is staged while t - 1 is tested)
-constexpr int kSpinLimit = 1 << 16;  // polls of a stage-sync wait (each one s_sleep 1)
 
 template <bool L2, bool MULTI, bool FILT, bool DYN, bool FULL>
 __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
@@ -152,36 +151,12 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     // reuse, so the one wait covers both. A wait gives up after kSpinLimit polls (about
     // 5 ms) and reports it (a.spin_fail), so that a wave always finishes.
     auto publish = [&](int v) __attribute__((always_inline)) {
-        if (lane == 0)
-            __hip_atomic_store(committed + wave, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        stage_publish(committed, wave, lane, v);
     };
-    // Every wave has committed stage ct: each lane polls committed[lane & 7]. The poll loop
-    // is one asm block: as a loop in the compiled code it split the stage's schedule and
-    // cost register spills. Its s_waitcnt makes the load acquire (LDS at workgroup scope
-    // needs no more), and the "memory" clobber keeps the stage buffer accesses after it.
-    // The poll count is early-clobber ("+&s"): as a plain in-out operand it may share a
-    // register with an equal input (it was given ct's, and each poll then raised the target).
     const unsigned caddr = (unsigned)(uintptr_t)(committed + (lane & 7));
     auto wait_committed = [&](int ct) __attribute__((always_inline)) {
-        int v, spins = 0;
-        unsigned long long m;
-        asm volatile(
-            ".Lpx_poll%=:\n"
-            "  ds_read_b32 %[v], %[addr]\n"
-            "  s_waitcnt lgkmcnt(0)\n"
-            "  v_cmp_lt_i32_e64 %[m], %[v], %[ct]\n"
-            "  s_cmp_lg_u64 %[m], 0\n"
-            "  s_cbranch_scc0 .Lpx_done%=\n"
-            "  s_add_u32 %[sp], %[sp], 1\n"
-            "  s_cmp_ge_u32 %[sp], %[lim]\n"
-            "  s_cbranch_scc1 .Lpx_done%=\n"
-            "  s_sleep 1\n"
-            "  s_branch .Lpx_poll%=\n"
-            ".Lpx_done%=:\n"
-            : [v] "=&v"(v), [m] "=&s"(m), [sp] "+&s"(spins)
-            : [addr] "v"(caddr), [ct] "s"(ct), [lim] "s"(kSpinLimit)
-            : "memory", "scc");
-        if (spins >= kSpinLimit && a.spin_fail && lane == 0) atomicOr(a.spin_fail, 1);
+        if (stage_wait(caddr, ct) >= kSpinLimit && a.spin_fail && lane == 0)
+            atomicOr(a.spin_fail, 1);
     };
 
     // A wave whose 32 queries are all padding (last query tile) only helps stage the
@@ -399,16 +374,9 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         // the next stage's first A operands and this wave's part of stage s + 2, once every
         // wave has committed stage s + 1
         wait_committed(s + 1);
-        // Of this SIMD's pair (waves w and w ^ 4), the one behind issues first: the matrix
-        // unit otherwise favours the older wave, which runs a stage ahead and then idles at
-        // this wait while the other finishes and commits (one stage of slack is all three
-        // stage buffers allow). Partner past stage s + 1: this wave is behind.
-        {
-            const int partner = __hip_atomic_load(committed + (wave ^ 4), __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_WORKGROUP);
-            if (partner > s + 1) __builtin_amdgcn_s_setprio(2);
-            else __builtin_amdgcn_s_setprio(0);
-        }
+        pair_priority(__hip_atomic_load(committed + (wave ^ 4), __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_WORKGROUP),
+                      s + 1);
         if (s + 1 < nstages) {
             an0 = *reinterpret_cast<const float4*>(tile[rb_nxt] + j * kLdsStride + h * 4);
             an1 = *reinterpret_cast<const float4*>(tile[rb_nxt] + (32 + j) * kLdsStride + h * 4);

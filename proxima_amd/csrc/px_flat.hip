@@ -136,8 +136,14 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     constexpr int kRowStep = NT / kF4PerRow;               // rows between a thread's loads
     constexpr int kPF = kTileRows / kRowStep;              // float4 per thread per stage
     static_assert(NT % kF4PerRow == 0 && kTileRows % kRowStep == 0, "uneven stage split");
-    __shared__ __attribute__((aligned(16))) float tile[2][kTileRows * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float tnorm[2][kTileRows];
+    static_assert(!COLLECT || WAVES == 8, "the collect stage sync is for eight waves");
+    // Stage buffers and norm slots. Lists: two buffers, a barrier per stage. Collect: three
+    // buffers and four norm slots, no barrier per stage (the stage sync of px_collect.hip's
+    // scan: a wave may run a stage ahead of the slowest).
+    constexpr int kBufs = COLLECT ? 3 : 2, kNorms = COLLECT ? 4 : 2;
+    __shared__ __attribute__((aligned(16))) float tile[kBufs][kTileRows * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float tnorm[kNorms][kTileRows];
+    __shared__ int committed[8];  // collect: the last stage each wave has committed
     __shared__ float lkeys[WAVES][32][KP];
     using IdT = typename ListId<KP>::type;
     __shared__ IdT lids[WAVES][32][KP];
@@ -375,9 +381,23 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         tile_ids(0);
         fetch(0);
         commit(0, 0, 0);
-        tile_ids(nch > 1 ? 0 : 1);  // ids for the tile of stage 1
+        if constexpr (COLLECT) {
+            // stage 1 in LDS too, ids for the tile of stage 2
+            int c1, c2;
+            int64_t t1, t2;
+            next_stage(0, 0, c1, t1);
+            next_stage(c1, t1, c2, t2);
+            tile_ids(t1);
+            fetch(c1);
+            commit(1, c1, (int)(t1 & (kNorms - 1)));
+            tile_ids(t2);
+        } else {
+            tile_ids(nch > 1 ? 0 : 1);  // ids for the tile of stage 1
+        }
     }
+    if (COLLECT && tid < 8) committed[tid] = 1;
     __syncthreads();
+    const unsigned caddr = (unsigned)(uintptr_t)(committed + (lane & 7));
 
     if constexpr (!COLLECT) {
         // A wave whose 32 queries are all padding (small batches) only helps stage the
@@ -405,11 +425,13 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     f32x16 acc0 = {0.f}, acc1 = {0.f};
     int c = 0;        // chunk of stage s
     int64_t ti = 0;   // its tile
+    int rb = 0;       // collect: its stage buffer (s % 3)
     for (int64_t s = 0; s < nstages; ++s) {
-        int c1, c2;
-        int64_t t1, t2;
+        int c1, c2, c3 = 0;
+        int64_t t1, t2, t3 = 0;
         next_stage(c, ti, c1, t1);
         next_stage(c1, t1, c2, t2);
+        if constexpr (COLLECT) next_stage(c2, t2, c3, t3);
         const int64_t t0 = row0 + ti * kTileRows;
         int gt_raw = kTotalKeyInf;
         if constexpr (!COLLECT)
@@ -420,15 +442,23 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         // finite, and padding queries' keys are never used.
         const int cn = c1;
         const int dcn = min(kChunk, a.dp - cn * kChunk);
-        fetch(c1);  // past the last stage every row is -1: harmless clamped loads
-        tile_ids(t2);  // ids for the tile of stage s + 2
+        // lists: stage s + 1's loads and the ids of stage s + 2's tile; collect: stage s + 2's
+        // and stage s + 3's (past the last stage every row is -1: harmless clamped loads)
+        if constexpr (COLLECT) {
+            fetch(c2);
+            tile_ids(t3);
+        } else {
+            fetch(c1);
+            tile_ids(t2);
+        }
         if (c == 0) {
             acc0 = (f32x16){0.f};
             acc1 = (f32x16){0.f};
         }
         const int ng = wave_live ? min(kChunk, a.dp - c * kChunk) >> 3 : 0;
-        const float* ta0 = tile[s & 1] + j * kLdsStride + h * 4;
-        const float* ta1 = tile[s & 1] + (32 + j) * kLdsStride + h * 4;
+        const int sb = COLLECT ? rb : (int)(s & 1);
+        const float* ta0 = tile[sb] + j * kLdsStride + h * 4;
+        const float* ta1 = tile[sb] + (32 + j) * kLdsStride + h * 4;
 #pragma unroll
         for (int g = 0; g < 16; ++g) {
             if (g < ng) {
@@ -466,7 +496,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             // the merge re-ranks exactly), so key = ||x||^2 - 2 q.x; IP key = -q.x.
             // (collect mode writes them straight into pkey, where the next tile's MFMA loop
             // tests them: the previous tile's keys there have been tested already)
-            const float* tn = tnorm[ti & 1];
+            const float* tn = tnorm[ti & (kNorms - 1)];
             float key_own[COLLECT ? 1 : 32];
             auto& key = [&]() -> float(&)[32] {
                 if constexpr (COLLECT) return pkey;
@@ -654,12 +684,25 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             }  // !COLLECT
         }
 
-        commit((int)((s + 1) & 1), c1, (int)(t1 & 1));
+        if constexpr (COLLECT) {
+            // every wave has committed stage s + 1 (so none still reads stage s - 1, whose
+            // buffer and norm slot stage s + 2 takes), then this wave's part of stage s + 2
+            if (stage_wait(caddr, (int)(s + 1)) >= kSpinLimit && a.spin_fail && lane == 0)
+                atomicOr(a.spin_fail, 1);
+            pair_priority(__hip_atomic_load(committed + (wave ^ 4), __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_WORKGROUP),
+                          (int)(s + 1));
+            commit(rb == 0 ? 2 : rb - 1, c2, (int)(t2 & (kNorms - 1)));
+            stage_publish(committed, wave, lane, (int)(s + 2));
+        } else {
+            commit((int)((s + 1) & 1), c1, (int)(t1 & 1));
+        }
         if (dyn && pub_now) {
             atomicMin(gbest + (split & 31), cpub);
             pub_now = false;
         }
-        __syncthreads();
+        if constexpr (!COLLECT) __syncthreads();
+        rb = rb == 2 ? 0 : rb + 1;
         c = c1;
         ti = t1;
     }

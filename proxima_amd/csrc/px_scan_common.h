@@ -25,6 +25,54 @@ __device__ __forceinline__ f32x16 mfma4(float4 a, float4 b, f32x16 c) {
     return c;
 }
 
+// Stage sync of the collect scans (no barrier per stage): each wave publishes in an 8-word
+// LDS array the last stage it has committed to a stage buffer (stage_publish, release), and
+// waits with stage_wait until every wave has committed a given stage (acquire).
+constexpr int kSpinLimit = 1 << 16;  // polls of a stage wait (each one s_sleep 1: ~5 ms)
+
+__device__ __forceinline__ void stage_publish(int* committed, int wave, int lane, int v) {
+    if (lane == 0)
+        __hip_atomic_store(committed + wave, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Polls until every word of the 8-word array is >= ct; addr: the LDS address of word
+// lane & 7. Returns the number of polls, kSpinLimit if it gave up (the caller reports it).
+// One asm block: as a compiled loop in the middle of an unrolled stage it split the
+// schedule and cost register spills. Its s_waitcnt makes the load acquire (LDS at workgroup
+// scope needs no more), and the "memory" clobber keeps the stage buffer accesses after it.
+// The poll count is early-clobber ("+&s"): as a plain in-out operand it may share a
+// register with an equal input (it was given ct's, and each poll then raised the target).
+__device__ __forceinline__ int stage_wait(unsigned addr, int ct) {
+    int v, spins = 0;
+    unsigned long long m;
+    asm volatile(
+        ".Lpx_poll%=:\n"
+        "  ds_read_b32 %[v], %[addr]\n"
+        "  s_waitcnt lgkmcnt(0)\n"
+        "  v_cmp_lt_i32_e64 %[m], %[v], %[ct]\n"
+        "  s_cmp_lg_u64 %[m], 0\n"
+        "  s_cbranch_scc0 .Lpx_done%=\n"
+        "  s_add_u32 %[sp], %[sp], 1\n"
+        "  s_cmp_ge_u32 %[sp], %[lim]\n"
+        "  s_cbranch_scc1 .Lpx_done%=\n"
+        "  s_sleep 1\n"
+        "  s_branch .Lpx_poll%=\n"
+        ".Lpx_done%=:\n"
+        : [v] "=&v"(v), [m] "=&s"(m), [sp] "+&s"(spins)
+        : [addr] "v"(addr), [ct] "s"(ct), [lim] "s"(kSpinLimit)
+        : "memory", "scc");
+    return spins;
+}
+
+// Of a SIMD's pair of waves (w and w ^ 4), the one behind issues first: the matrix unit
+// otherwise favours the older wave, which runs the one stage ahead the stage buffers allow
+// and then idles at its wait while the other finishes and commits. partner_committed: the
+// partner's published stage; mine: this wave's (the partner is behind when it is not past).
+__device__ __forceinline__ void pair_priority(int partner_committed, int mine) {
+    if (partner_committed > mine) __builtin_amdgcn_s_setprio(2);
+    else __builtin_amdgcn_s_setprio(0);
+}
+
 // Total-order int of a key (flat.rs:30's f32::total_cmp) and back; the mapping is its own
 // inverse. Shared thresholds are published as these ints with atomicMin.
 __device__ __forceinline__ float from_total_key(int t) {
