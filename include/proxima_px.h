@@ -36,7 +36,9 @@ extern "C" {
 #define PX_ERR_NONFINITE (-4)  /* NaN or infinite input (flat.rs:79-82, 114-117) */
 #define PX_ERR_ARG (-5)        /* null handle/pointer, negative size, bad metric or params */
 #define PX_ERR_UNTRAINED (-6)  /* PQ index used before train (crates/py/src/lib.rs:492-504) */
-#define PX_ERR_DEVICE (-7)     /* no usable gfx950 device */
+#define PX_ERR_DEVICE (-7)     /* no usable gfx950 device, or a device-side failure of the search
+                                  (a collect scan whose workgroup stage sync gave up: no
+                                  results; px_last_error names it) */
 
 /* Largest k of the reference's GPU seam (knn_gpu_search). px_flat_search* and
  * px_pq_search* take any k >= 0, as the reference's FlatIndex and PqIndex do

@@ -1,6 +1,8 @@
-"""CPU model check of the collect scan's stage sync (flat_collect_kernel, px_collect.hip).
+"""CPU model check of the collect scans' stage sync (flat_collect_kernel, px_collect.hip, and
+the collect mode of flat_scan_kernel, px_flat.hip, which reads a stage's first A operands at
+the start of the stage instead of after the wait before it: the same order).
 
-The kernel has no barrier per stage. Each wave publishes in LDS the last stage it has
+The kernels have no barrier per stage. Each wave publishes in LDS the last stage it has
 committed to a stage buffer (C). Stage s of a wave with queries:
 
     MFMAs over buffer s % 3 (its first A operands were read at the end of stage s - 1), and
