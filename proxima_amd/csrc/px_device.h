@@ -49,8 +49,9 @@ __device__ __forceinline__ int readlane_i(int v, int lane) {
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & 63u); }
 
-// List slot ids: int positions, or (for the larger list capacities, to fit more waves in
-// LDS) 16-bit offsets from the split's first position with 0xffff as the empty sentinel.
+// List slot ids: int positions, or (to fit the lists of eight waves beside three stage
+// buffers, or more waves beside two) 16-bit offsets from the split's first position with
+// 0xffff as the empty sentinel.
 template <typename IdT>
 __device__ __forceinline__ int id_load(IdT v, int base) {
     if constexpr (sizeof(IdT) == 2) return v == 0xffff ? kIdNone : base + (int)v;

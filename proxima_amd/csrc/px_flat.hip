@@ -29,13 +29,15 @@ int flat_list_capacity(int kl) {
     if (kl <= 120) return 120;
     return 128;
 }
-bool flat_list_narrow_ids(int kp) { return kp == 56 || kp == 120; }
-// Waves per workgroup: the waves share one double-buffered corpus stage (67.6 KB of LDS);
-// the per-wave candidate lists take 32 * KP * (4 + id bytes) each.
+bool flat_list_narrow_ids(int kp) { return kp == 32 || kp == 56 || kp == 120; }
+// Waves per workgroup: the waves share the corpus stage buffers (two, 67.6 KB of LDS; three
+// for lists of 32, 101.4 KB); the per-wave candidate lists take 32 * KP * (4 + id bytes)
+// each.
 constexpr int flat_waves(int kp) { return kp <= 56 ? 8 : (kp <= 120 ? 4 : 2); }
 template <int KP>
 struct ListId {
-    using type = typename std::conditional<KP == 56 || KP == 120, unsigned short, int>::type;
+    using type =
+        typename std::conditional<KP == 32 || KP == 56 || KP == 120, unsigned short, int>::type;
 };
 int flat_queries_per_block(int kp) { return 32 * flat_waves(kp); }
 
@@ -136,14 +138,17 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     constexpr int kRowStep = NT / kF4PerRow;               // rows between a thread's loads
     constexpr int kPF = kTileRows / kRowStep;              // float4 per thread per stage
     static_assert(NT % kF4PerRow == 0 && kTileRows % kRowStep == 0, "uneven stage split");
-    static_assert(!COLLECT || WAVES == 8, "the collect stage sync is for eight waves");
-    // Stage buffers and norm slots. Lists: two buffers, a barrier per stage. Collect: three
-    // buffers and four norm slots, no barrier per stage (the stage sync of px_collect.hip's
-    // scan: a wave may run a stage ahead of the slowest).
-    constexpr int kBufs = COLLECT ? 3 : 2, kNorms = COLLECT ? 4 : 2;
+    // Stage buffers and norm slots. Collect mode and lists of 32: three buffers and four
+    // norm slots, no barrier per stage (the stage sync of px_collect.hip's scan: a wave may
+    // run a stage ahead of the slowest, so that one wave's list insertions or appends do not
+    // hold up the others). Longer lists: two buffers (a third does not fit beside them), a
+    // barrier per stage.
+    constexpr bool RELAXED = COLLECT || KP == 32;
+    static_assert(!RELAXED || WAVES == 8, "the stage sync is for eight waves");
+    constexpr int kBufs = RELAXED ? 3 : 2, kNorms = RELAXED ? 4 : 2;
     __shared__ __attribute__((aligned(16))) float tile[kBufs][kTileRows * kLdsStride];
     __shared__ __attribute__((aligned(16))) float tnorm[kNorms][kTileRows];
-    __shared__ int committed[8];  // collect: the last stage each wave has committed
+    __shared__ int committed[8];  // RELAXED: the last stage each wave has committed
     __shared__ float lkeys[WAVES][32][KP];
     using IdT = typename ListId<KP>::type;
     __shared__ IdT lids[WAVES][32][KP];
@@ -381,7 +386,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         tile_ids(0);
         fetch(0);
         commit(0, 0, 0);
-        if constexpr (COLLECT) {
+        if constexpr (RELAXED) {
             // stage 1 in LDS too, ids for the tile of stage 2
             int c1, c2;
             int64_t t1, t2;
@@ -395,7 +400,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             tile_ids(nch > 1 ? 0 : 1);  // ids for the tile of stage 1
         }
     }
-    if (COLLECT && tid < 8) committed[tid] = 1;
+    if (RELAXED && tid < 8) committed[tid] = 1;
     __syncthreads();
     const unsigned caddr = (unsigned)(uintptr_t)(committed + (lane & 7));
 
@@ -406,17 +411,31 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         if (qt * (WAVES * 32) + wave * 32 >= a.nq) {
             int c = 0;
             int64_t t = 0;
+            int rb = 0;
             for (int64_t s = 0; s < nstages; ++s) {
                 int c1, c2;
                 int64_t t1, t2;
                 next_stage(c, t, c1, t1);
                 next_stage(c1, t1, c2, t2);
-                fetch(c1);
-                tile_ids(t2);
-                commit((int)((s + 1) & 1), c1, (int)(t1 & 1));
+                if constexpr (RELAXED) {
+                    int c3;
+                    int64_t t3;
+                    next_stage(c2, t2, c3, t3);
+                    fetch(c2);
+                    tile_ids(t3);
+                    if (stage_wait(caddr, (int)(s + 1)) >= kSpinLimit && a.spin_fail && lane == 0)
+                        atomicOr(a.spin_fail, 1);
+                    commit(rb == 0 ? 2 : rb - 1, c2, (int)(t2 & (kNorms - 1)));
+                    stage_publish(committed, wave, lane, (int)(s + 2));
+                    rb = rb == 2 ? 0 : rb + 1;
+                } else {
+                    fetch(c1);
+                    tile_ids(t2);
+                    commit((int)((s + 1) & 1), c1, (int)(t1 & 1));
+                    __syncthreads();
+                }
                 c = c1;
                 t = t1;
-                __syncthreads();
             }
             return;
         }
@@ -425,13 +444,13 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     f32x16 acc0 = {0.f}, acc1 = {0.f};
     int c = 0;        // chunk of stage s
     int64_t ti = 0;   // its tile
-    int rb = 0;       // collect: its stage buffer (s % 3)
+    int rb = 0;       // RELAXED: its stage buffer (s % 3)
     for (int64_t s = 0; s < nstages; ++s) {
         int c1, c2, c3 = 0;
         int64_t t1, t2, t3 = 0;
         next_stage(c, ti, c1, t1);
         next_stage(c1, t1, c2, t2);
-        if constexpr (COLLECT) next_stage(c2, t2, c3, t3);
+        if constexpr (RELAXED) next_stage(c2, t2, c3, t3);
         const int64_t t0 = row0 + ti * kTileRows;
         int gt_raw = kTotalKeyInf;
         if constexpr (!COLLECT)
@@ -442,9 +461,10 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         // finite, and padding queries' keys are never used.
         const int cn = c1;
         const int dcn = min(kChunk, a.dp - cn * kChunk);
-        // lists: stage s + 1's loads and the ids of stage s + 2's tile; collect: stage s + 2's
-        // and stage s + 3's (past the last stage every row is -1: harmless clamped loads)
-        if constexpr (COLLECT) {
+        // barrier per stage: stage s + 1's loads and the ids of stage s + 2's tile; RELAXED:
+        // stage s + 2's and stage s + 3's (past the last stage every row is -1: harmless
+        // clamped loads)
+        if constexpr (RELAXED) {
             fetch(c2);
             tile_ids(t3);
         } else {
@@ -456,7 +476,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             acc1 = (f32x16){0.f};
         }
         const int ng = wave_live ? min(kChunk, a.dp - c * kChunk) >> 3 : 0;
-        const int sb = COLLECT ? rb : (int)(s & 1);
+        const int sb = RELAXED ? rb : (int)(s & 1);
         const float* ta0 = tile[sb] + j * kLdsStride + h * 4;
         const float* ta1 = tile[sb] + (32 + j) * kLdsStride + h * 4;
 #pragma unroll
@@ -684,7 +704,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             }  // !COLLECT
         }
 
-        if constexpr (COLLECT) {
+        if constexpr (RELAXED) {
             // every wave has committed stage s + 1 (so none still reads stage s - 1, whose
             // buffer and norm slot stage s + 2 takes), then this wave's part of stage s + 2
             if (stage_wait(caddr, (int)(s + 1)) >= kSpinLimit && a.spin_fail && lane == 0)
@@ -701,7 +721,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             atomicMin(gbest + (split & 31), cpub);
             pub_now = false;
         }
-        if constexpr (!COLLECT) __syncthreads();
+        if constexpr (!RELAXED) __syncthreads();
         rb = rb == 2 ? 0 : rb + 1;
         c = c1;
         ti = t1;
