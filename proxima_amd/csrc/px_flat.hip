@@ -1428,6 +1428,11 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
 __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
     constexpr int kPer = kMaxLadderEntries / 1024;
     constexpr unsigned kNone = 0xffffffffu;
+    constexpr int kWaves = 16;
+    // the first pass counts every key once for both rungs, into one histogram per wave (16
+    // waves contending for 256 bins cost more than the sum over waves afterwards); the later
+    // passes count only the keys under a rung's prefix, few, straight into the rung's bins
+    __shared__ unsigned whist[kWaves][256];
     __shared__ unsigned hist[kRungs][256];
     __shared__ unsigned s_prefix[kRungs], s_rank[kRungs];
     const int q = blockIdx.x;
@@ -1445,22 +1450,37 @@ __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
         s_prefix[t] = 0;
         s_rank[t] = (unsigned)a.ranks[t];
     }
+    for (int x = t; x < kWaves * 256; x += blockDim.x) (&whist[0][0])[x] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+        if (u[i] != kNone) atomicAdd(&whist[wv][u[i] >> 24], 1u);
+    __syncthreads();
+    for (int x = t; x < 256; x += blockDim.x) {
+        unsigned c = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) c += whist[w][x];
+#pragma unroll
+        for (int r = 0; r < kRungs; ++r) hist[r][x] = c;
+    }
+    __syncthreads();
     for (int pass = 0; pass < 3; ++pass) {
         const int shift = 24 - 8 * pass;  // digit bits [shift, shift + 8)
-        for (int x = t; x < kRungs * 256; x += blockDim.x) (&hist[0][0])[x] = 0;
-        __syncthreads();
+        if (pass > 0) {
+            for (int x = t; x < kRungs * 256; x += blockDim.x) (&hist[0][0])[x] = 0;
+            __syncthreads();
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-            if (u[i] == kNone) continue;
-            const unsigned d = (u[i] >> shift) & 0xffu;
+            for (int i = 0; i < kPer; ++i) {
+                if (u[i] == kNone) continue;
+                const unsigned d = (u[i] >> shift) & 0xffu;
 #pragma unroll
-            for (int r = 0; r < kRungs; ++r) {
-                // keys whose higher digits match the rung's prefix so far
-                const bool match = pass == 0 || (u[i] >> (shift + 8)) == s_prefix[r];
-                if (match) atomicAdd(&hist[r][d], 1u);
+                for (int r = 0; r < kRungs; ++r) {
+                    // keys whose higher digits match the rung's prefix so far
+                    if ((u[i] >> (shift + 8)) == s_prefix[r]) atomicAdd(&hist[r][d], 1u);
+                }
             }
+            __syncthreads();
         }
-        __syncthreads();
         if (wv < kRungs) {
             // lane holds bins 4 lane .. 4 lane + 3; inclusive scan across the wave
             unsigned c[4], sum = 0;
