@@ -1358,6 +1358,90 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
         __syncthreads();
         avail = s_total;
     }
+    // Many more candidates than the kk it keeps (a threshold round holds several times kk):
+    // the kk-th smallest key by a radix select (four 8-bit passes over the order-preserving
+    // unsigned form of the total-order key, so the key is exact), then only the candidates
+    // at or below it (at least kk, ties included) are compacted and sorted.
+    if (avail > 512 && avail > 4 * a.kk) {
+        __shared__ unsigned rhist[256];
+        __shared__ unsigned s_pre, s_need;
+        if (t == 0) {
+            s_pre = 0;
+            s_need = (unsigned)a.kk;
+        }
+        for (int pass = 0; pass < 4; ++pass) {
+            const int shift = 24 - 8 * pass;  // digit bits [shift, shift + 8)
+            for (int x = t; x < 256; x += nt) rhist[x] = 0;
+            __syncthreads();
+            const unsigned pre = s_pre;
+            for (int x = t; x < avail; x += nt) {
+                const unsigned u = (unsigned)total_key(sk[x]) ^ 0x80000000u;
+                if (pass == 0 || (u >> (shift + 8)) == pre) atomicAdd(&rhist[(u >> shift) & 0xffu], 1u);
+            }
+            __syncthreads();
+            if (t < 64) {
+                // lane t holds bins 4t .. 4t + 3; the bin where the count reaches s_need
+                unsigned c[4], sum = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    c[e] = rhist[4 * t + e];
+                    sum += c[e];
+                }
+                unsigned incl = sum;
+                for (int off = 1; off < 64; off <<= 1) {
+                    const unsigned v = __shfl_up(incl, off);
+                    if (lane >= off) incl += v;
+                }
+                const unsigned need = s_need;
+                unsigned before = incl - sum;
+                int digit = -1;
+                unsigned below = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (digit < 0 && before + c[e] >= need) {
+                        digit = 4 * t + e;
+                        below = before;
+                    }
+                    before += c[e];
+                }
+                // some bin reaches it: need <= the keys under the prefix, at least kk at first
+                const unsigned long long m = __ballot(digit >= 0);
+                const int src = __builtin_ctzll(m);
+                const int dsel = __shfl(digit, src);
+                const unsigned bsel = __shfl(below, src);
+                if (t == 0) {
+                    s_pre = (pre << 8) | (unsigned)dsel;
+                    s_need = need - bsel;
+                }
+            }
+            __syncthreads();
+        }
+        const unsigned kth = s_pre;
+        // this thread's entries (at most lcap / blockDim = 16), then the survivors to the front
+        constexpr int kHeld = kMaxCollect / 1024;
+        PX_DCHECK(a.dbg, kDbgFlat, avail <= kHeld * nt);
+        float ck[kHeld];
+        int ci[kHeld];
+#pragma unroll
+        for (int u = 0; u < kHeld; ++u) {
+            const int x = t + u * nt;
+            ck[u] = x < avail ? sk[x] : kInf;
+            ci[u] = x < avail ? si[x] : kIdNone;
+        }
+        if (t == 0) s_total = 0;
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < kHeld; ++u) {
+            const int x = t + u * nt;
+            if (x < avail && ((unsigned)total_key(ck[u]) ^ 0x80000000u) <= kth) {
+                const int i = atomicAdd(&s_total, 1);
+                sk[i] = ck[u];
+                si[i] = ci[u];
+            }
+        }
+        __syncthreads();
+        avail = s_total;
+    }
     int p = 1;
     while (p < avail) p <<= 1;
     for (int x = avail + threadIdx.x; x < p; x += blockDim.x) {
