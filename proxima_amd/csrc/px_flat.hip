@@ -1358,11 +1358,11 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
         __syncthreads();
         avail = s_total;
     }
-    // Many more candidates than the kk it keeps (a threshold round holds several times kk):
+    // Many more candidates than the kk it keeps (a threshold round holds two to ten times kk):
     // the kk-th smallest key by a radix select (four 8-bit passes over the order-preserving
     // unsigned form of the total-order key, so the key is exact), then only the candidates
     // at or below it (at least kk, ties included) are compacted and sorted.
-    if (avail > 512 && avail > 4 * a.kk) {
+    if (avail > 512 && avail > 2 * a.kk) {
         __shared__ unsigned rhist[256];
         __shared__ unsigned s_pre, s_need;
         if (t == 0) {

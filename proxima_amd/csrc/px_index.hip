@@ -764,6 +764,14 @@ int run_collect(CollectJob& j) {
             // sorts only those below the final bound: 32 KB of LDS lets five selects share a
             // CU where 64 KB let two (more than 4,096 candidates counts as an overflow)
             if (j.sel_gbest) lcap = std::max<int64_t>(std::min<int64_t>(lcap, 4096), 2 * kk + 1);
+            // a sampled first round holds about `expect` candidates a query (its threshold
+            // sits five standard deviations above the k'-th): where twice that fits 8,192
+            // entries the select takes no more (64 KB of LDS: two workgroups a CU, where room
+            // for every region full took 128 KB and one; 1M x 128, k = 1000); more is an
+            // overflow. Later rounds keep the room of their regions.
+            else if (round == 0 && 2.0 * expect + 1 <= 8192.0 && 2 * kk + 1 <= 8192) {
+                lcap = std::min<int64_t>(lcap, 8192);
+            }
 
             PX_INTERNAL(lcap >= 1 && lcap <= px::kMaxCollect && (lcap & (lcap - 1)) == 0);
             PX_INTERNAL((size_t)(take * regions) * 4 <= ws.cand_n.cap);
