@@ -1020,12 +1020,47 @@ hipError_t launch_copy_to_host(const int* src, int* host_dst, int64_t n, hipStre
     return hipGetLastError();
 }
 
-// In-LDS bitonic sort (ascending by (key total-order, id)) of p = 2^x entries.
+// In-LDS bitonic sort (ascending by (key total-order, id)) of p = 2^x entries. A stage of
+// stride 64 or more exchanges through LDS between barriers; the stages of stride below 64
+// pair entries whose indices differ only in their low six bits, and entry x is handled by
+// thread x % blockDim (a multiple of 64), so they pair lanes of one wave: each run of them
+// is one pass in registers with cross-lane shuffles. 1,024 entries: 16 barriers, not 56.
 __device__ void bitonic_sort(float* sk, int* si, int p) {
-    for (int size = 2; size <= p; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+    const int nt = blockDim.x, t = threadIdx.x;
+    const float kInf = __int_as_float(0x7f800000);
+    // merge sizes size_from .. size_to, each with its strides below 64 (entries past p are
+    // padding that no entry below p pairs with)
+    auto reg_pass = [&](int size_from, int size_to) {
+        for (int base = 0; base < p; base += nt) {
+            const int x = base + t;
+            const bool live = x < p;
+            float k = live ? sk[x] : kInf;
+            int id = live ? si[x] : kIdNone;
+            for (int size = size_from; size <= size_to; size <<= 1) {
+                const bool asc = (x & size) == 0;
+                for (int st = min(size >> 1, 32); st > 0; st >>= 1) {
+                    const float ko = __shfl_xor(k, st);
+                    const int io = __shfl_xor(id, st);
+                    // the lower entry of an ascending pair keeps the smaller (and so on)
+                    const bool other_less = cand_less(ko, io, k, id);
+                    if (((x & st) == 0) == asc ? other_less : !other_less) {
+                        k = ko;
+                        id = io;
+                    }
+                }
+            }
+            if (live) {
+                sk[x] = k;
+                si[x] = id;
+            }
+        }
+    };
+    __syncthreads();
+    reg_pass(2, min(p, 64));
+    for (int size = 128; size <= p; size <<= 1) {
+        for (int stride = size >> 1; stride >= 64; stride >>= 1) {
             __syncthreads();
-            for (int x = threadIdx.x; x < (p >> 1); x += blockDim.x) {
+            for (int x = t; x < (p >> 1); x += nt) {
                 const int lo = 2 * x - (x & (stride - 1));
                 const int hi = lo + stride;
                 const bool asc = (lo & size) == 0;
@@ -1037,6 +1072,8 @@ __device__ void bitonic_sort(float* sk, int* si, int p) {
                 }
             }
         }
+        __syncthreads();
+        reg_pass(size, size);
     }
     __syncthreads();
 }
