@@ -37,6 +37,7 @@ sys.path.insert(0, ROOT)
 from proxima_amd import FlatIndex, Metric, PqIndex, _lib, datagen  # noqa: E402
 
 FP32_MFMA_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix peak
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 matrix peak
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
 
 
@@ -293,18 +294,23 @@ def bench_flat(args, dev):
         if search(*search_args):
             raise RuntimeError(_lib.last_error())
 
+    def timed_loop(steps, warmup):
+        for _ in range(warmup):
+            step()
+        scan, total = [], []
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+            read_timing(*timing_args)
+            scan.append(ev_scan.value)
+            total.append(ev_total.value)
+        return time.perf_counter() - t0, scan, total
+
     idx._timing(True)
-    for _ in range(args.warmup):
-        step()
-    log("[bench] warmup done")
-    scan_ms, total_ms = [], []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-        read_timing(*timing_args)
-        scan_ms.append(ev_scan.value)
-        total_ms.append(ev_total.value)
-    elapsed = time.perf_counter() - t0
+    # the metric is the fp32 scan's: the fp16 scan (rows and queries exact in fp16) is timed
+    # after it, as its own object of the line
+    idx._scan_f16(False)
+    elapsed, scan_ms, total_ms = timed_loop(args.steps, args.warmup)
     info = idx._last_timing()
     log(f"[bench] {args.steps} steps in {elapsed:.3f} s; scan {np.mean(scan_ms):.3f} ms, "
         f"pipeline {np.mean(total_ms):.3f} ms, splits {info['splits']}, blocks {info['blocks']}")
@@ -320,6 +326,29 @@ def bench_flat(args, dev):
                                                              dists.view(np.uint32)))
     log(f"[bench] host-buffer search_batch: {hb['ms_median']:.3f} ms median of 7, "
         f"{hb['value']:.0f} QPS")
+
+    # the same searches with the collect scan multiplying in fp16, where every value of the
+    # rows and queries is exact in fp16 (the products are then exact either way)
+    f16 = None
+    if not args.no_f16:
+        idx._scan_f16(True)
+        el16, scan16, total16 = timed_loop(args.steps, max(args.warmup, 1))
+        info16 = idx._last_timing()
+        if info16["scan_f16"]:
+            ids16 = dev.get(di, np.empty((nq, k), dtype=np.int64))
+            d16 = dev.get(dd, np.empty((nq, k), dtype=np.float32))
+            fl16 = 2.0 * nq * n_eff * dim / (np.mean(scan16) * 1e-3) / 1e12
+            f16 = {"value": nq * args.steps / el16, "unit": "queries/s",
+                   "ms_per_step": el16 / args.steps * 1e3,
+                   "kernel_ms": float(np.mean(scan16)), "pipeline_ms": float(np.mean(total16)),
+                   "achieved_tflops": fl16, "peak_tflops": FP16_MFMA_PEAK_TFLOPS,
+                   "frac": fl16 / FP16_MFMA_PEAK_TFLOPS, "collect_rounds": info16["collect_rounds"],
+                   "same_results_as_fp32_scan": bool(
+                       np.array_equal(ids16, ids) and
+                       np.array_equal(d16.view(np.uint32), dists.view(np.uint32)))}
+            log(f"[bench] fp16 scan: {f16['ms_per_step']:.3f} ms a batch, {f16['value']:.0f} QPS, "
+                f"scan {f16['kernel_ms']:.3f} ms, same results {f16['same_results_as_fp32_scan']}")
+        idx._scan_f16(False)
 
     flops = 2.0 * nq * n_eff * dim
     # rows of exactly 128 padded dims take flat_collect_kernel, other widths the collect mode
@@ -359,6 +388,8 @@ def bench_flat(args, dev):
         "pipeline_ms": float(np.mean(total_ms)),
         "host_buffer": hb,
     }
+    if f16 is not None:
+        result["f16_exact_scan"] = f16
     ctr = read_counters(COUNTER_PROFILES.get((c, n, nq, k, info["path"]), ""), not args.sift)
     if ctr and "mfma_busy_frac" in ctr:
         result["roofline"]["mfma_busy"] = {
@@ -514,6 +545,9 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 5],
                     help="flat: which FlatIndex workload (3, the headline, by default)")
     ap.add_argument("--k", type=int, default=None, help="override the workload's k")
+    ap.add_argument("--no-f16", action="store_true",
+                    help="flat: skip the timing of the fp16 collect scan (rows and queries "
+                         "exact in fp16)")
     ap.add_argument("--n", type=int, default=None, help="override the corpus rows")
     ap.add_argument("--nq", type=int, default=None, help="override the query count")
     ap.add_argument("--copy-mib", type=int, default=1024, help="copy: MiB per launch")

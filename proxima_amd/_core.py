@@ -266,18 +266,25 @@ class FlatIndex:
     def _timing(self, enable: bool = True) -> None:
         _check(self._lib.px_flat_set_timing(self._h, 1 if enable else 0))
 
+    def _scan_f16(self, enable: bool = True) -> None:
+        """Let the collect scan multiply in fp16 when rows and queries are exact in fp16
+        (default on); off keeps it on fp32. Diagnostic; no counterpart in the reference."""
+        _check(self._lib.px_flat_set_scan_f16(self._h, 1 if enable else 0))
+
     def _last_timing(self) -> dict:
         scan, total = ctypes.c_float(), ctypes.c_float()
         splits, blocks = ctypes.c_int(), ctypes.c_int()
         _check(self._lib.px_flat_last_timing(self._h, ctypes.byref(scan), ctypes.byref(total),
                                              ctypes.byref(splits), ctypes.byref(blocks)))
-        rounds, path = ctypes.c_int(), ctypes.c_int()
+        rounds, path, f16 = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
         _check(self._lib.px_flat_last_rounds(self._h, ctypes.byref(rounds)))
         _check(self._lib.px_flat_last_path(self._h, ctypes.byref(path)))
+        _check(self._lib.px_flat_last_scan_f16(self._h, ctypes.byref(f16)))
         return {"scan_ms": scan.value, "total_ms": total.value, "splits": splits.value,
                 "blocks": blocks.value, "collect_rounds": rounds.value,
                 "path": ("lists", "collect-sampled", "collect-bounded", "vector",
-                         "full-sort")[path.value]}
+                         "full-sort")[path.value],
+                "scan_f16": bool(f16.value)}
 
 
 class PqIndex:

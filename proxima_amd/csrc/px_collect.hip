@@ -52,13 +52,22 @@ namespace {
 constexpr int kStageBufs = 3;  // LDS stage buffers
 constexpr int kNormBufs = 4;   // LDS norm buffers (tile t + 2 is staged while t - 1 is tested)
 
-template <bool L2, bool MULTI, bool FILT, bool DYN, bool FULL>
+template <bool L2, bool MULTI, bool FILT, bool DYN, bool FULL, bool H16>
 __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     constexpr int NT = 512;
-    constexpr int kF4PerRow = kChunk / 4;        // 32 float4 per staged row
-    constexpr int kRowStep = NT / kF4PerRow;     // 16 rows between a thread's loads
-    constexpr int kPF = kTileRows / kRowStep;    // 4 float4 per thread per stage
+    // H16: rows and queries as fp16 (FlatScanArgs::corpus_h, queries_h), 16 dims a MFMA;
+    // a staged row is 256 bytes (else 512), its LDS pitch 16 bytes more (conflict-free b128
+    // reads: sixteen consecutive rows' same piece fall in sixteen different bank groups)
+    constexpr int kRowBytes = H16 ? kChunk * 2 : kChunk * 4;
+    constexpr int kPitch = kRowBytes + 16;
+    constexpr int kF4PerRow = kRowBytes / 16;    // 16-byte pieces per staged row (32; H16 16)
+    constexpr int kRowStep = NT / kF4PerRow;     // rows between a thread's loads (16; H16 32)
+    constexpr int kPF = kTileRows / kRowStep;    // pieces per thread per stage (4; H16 2)
+    constexpr int NG = H16 ? 8 : 16;             // MFMA dim groups per 128-dim chunk
+    constexpr int KPG = 32 / NG;                 // keys of the previous tile tested per group
     static_assert(NT % kF4PerRow == 0 && kTileRows % kRowStep == 0, "uneven stage split");
+    static_assert(!(H16 && MULTI), "fp16 rows are one 128-dim chunk");
+    static_assert(kTileRows * kPitch <= kTileRows * kLdsStride * 4, "stage buffer too small");
     static_assert(!(DYN && MULTI), "the shared bound serves one-chunk scans");
     __shared__ __attribute__((aligned(16))) float tile[kStageBufs][kTileRows * kLdsStride];
     __shared__ __attribute__((aligned(16))) float tnorm[kNormBufs][kTileRows];
@@ -106,25 +115,33 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         const int v = FILT ? a.rowidx[min(pos, (int64_t)row1 - 1)] : (int)pos;
         pid = (tid < kTileRows && pos < row1) ? v : -1;
     };
-    static_assert(kPF == 4, "four staged float4 per thread");
+    static_assert(kPF == (H16 ? 2 : 4), "four staged pieces per thread (fp16: two)");
     float4 pf0, pf1, pf2, pf3;  // separate variables: an array of them ended up in memory
     float pn = 0.f;
     auto fetch = [&](int s) __attribute__((always_inline)) {
         const int c = MULTI ? (int)(s % nch) : 0;
-        const int f4r = min(kChunk, a.dp - c * kChunk) >> 2;
-        const float* base = a.corpus + c * kChunk + min(cc, f4r - 1) * 4;
-        pf0 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[0], 0) * a.dp);
-        pf1 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[1], 0) * a.dp);
-        pf2 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[2], 0) * a.dp);
-        pf3 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[3], 0) * a.dp);
+        if constexpr (H16) {
+            const unsigned short* base = a.corpus_h + cc * 8;
+            pf0 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[0], 0) * kChunk);
+            pf1 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[1], 0) * kChunk);
+        } else {
+            const int f4r = min(kChunk, a.dp - c * kChunk) >> 2;
+            const float* base = a.corpus + c * kChunk + min(cc, f4r - 1) * 4;
+            pf0 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[0], 0) * a.dp);
+            pf1 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[1], 0) * a.dp);
+            pf2 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[2], 0) * a.dp);
+            pf3 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[3], 0) * a.dp);
+        }
         if (L2 && c == 0) pn = a.norms[max(pid, 0)];
     };
     auto commit = [&](int s, int buf) __attribute__((always_inline)) {
-        float* tb = tile[buf] + rr0 * kLdsStride + cc * 4;
+        char* tb = reinterpret_cast<char*>(tile[buf]) + rr0 * kPitch + cc * 16;
         *reinterpret_cast<float4*>(tb) = pf0;
-        *reinterpret_cast<float4*>(tb + kRowStep * kLdsStride) = pf1;
-        *reinterpret_cast<float4*>(tb + 2 * kRowStep * kLdsStride) = pf2;
-        *reinterpret_cast<float4*>(tb + 3 * kRowStep * kLdsStride) = pf3;
+        *reinterpret_cast<float4*>(tb + kRowStep * kPitch) = pf1;
+        if constexpr (!H16) {
+            *reinterpret_cast<float4*>(tb + 2 * kRowStep * kPitch) = pf2;
+            *reinterpret_cast<float4*>(tb + 3 * kRowStep * kPitch) = pf3;
+        }
         const int c = MULTI ? (int)(s % nch) : 0;
         if (L2 && c == 0 && tid < kTileRows) tnorm[(s / nch) & (kNormBufs - 1)][tid] = pn;
     };
@@ -266,19 +283,29 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
 
     // query chunk 0 (MFMA B operand): dims past the chunk's end are loaded clamped and never
     // multiplied; padding query slots load query 0's row and are never tested
+    // (H16: dims 16 g + 8 h .. + 7 of the query, fp16)
     const float* qrow = a.queries + (int64_t)(qvalid ? q : 0) * a.dp;
-    float4 b[16];
-    {
+    using Frag = std::conditional_t<H16, f16x8, float4>;  // one lane's operand of a dim group
+    Frag b[NG];
+    if constexpr (H16) {
+        const unsigned short* qh = a.queries_h + (int64_t)(qvalid ? q : 0) * kChunk + h * 8;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) b[g] = *reinterpret_cast<const f16x8*>(qh + g * 16);
+    } else {
         const int dc = min(kChunk, a.dp);
 #pragma unroll
-        for (int g = 0; g < 16; ++g)
+        for (int g = 0; g < NG; ++g)
             b[g] = *reinterpret_cast<const float4*>(qrow + min(g * 8 + h * 4, dc - 4));
     }
 
     f32x16 accA[2], accB[2];
-    // A operands of the next stage's first dim group (read at the end of each stage)
-    float4 an0 = *reinterpret_cast<const float4*>(tile[0] + j * kLdsStride + h * 4);
-    float4 an1 = *reinterpret_cast<const float4*>(tile[0] + (32 + j) * kLdsStride + h * 4);
+    // A operands of the next stage's first dim group (read at the end of each stage): rows
+    // j and 32 + j, the lane's 16 bytes of a 32-byte dim group
+    auto tile_at = [&](int buf, int row) __attribute__((always_inline)) {
+        return reinterpret_cast<const char*>(tile[buf]) + row * kPitch + h * 16;
+    };
+    Frag an0 = *reinterpret_cast<const Frag*>(tile_at(0, j));
+    Frag an1 = *reinterpret_cast<const Frag*>(tile_at(0, 32 + j));
     int rb_cur = 0;  // LDS buffer of the current stage
     int s = 0;       // stage index
 
@@ -303,44 +330,52 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         }
         const int pt0 = row0 + (t - 1) * kTileRows;  // first position of tile t - 1
         float vmin = kInf;  // DYN: smallest key of tile t - 1
-        // dim groups of this chunk (FULL: dp is a multiple of 128, every chunk has 16)
-        const int ng = FULL ? 16 : min(kChunk, a.dp - c * kChunk) >> 3;
+        // dim groups of this chunk (FULL: dp is a multiple of 128, every chunk has all NG)
+        const int ng = FULL ? NG : min(kChunk, a.dp - c * kChunk) >> 3;
         const int cn = MULTI ? (c + 1 == nch ? 0 : c + 1) : 0;
         const int dcn = min(kChunk, a.dp - cn * kChunk);
-        const float* ta0 = tile[rb_cur] + j * kLdsStride + h * 4;
-        const float* ta1 = tile[rb_cur] + (32 + j) * kLdsStride + h * 4;
+        const char* ta0 = tile_at(rb_cur, j);
+        const char* ta1 = tile_at(rb_cur, 32 + j);
         float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
+        for (int g = 0; g < NG; ++g) {
             if (g < ng) {
-                const float4 x0 = g == 0 ? an0 : *reinterpret_cast<const float4*>(ta0 + g * 8);
-                const float4 x1 = g == 0 ? an1 : *reinterpret_cast<const float4*>(ta1 + g * 8);
+                const Frag x0 = g == 0 ? an0 : *reinterpret_cast<const Frag*>(ta0 + g * 32);
+                const Frag x1 = g == 0 ? an1 : *reinterpret_cast<const Frag*>(ta1 + g * 32);
                 if (g == 0 && first) {
-                    cur[0] = mfma4z(x0, b[0]);
-                    cur[1] = mfma4z(x1, b[0]);
+                    cur[0] = mfma_group_z(x0, b[0]);
+                    cur[1] = mfma_group_z(x1, b[0]);
                 } else {
-                    cur[0] = mfma4(x0, b[g], cur[0]);
-                    cur[1] = mfma4(x1, b[g], cur[1]);
+                    cur[0] = mfma_group(x0, b[g], cur[0]);
+                    cur[1] = mfma_group(x1, b[g], cur[1]);
                 }
             }
             if constexpr (MULTI)
                 b[g] = *reinterpret_cast<const float4*>(qrow + cn * kChunk +
                                                         min(g * 8 + h * 4, dcn - 4));
             if constexpr (TEST) {
-                // rows x = 2g, 2g + 1 of tile t - 1: block rb = g / 8, MFMA rows r, r + 1
-                const int rb = g >> 3, r = (2 * g) & 15;
+                // rows x = KPG g .. KPG g + KPG - 1 of tile t - 1: block rb = x / 16, MFMA
+                // rows r .. r + KPG - 1
+                const int rb = (KPG * g) >> 4, r = (KPG * g) & 15;
                 if (!keys_ready) {
-                    if (L2 && (g & 1) == 0)
+                    if (L2 && (r & 3) == 0)
                         nv = *reinterpret_cast<const float4*>(tn + rb * 32 + 8 * (r >> 2) + 4 * h);
-                    const float n0 = (g & 1) ? nv.z : nv.x, n1 = (g & 1) ? nv.w : nv.y;
-                    prev[rb][r] = key_of(prev[rb][r], n0);
-                    prev[rb][r + 1] = key_of(prev[rb][r + 1], n1);
+                    const float nn[4] = {nv.x, nv.y, nv.z, nv.w};
+#pragma unroll
+                    for (int e = 0; e < KPG; ++e)
+                        prev[rb][r + e] = key_of(prev[rb][r + e], nn[(r & 3) + e]);
                 }
-                const float k0 = prev[rb][r], k1 = prev[rb][r + 1];
-                if constexpr (DYN) vmin = fminf(vmin, fminf(k0, k1));
-                if (__ballot(k0 <= ctest || k1 <= ctest)) {
-                    test_row(k0, pt0 + rb * 32 + mfma_row(r, h));
-                    test_row(k1, pt0 + rb * 32 + mfma_row(r + 1, h));
+                float kv[KPG];
+                bool any = false;
+#pragma unroll
+                for (int e = 0; e < KPG; ++e) {
+                    kv[e] = prev[rb][r + e];
+                    any = any || kv[e] <= ctest;
+                    if constexpr (DYN) vmin = fminf(vmin, kv[e]);
+                }
+                if (__ballot(any)) {
+#pragma unroll
+                    for (int e = 0; e < KPG; ++e) test_row(kv[e], pt0 + rb * 32 + mfma_row(r + e, h));
                 }
             }
         }
@@ -378,8 +413,8 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
                                         __HIP_MEMORY_SCOPE_WORKGROUP),
                       s + 1);
         if (s + 1 < nstages) {
-            an0 = *reinterpret_cast<const float4*>(tile[rb_nxt] + j * kLdsStride + h * 4);
-            an1 = *reinterpret_cast<const float4*>(tile[rb_nxt] + (32 + j) * kLdsStride + h * 4);
+            an0 = *reinterpret_cast<const Frag*>(tile_at(rb_nxt, j));
+            an1 = *reinterpret_cast<const Frag*>(tile_at(rb_nxt, 32 + j));
         }
         commit(s + 2, rb_wr);
         publish(s + 2);
@@ -458,8 +493,17 @@ hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s) {
     const dim3 grid((unsigned)(qtiles * a.splits)), block(512);
     const bool dyn = a.gbest != nullptr;
     if (dyn && a.dense) return hipErrorInvalidValue;
-#define PX_COLLECT(L2, FILT, DYN) \
-    hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true>), grid, block, 0, s, a)
+    if ((a.corpus_h == nullptr) != (a.queries_h == nullptr)) return hipErrorInvalidValue;
+    const bool h16 = a.corpus_h != nullptr;
+#define PX_COLLECT(L2, FILT, DYN)                                                              \
+    do {                                                                                       \
+        if (h16)                                                                               \
+            hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true, true>), grid,   \
+                               block, 0, s, a);                                                \
+        else                                                                                   \
+            hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true, false>), grid,  \
+                               block, 0, s, a);                                                \
+    } while (0)
     if (a.metric == 0) {
         if (a.rowidx) {
             if (dyn) PX_COLLECT(true, true, true);

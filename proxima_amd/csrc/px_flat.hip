@@ -1737,6 +1737,39 @@ hipError_t launch_nonfinite_check(const float* x, int64_t count, int* flag, hipS
     return hipGetLastError();
 }
 
+// out[i] = x[i] as fp16 bits; *inexact = 1 when any x[i] is not exactly an fp16 zero or
+// normal number (a rounded value, past 65504, or below fp16's smallest normal 2^-14: fp16
+// subnormals are excluded so that no MFMA input depends on subnormal handling). count is a
+// multiple of 4; x and out are 16- and 8-byte aligned.
+__global__ __launch_bounds__(256) void to_f16_kernel(const float4* x, int64_t count4,
+                                                     ushort4* out, int* inexact) {
+    bool bad = false;
+    auto one = [&](float v) -> unsigned short {
+        const _Float16 hv = (_Float16)v;
+        bad |= !((float)hv == v && (v == 0.f || fabsf(v) >= 0x1p-14f));
+        return __builtin_bit_cast(unsigned short, hv);
+    };
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count4;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float4 v = x[i];
+        out[i] = make_ushort4(one(v.x), one(v.y), one(v.z), one(v.w));
+    }
+    if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(inexact, 1);
+}
+
+hipError_t launch_to_f16(const float* x, int64_t count, unsigned short* out, int* inexact,
+                         hipStream_t s) {
+    if (count % 4 != 0 || ((uintptr_t)x & 15) != 0 || ((uintptr_t)out & 7) != 0)
+        return hipErrorInvalidValue;
+    if (count <= 0) return hipSuccess;
+    const int64_t count4 = count / 4;
+    const int64_t blocks = std::min<int64_t>((count4 + 255) / 256, 4096);
+    hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                       reinterpret_cast<const float4*>(x), count4,
+                       reinterpret_cast<ushort4*>(out), inexact);
+    return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void list_prologue_kernel(const float* x, int64_t count,
                                                             int* flag, int seq, int* gtau,
                                                             int64_t ngtau, int* gbest,

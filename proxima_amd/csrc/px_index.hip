@@ -178,6 +178,7 @@ struct Workspace {
     // collect path (k' past the lists)
     DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
     DevBuf cand_d;           // smallest dropped key of each overflowing region
+    DevBuf qh;               // a collect batch's queries as fp16 (px_flat::d_xh)
     DevBuf fflag;            // finiteness verdicts of list-path searches (next_finite_seq)
     int fseq = 0;
     DevBuf dbgw;             // debug build: the debug word of the kernels' index checks ...
@@ -234,7 +235,8 @@ struct Workspace {
     void release() {
         for (DevBuf* b : {&q, &qn, &mask, &rowidx, &scratch, &count, &part_k, &part_i, &out_ids,
                           &out_d, &gtau, &gbest, &thr_k, &thr_p, &lad_k, &lad_p, &rung, &status,
-                          &cand_k, &cand_p, &cand_n, &cand_d, &samp_row, &qlist, &sort_scratch,
+                          &cand_k, &cand_p, &cand_n, &cand_d, &qh, &samp_row, &qlist,
+                          &sort_scratch,
                           &fflag,
                           &dbgw})
             b->release();
@@ -503,6 +505,14 @@ struct px_flat {
     float* d_x = nullptr;          // [cap][dp]
     float* d_norm = nullptr;       // [cap]
     int64_t d_rows = 0, d_cap = 0;
+    // 128-dim rows: their fp16 mirror [cap][128], kept while every value mirrored so far is
+    // exactly an fp16 zero or normal number (integer descriptors such as SIFT's are); the
+    // collect scan then multiplies in fp16 for a batch whose queries are exact too. Dropped
+    // for good at the first row that is not (or if its memory cannot be had).
+    unsigned short* d_xh = nullptr;
+    bool xh_exact = true;
+    bool scan_f16 = true;          // px_flat_set_scan_f16
+    bool last_f16 = false;         // the last search's collect scan multiplied in fp16
     Workspace ws;
     Timing timing;
     int last_path = PX_PATH_LISTS; // selection path of the last search
@@ -561,11 +571,25 @@ int flat_sync(px_flat* f) {
             PX_HIP(hipMemcpyAsync(nn, f->d_norm, sizeof(float) * f->d_rows,
                                   hipMemcpyDeviceToDevice, f->stream));
         }
+        // the fp16 mirror grows with them, or is dropped if its memory cannot be had
+        unsigned short* nxh = nullptr;
+        if (f->dp == 128 && f->xh_exact) {
+            if (dev_malloc(&nxh, sizeof(unsigned short) * cap * 128) != hipSuccess) {
+                (void)hipGetLastError();
+                nxh = nullptr;
+                f->xh_exact = false;
+            } else if (f->d_rows) {
+                PX_HIP(hipMemcpyAsync(nxh, f->d_xh, sizeof(unsigned short) * f->d_rows * 128,
+                                      hipMemcpyDeviceToDevice, f->stream));
+            }
+        }
         PX_HIP(hipStreamSynchronize(f->stream));
         dev_free(f->d_x);
         dev_free(f->d_norm);
+        dev_free(f->d_xh);
         f->d_x = nx;
         f->d_norm = nn;
+        f->d_xh = nxh;
         f->d_cap = cap;
     }
     float* dst = f->d_x + f->d_rows * f->dp;
@@ -587,7 +611,23 @@ int flat_sync(px_flat* f) {
         }
     }
     PX_HIP(px::launch_row_norms(dst, add, (int)f->dp, f->d_norm + f->d_rows, f->stream));
+    int* xflag = nullptr;  // set if a new row is not exact in fp16
+    if (f->d_xh) {
+        PX_TRY(f->ws.count.reserve(sizeof(int)));
+        PX_TRY(f->ws.ensure_pinned());
+        xflag = f->ws.count.as<int>();
+        PX_HIP(px::launch_fill_int(xflag, 1, 0, f->stream));
+        PX_HIP(px::launch_to_f16(dst, add * 128, f->d_xh + f->d_rows * 128, xflag, f->stream));
+    }
     PX_HIP(hipStreamSynchronize(f->stream));
+    if (xflag) {
+        PX_TRY(read_back_int(xflag, f->ws.h_count, f->ws.h_count_dev, f->stream));
+        if (*f->ws.h_count) {
+            dev_free(f->d_xh);
+            f->d_xh = nullptr;
+            f->xh_exact = false;
+        }
+    }
     f->d_rows = need;
     std::vector<float>().swap(f->pending);
     return PX_OK;
@@ -911,6 +951,21 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     Workspace& ws = f->ws;
     hipStream_t s = f->stream;
     const int cus = std::max(f->dev.cus, 1);
+    // the fp16 scan: rows exact in fp16 (d_xh) and so are this batch's queries (one
+    // conversion pass, its verdict read back)
+    const unsigned short* qh = nullptr;
+    if (f->scan_f16 && f->d_xh && f->dp == 128 && !vec_collect(nq, f->dp) &&
+        ((uintptr_t)d_q & 15) == 0) {
+        PX_TRY(ws.qh.reserve(sizeof(unsigned short) * nq * 128));
+        PX_TRY(ws.count.reserve(sizeof(int)));
+        PX_TRY(ws.ensure_pinned());
+        PX_HIP(px::launch_fill_int(ws.count.as<int>(), 1, 0, s));
+        PX_HIP(px::launch_to_f16(d_q, nq * 128, ws.qh.as<unsigned short>(), ws.count.as<int>(),
+                                 s));
+        PX_TRY(read_back_int(ws.count.as<int>(), ws.h_count, ws.h_count_dev, s));
+        if (*ws.h_count == 0) qh = ws.qh.as<unsigned short>();
+    }
+    f->last_f16 = qh != nullptr;
     CollectJob j;
     j.ws = &ws;
     j.stream = s;
@@ -988,6 +1043,8 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.dense = 1;
         a.dense_ld = ld;
         a.spin_fail = ws.status.as<int>() + nq;
+        a.corpus_h = qh ? f->d_xh : nullptr;
+        a.queries_h = qh;
         a.xcd_major = xcd_major_for(a, 256, std::max(f->dev.cus, 1));
         PX_HIP(px::launch_flat_collect(a, s));
         px::LadderArgs la{};
@@ -1093,6 +1150,8 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.cand_dmin = keeps_dmin ? ws.cand_d.as<int>() : nullptr;
         j.sel_dmin = a.cand_dmin;
         a.spin_fail = ws.status.as<int>() + j.nq;
+        a.corpus_h = qh ? f->d_xh : nullptr;
+        a.queries_h = qh;
         // the shared bound needs k' publishing slots (one per split, at most 32); it is
         // applied where the first round has no sampled thresholds (with them it measured
         // no faster on 1M x 128 and 1M x 384, and 11% slower on 100k x 384 at k = 16)
@@ -1177,13 +1236,16 @@ int run_full_sort(Workspace& ws, hipStream_t s, Timing& timing, int64_t nq, int6
 int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
                      const int* rowidx, int64_t* d_ids, float* d_out, int raw_keys) {
     int rounds = 0;
+    bool all_f16 = true;
     for (int64_t b0 = 0; b0 < nq; b0 += kCollectBatch) {
         const int64_t b = std::min(kCollectBatch, nq - b0);
         PX_TRY(flat_run_collect_batch(f, d_q + b0 * f->dp, b, k, n_eff, rowidx, d_ids + b0 * k,
                                       d_out + b0 * k, raw_keys));
         rounds = std::max(rounds, f->last_rounds);
+        all_f16 = all_f16 && f->last_f16;
     }
     f->last_rounds = rounds;
+    f->last_f16 = all_f16 && nq > 0;
     return PX_OK;
 }
 
@@ -1310,6 +1372,7 @@ int flat_run_paths(px_flat* f, const float* d_q, int64_t nq, int64_t k, const ui
     }
     f->last_rounds = 0;
     f->last_path = PX_PATH_LISTS;
+    f->last_f16 = false;
     if (k > PX_MAX_K) {
         PX_TRY(check_now());
         f->last_path = PX_PATH_FULL_SORT;
@@ -1837,6 +1900,7 @@ void px_flat_destroy(px_flat* f) {
         if (f->stream) (void)hipStreamSynchronize(f->stream);
         dev_free(f->d_x);
         dev_free(f->d_norm);
+        dev_free(f->d_xh);
         f->ws.release();
         f->timing.destroy();
         if (f->stream) (void)hipStreamDestroy(f->stream);
@@ -2036,6 +2100,19 @@ int px_flat_last_timing(const px_flat* f, float* scan_ms, float* total_ms, int* 
 int px_flat_last_rounds(const px_flat* f, int* rounds) {
     if (!f) return fail(PX_ERR_ARG, "null index handle");
     if (rounds) *rounds = f->last_rounds;
+    return PX_OK;
+}
+
+int px_flat_set_scan_f16(px_flat* f, int enable) {
+    if (!f) return fail(PX_ERR_ARG, "null index handle");
+    std::lock_guard<std::mutex> lock(f->mu);
+    f->scan_f16 = enable != 0;
+    return PX_OK;
+}
+
+int px_flat_last_scan_f16(const px_flat* f, int* used) {
+    if (!f || !used) return fail(PX_ERR_ARG, "null index handle or output pointer");
+    *used = f->last_f16 ? 1 : 0;
     return PX_OK;
 }
 

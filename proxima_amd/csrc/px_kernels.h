@@ -69,6 +69,12 @@ struct FlatScanArgs {
     // optional (launch_flat_collect, 128-dim rows): set nonzero if a stage-sync wait of the
     // scan gave up (a bug: the results of that launch are not to be used)
     int* spin_fail;
+    // optional (launch_flat_collect, 128-dim rows), both or neither: the corpus [n][128] and
+    // the queries [nq][128] as fp16 bit patterns, given only when every value of both is
+    // exactly representable in fp16; the scan then multiplies in fp16 (exact products,
+    // fp32 accumulation): its keys equal the fp32 scan's up to the rounding of the sums
+    const unsigned short* corpus_h;
+    const unsigned short* queries_h;
 };
 
 // Waves per workgroup and list capacity used for a list length kl.
@@ -211,6 +217,11 @@ hipError_t launch_pad_rows(const float* src, int64_t rows, int dim, int dp, floa
 
 // *flag = 1 when any of x[0 .. count) is NaN or infinite, else 0 (the flag is cleared first).
 hipError_t launch_nonfinite_check(const float* x, int64_t count, int* flag, hipStream_t s);
+// out[0 .. count) = x as fp16 bit patterns; atomically ORs 1 into *inexact when any value is
+// not exactly an fp16 zero or normal number (the caller clears it). count % 4 == 0, x 16-byte
+// and out 8-byte aligned.
+hipError_t launch_to_f16(const float* x, int64_t count, unsigned short* out, int* inexact,
+                         hipStream_t s);
 // The per-split list path's first kernel: *flag = max(*flag, seq) when any of count floats
 // of x is NaN or infinite (flag is never cleared: each search takes a larger seq), and
 // gtau[0..ngtau) and gbest[0..ngbest) filled with kTotalKeyInf. One launch where a flag

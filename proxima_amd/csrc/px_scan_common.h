@@ -89,6 +89,23 @@ __device__ __forceinline__ f32x16 mfma4z(float4 a, float4 b) {
     return c;
 }
 
+// fp16 operands, fp32 accumulation: v_mfma_f32_32x32x16_f16 (gfx950), 16 dims a tile. Lane l
+// holds row l % 32 (A) or column l % 32 (B) at dims 8 (l / 32) .. 8 (l / 32) + 7; the
+// result layout is the fp32 tiles' (mfma_row). Products of fp16 values are exact in fp32.
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ f32x16 mfma16(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma16z(f16x8 a, f16x8 b) {
+    const f32x16 z = {0.f};
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, z, 0, 0, 0);
+}
+// One dim group of a 128-dim chunk: 8 dims (fp32, four tiles) or 16 (fp16, one tile).
+__device__ __forceinline__ f32x16 mfma_group(float4 a, float4 b, f32x16 c) { return mfma4(a, b, c); }
+__device__ __forceinline__ f32x16 mfma_group(f16x8 a, f16x8 b, f32x16 c) { return mfma16(a, b, c); }
+__device__ __forceinline__ f32x16 mfma_group_z(float4 a, float4 b) { return mfma4z(a, b); }
+__device__ __forceinline__ f32x16 mfma_group_z(f16x8 a, f16x8 b) { return mfma16z(a, b); }
+
 // rank-th smallest (1-based, rank <= 32) of the 32 ints held as v[0..15] by this lane and
 // by lane ^ 32; both lanes return it. Bitonic: sort 16 in registers, split the union into
 // its 16 smallest and 16 largest with the partner's list reversed, sort those halves.

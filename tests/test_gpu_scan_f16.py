@@ -1,0 +1,169 @@
+"""GPU parity of the fp16 collect scan (flat_collect_kernel with fp16 operands).
+
+When every value of the rows and of a batch's queries is exactly an fp16 zero or normal
+number -- integer-valued descriptors such as the SIFT-like workload's are -- every product
+q_i * x_i is exact in fp16 as in fp32, so the collect scan multiplies on the fp16 matrix
+cores with fp32 accumulation; the candidates it collects are re-ranked in the reference's
+arithmetic (distance.rs:3-39) exactly as on the fp32 scan. Results must equal the oracle's
+(flat.rs:106-148) bit for bit on integer data, equal the fp32 scan's, and the scan must fall
+back to fp32 whenever a row or a query is not exact in fp16 (rounded, past 65504, or an fp16
+subnormal).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_parity
+from proxima_amd import FlatIndex, Metric, datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def _key_of(data, queries, metric):
+    def key_of(qi, row):
+        if metric == oracle.L2:
+            return float(oracle.l2_sqr(queries[qi], data[row]))
+        return float(-oracle.inner_product(queries[qi], data[row]))
+    return key_of
+
+
+def _index(data, metric):
+    idx = FlatIndex(data.shape[1], Metric.L2 if metric == oracle.L2 else Metric.InnerProduct)
+    idx.add(data)
+    return idx
+
+
+def _run(idx, q, k, mask=None):
+    if mask is None:
+        ids, d = idx.search_batch(q, k=k)
+    else:
+        ids, d = idx.search_batch_filtered(q, mask, k=k)
+    info = idx._last_timing()
+    return ids, d, info
+
+
+def _same(a_ids, a_d, b_ids, b_d):
+    return np.array_equal(a_ids, b_ids) and np.array_equal(a_d.view(np.uint32), b_d.view(np.uint32))
+
+
+@pytest.mark.parametrize("metric", [oracle.L2, oracle.IP])
+@pytest.mark.parametrize("k", [100, 1000])
+def test_integer_rows_f16_equals_oracle_and_fp32(gpu, metric, k):
+    # the sampled collect path (threshold sample scan, ladder, collect scan)
+    data = datagen.sift_like(100_000, 128, 701)
+    q = datagen.sift_like(1000, 128, 702)
+    idx = _index(data, metric)
+    print(f"case sift-like 100000 x 128, 1000 queries, k={k}, metric={metric}", flush=True)
+    ids, d, info = _run(idx, q, k)
+    print(f"  path {info['path']}, f16 {info['scan_f16']}, rounds {info['collect_rounds']}",
+          flush=True)
+    assert info["path"].startswith("collect")
+    assert info["scan_f16"]
+    o_ids, o_d, _ = oracle.flat_search(data, q, k, metric)
+    assert np.array_equal(ids, o_ids)
+    assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+    idx._scan_f16(False)
+    ids32, d32, info32 = _run(idx, q, k)
+    assert not info32["scan_f16"] and info32["path"] == info["path"]
+    assert _same(ids, d, ids32, d32)
+
+
+def test_integer_rows_filtered(gpu):
+    data = datagen.sift_like(120_000, 128, 711)
+    q = datagen.sift_like(600, 128, 712)
+    mask = datagen.mask(120_000, 0.3, 713)
+    idx = _index(data, oracle.L2)
+    for k in (10, 200):
+        print(f"case sift-like filtered 30%, k={k}", flush=True)
+        ids, d, info = _run(idx, q, k, mask)
+        print(f"  path {info['path']}, f16 {info['scan_f16']}", flush=True)
+        o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2, mask=mask)
+        assert np.array_equal(ids, o_ids)
+        assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+        assert info["scan_f16"] == info["path"].startswith("collect")
+
+
+@pytest.mark.parametrize("metric", [oracle.L2, oracle.IP])
+def test_bounded_path(gpu, metric):
+    # the 1M x 128 workload's route (collect-bounded: no sample, the splits' shared bound):
+    # 2,048 queries over 60,000 rows (32 splits)
+    data = datagen.sift_like(60_000, 128, 721)
+    q = datagen.sift_like(2048, 128, 722)
+    idx = _index(data, metric)
+    for k in (1, 10, 16):
+        print(f"case sift-like 60000 x 128, 2048 queries, k={k}, metric={metric}", flush=True)
+        ids, d, info = _run(idx, q, k)
+        print(f"  path {info['path']}, f16 {info['scan_f16']}", flush=True)
+        assert info["path"] == "collect-bounded" and info["scan_f16"]
+        o_ids, o_d, _ = oracle.flat_search(data, q, k, metric)
+        assert np.array_equal(ids, o_ids)
+        assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+
+
+def test_fp16_exact_fractions_and_signs(gpu):
+    # multiples of 1/16 with signs: exact in fp16 (normal numbers or zero), not integers
+    rng = np.random.default_rng(731)
+    data = (rng.integers(-400, 400, size=(60_000, 128)) / 16.0).astype(np.float32)
+    q = (rng.integers(-400, 400, size=(700, 128)) / 16.0).astype(np.float32)
+    for metric in (oracle.L2, oracle.IP):
+        idx = _index(data, metric)
+        print(f"case fractions metric={metric}", flush=True)
+        ids, d, info = _run(idx, q, 100)
+        assert info["scan_f16"]
+        o_ids, o_d, _ = oracle.flat_search(data, q, 100, metric)
+        assert_parity(ids, d, o_ids, o_d, _key_of(data, q, metric))
+        idx._scan_f16(False)
+        ids32, d32, _ = _run(idx, q, 100)
+        assert_parity(ids32, d32, o_ids, o_d, _key_of(data, q, metric))
+
+
+def test_fallback_when_not_exact(gpu):
+    rows = datagen.sift_like(40_000, 128, 741)
+    q = datagen.sift_like(400, 128, 742)
+    k = 100
+    cases = {
+        "rounded query value": (rows, np.where(np.arange(128) == 5, q + 0.3, q).astype(np.float32)),
+        "query past 65504": (rows, np.where(np.arange(128) == 7, 70000.0, q).astype(np.float32)),
+        "query fp16 subnormal": (rows, np.where(np.arange(128) == 9, 2.0 ** -20, q).astype(np.float32)),
+        "gaussian rows": (datagen.gaussian(40_000, 128, 743), q),
+    }
+    for name, (data, qq) in cases.items():
+        print(f"case fallback: {name}", flush=True)
+        idx = _index(data, oracle.L2)
+        ids, d, info = _run(idx, qq, k)
+        assert info["path"].startswith("collect")
+        assert not info["scan_f16"], name
+        o_ids, o_d, _ = oracle.flat_search(data, qq, k, oracle.L2)
+        assert_parity(ids, d, o_ids, o_d, _key_of(data, qq, oracle.L2))
+
+
+def test_inexact_rows_added_later_drop_the_fp16_copy(gpu):
+    a = datagen.sift_like(30_000, 128, 751)
+    b = datagen.gaussian(5_000, 128, 752)
+    q = datagen.sift_like(300, 128, 753)
+    idx = _index(a, oracle.L2)
+    _, _, info = _run(idx, q, 100)
+    assert info["scan_f16"]
+    idx.add(b)
+    print("case rows added that are not exact in fp16", flush=True)
+    ids, d, info = _run(idx, q, 100)
+    assert not info["scan_f16"]
+    both = np.concatenate([a, b])
+    o_ids, o_d, _ = oracle.flat_search(both, q, 100, oracle.L2)
+    assert_parity(ids, d, o_ids, o_d, _key_of(both, q, oracle.L2))
+
+
+def test_exact_rows_added_later_keep_the_fp16_copy(gpu):
+    # the fp16 copy grows with the rows (a second add past the first allocation)
+    a = datagen.sift_like(20_000, 128, 761)
+    b = datagen.sift_like(50_000, 128, 762)
+    q = datagen.sift_like(300, 128, 763)
+    idx = _index(a, oracle.L2)
+    idx.add(b)
+    print("case exact rows added twice", flush=True)
+    ids, d, info = _run(idx, q, 150)
+    assert info["scan_f16"]
+    both = np.concatenate([a, b])
+    o_ids, o_d, _ = oracle.flat_search(both, q, 150, oracle.L2)
+    assert np.array_equal(ids, o_ids)
+    assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
