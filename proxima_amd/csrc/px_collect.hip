@@ -337,11 +337,28 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         const char* ta0 = tile_at(rb_cur, j);
         const char* ta1 = tile_at(rb_cur, 32 + j);
         float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
+        // H16 (two MFMAs a group, too few to cover an LDS read): each group's A operands and
+        // norms are read a group ahead, before the group's MFMAs and tests
+        Frag xa0 = an0, xa1 = an1;
+        float4 nvn = make_float4(0.f, 0.f, 0.f, 0.f);
+        if constexpr (H16 && TEST && L2) {
+            if (!keys_ready) nvn = *reinterpret_cast<const float4*>(tn + 4 * h);
+        }
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             if (g < ng) {
-                const Frag x0 = g == 0 ? an0 : *reinterpret_cast<const Frag*>(ta0 + g * 32);
-                const Frag x1 = g == 0 ? an1 : *reinterpret_cast<const Frag*>(ta1 + g * 32);
+                Frag x0, x1;
+                if constexpr (H16) {
+                    x0 = xa0;
+                    x1 = xa1;
+                    if (g + 1 < NG) {
+                        xa0 = *reinterpret_cast<const Frag*>(ta0 + (g + 1) * 32);
+                        xa1 = *reinterpret_cast<const Frag*>(ta1 + (g + 1) * 32);
+                    }
+                } else {
+                    x0 = g == 0 ? an0 : *reinterpret_cast<const Frag*>(ta0 + g * 32);
+                    x1 = g == 0 ? an1 : *reinterpret_cast<const Frag*>(ta1 + g * 32);
+                }
                 if (g == 0 && first) {
                     cur[0] = mfma_group_z(x0, b[0]);
                     cur[1] = mfma_group_z(x1, b[0]);
@@ -358,22 +375,31 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
                 // rows r .. r + KPG - 1
                 const int rb = (KPG * g) >> 4, r = (KPG * g) & 15;
                 if (!keys_ready) {
-                    if (L2 && (r & 3) == 0)
+                    if constexpr (H16) {
+                        // rows 4g .. 4g + 3: norms at 8 g + 4 h (rb = g / 4, r = 4 (g % 4))
+                        if (L2) {
+                            nv = nvn;
+                            if (g + 1 < NG)
+                                nvn = *reinterpret_cast<const float4*>(tn + 8 * (g + 1) + 4 * h);
+                        }
+                    } else if (L2 && (r & 3) == 0) {
                         nv = *reinterpret_cast<const float4*>(tn + rb * 32 + 8 * (r >> 2) + 4 * h);
+                    }
                     const float nn[4] = {nv.x, nv.y, nv.z, nv.w};
 #pragma unroll
                     for (int e = 0; e < KPG; ++e)
                         prev[rb][r + e] = key_of(prev[rb][r + e], nn[(r & 3) + e]);
                 }
+                // the group's smallest key decides whether any of its rows is tested (one
+                // compare), and feeds the tile's minimum
                 float kv[KPG];
-                bool any = false;
 #pragma unroll
-                for (int e = 0; e < KPG; ++e) {
-                    kv[e] = prev[rb][r + e];
-                    any = any || kv[e] <= ctest;
-                    if constexpr (DYN) vmin = fminf(vmin, kv[e]);
-                }
-                if (__ballot(any)) {
+                for (int e = 0; e < KPG; ++e) kv[e] = prev[rb][r + e];
+                float kmin = kv[0];
+#pragma unroll
+                for (int e = 1; e < KPG; ++e) kmin = fminf(kmin, kv[e]);
+                if constexpr (DYN) vmin = fminf(vmin, kmin);
+                if (__ballot(kmin <= ctest)) {
 #pragma unroll
                     for (int e = 0; e < KPG; ++e) test_row(kv[e], pt0 + rb * 32 + mfma_row(r + e, h));
                 }
