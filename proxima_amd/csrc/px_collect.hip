@@ -62,15 +62,21 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     constexpr int kPitch = kRowBytes + 16;
     constexpr int kF4PerRow = kRowBytes / 16;    // 16-byte pieces per staged row (32; H16 16)
     constexpr int kRowStep = NT / kF4PerRow;     // rows between a thread's loads (16; H16 32)
-    constexpr int kPF = kTileRows / kRowStep;    // pieces per thread per stage (4; H16 2)
+    // H16: a stage is two tiles (128 rows), so that the stage sync is paid once per 32 MFMAs
+    // of a wave, as on fp32 it is once per 128
+    constexpr int TPS = H16 ? 2 : 1;             // tiles per stage
+    constexpr int kStageRows = TPS * kTileRows;
+    constexpr int kPF = kStageRows / kRowStep;   // pieces per thread per stage (4)
     constexpr int NG = H16 ? 8 : 16;             // MFMA dim groups per 128-dim chunk
     constexpr int KPG = 32 / NG;                 // keys of the previous tile tested per group
-    static_assert(NT % kF4PerRow == 0 && kTileRows % kRowStep == 0, "uneven stage split");
+    constexpr int kNB = H16 ? 8 : kNormBufs;     // norm slots (one a tile)
+    constexpr int kBufFloats = H16 ? kStageRows * kPitch / 4 : kTileRows * kLdsStride;
+    static_assert(NT % kF4PerRow == 0 && kStageRows % kRowStep == 0, "uneven stage split");
     static_assert(!(H16 && MULTI), "fp16 rows are one 128-dim chunk");
-    static_assert(kTileRows * kPitch <= kTileRows * kLdsStride * 4, "stage buffer too small");
+    static_assert(H16 || kPitch == kLdsStride * 4, "fp32 rows keep the list scan's pitch");
     static_assert(!(DYN && MULTI), "the shared bound serves one-chunk scans");
-    __shared__ __attribute__((aligned(16))) float tile[kStageBufs][kTileRows * kLdsStride];
-    __shared__ __attribute__((aligned(16))) float tnorm[kNormBufs][kTileRows];
+    __shared__ __attribute__((aligned(16))) float tile[kStageBufs][kBufFloats];
+    __shared__ __attribute__((aligned(16))) float tnorm[kNB][kTileRows];
     // per wave: the last stage it has committed to a stage buffer (the stage sync below)
     __shared__ int committed[8];
 
@@ -91,7 +97,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     const float kInf = __int_as_float(0x7f800000);
     const int nch = MULTI ? (a.dp + kChunk - 1) / kChunk : 1;
     const int ntiles = (row1 - row0 + kTileRows - 1) / kTileRows;  // >= 1
-    const int nstages = ntiles * nch;
+    const int nstages = MULTI ? ntiles * nch : (ntiles + TPS - 1) / TPS;
     const int cc = tid % kF4PerRow;   // this thread's float4 column of a staged row
     const int rr0 = tid / kF4PerRow;  // its first row of a stage
 
@@ -102,8 +108,8 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     // past the chunk's end are skipped).
     int rid[kPF], pid;
     // (positions past the split's end are formed in 64 bits: near 2^31 rows they overflow)
-    auto tile_ids = [&](int t) __attribute__((always_inline)) {
-        const int64_t t0 = (int64_t)row0 + (int64_t)t * kTileRows;
+    auto tile_ids = [&](int t) __attribute__((always_inline)) {  // t: a stage's first tile / TPS
+        const int64_t t0 = (int64_t)row0 + (int64_t)t * kStageRows;
 #pragma unroll
         for (int u = 0; u < kPF; ++u) {
             const int64_t pos = t0 + rr0 + u * kRowStep;
@@ -113,9 +119,9 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         }
         const int64_t pos = t0 + tid;
         const int v = FILT ? a.rowidx[min(pos, (int64_t)row1 - 1)] : (int)pos;
-        pid = (tid < kTileRows && pos < row1) ? v : -1;
+        pid = (tid < kStageRows && pos < row1) ? v : -1;
     };
-    static_assert(kPF == (H16 ? 2 : 4), "four staged pieces per thread (fp16: two)");
+    static_assert(kPF == 4, "four staged pieces per thread");
     float4 pf0, pf1, pf2, pf3;  // separate variables: an array of them ended up in memory
     float pn = 0.f;
     auto fetch = [&](int s) __attribute__((always_inline)) {
@@ -124,6 +130,8 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
             const unsigned short* base = a.corpus_h + cc * 8;
             pf0 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[0], 0) * kChunk);
             pf1 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[1], 0) * kChunk);
+            pf2 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[2], 0) * kChunk);
+            pf3 = *reinterpret_cast<const float4*>(base + (int64_t)max(rid[3], 0) * kChunk);
         } else {
             const int f4r = min(kChunk, a.dp - c * kChunk) >> 2;
             const float* base = a.corpus + c * kChunk + min(cc, f4r - 1) * 4;
@@ -138,12 +146,15 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         char* tb = reinterpret_cast<char*>(tile[buf]) + rr0 * kPitch + cc * 16;
         *reinterpret_cast<float4*>(tb) = pf0;
         *reinterpret_cast<float4*>(tb + kRowStep * kPitch) = pf1;
-        if constexpr (!H16) {
-            *reinterpret_cast<float4*>(tb + 2 * kRowStep * kPitch) = pf2;
-            *reinterpret_cast<float4*>(tb + 3 * kRowStep * kPitch) = pf3;
+        *reinterpret_cast<float4*>(tb + 2 * kRowStep * kPitch) = pf2;
+        *reinterpret_cast<float4*>(tb + 3 * kRowStep * kPitch) = pf3;
+        if constexpr (H16) {
+            // the stage's two tiles' norms, one slot a tile
+            if (L2 && tid < kStageRows) tnorm[(TPS * s + (tid >> 6)) & (kNB - 1)][tid & 63] = pn;
+        } else {
+            const int c = MULTI ? (int)(s % nch) : 0;
+            if (L2 && c == 0 && tid < kTileRows) tnorm[(s / nch) & (kNormBufs - 1)][tid] = pn;
         }
-        const int c = MULTI ? (int)(s % nch) : 0;
-        if (L2 && c == 0 && tid < kTileRows) tnorm[(s / nch) & (kNormBufs - 1)][tid] = pn;
     };
 
     // prologue: stages 0 and 1 in LDS, ids of the tile of stage 2
@@ -310,19 +321,24 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     int s = 0;       // stage index
 
     // One stage: the MFMAs of chunk c of tile t into cur. TEST (the first stage of tiles
-    // t > 0): the keys of tile t - 1, in prev, computed and tested between them.
-    auto stage = [&](auto test_tag, auto first_tag, int t, int c, f32x16 (&cur)[2],
-                     f32x16 (&prev)[2]) __attribute__((always_inline)) {
+    // t > 0): the keys of tile t - 1, in prev, computed and tested between them. H16 (two
+    // tiles a stage): par_tag = t % 2; an even tile begins the stage (its loads), an odd
+    // one (or the last tile) ends it (the sync and commit).
+    auto stage = [&](auto test_tag, auto first_tag, auto par_tag, int t, int c,
+                     f32x16 (&cur)[2], f32x16 (&prev)[2]) __attribute__((always_inline)) {
         constexpr bool TEST = decltype(test_tag)::value;
+        constexpr bool BEGIN = !H16 || decltype(par_tag)::value == 0;
         const bool first = !MULTI || c == 0;
         const int rb_nxt = rb_cur == kStageBufs - 1 ? 0 : rb_cur + 1;
         const int rb_wr = rb_nxt == kStageBufs - 1 ? 0 : rb_nxt + 1;
-        fetch(s + 2);
-        tile_ids((s + 3) / nch);
+        if constexpr (BEGIN) {
+            fetch(s + 2);
+            tile_ids((s + 3) / nch);
+        }
         // DYN, the split's first tile (FIRST: t == 1): all its keys and its own bound before
         // its tests
         constexpr bool keys_ready = DYN && TEST && decltype(first_tag)::value;
-        const float* tn = tnorm[(t - 1) & (kNormBufs - 1)];
+        const float* tn = tnorm[(t - 1) & (kNB - 1)];
         if constexpr (keys_ready) {
             all_keys(prev, tn);
             first_tile_bound(prev, kTileRows);
@@ -334,15 +350,23 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         const int ng = FULL ? NG : min(kChunk, a.dp - c * kChunk) >> 3;
         const int cn = MULTI ? (c + 1 == nch ? 0 : c + 1) : 0;
         const int dcn = min(kChunk, a.dp - cn * kChunk);
-        const char* ta0 = tile_at(rb_cur, j);
-        const char* ta1 = tile_at(rb_cur, 32 + j);
+        constexpr int kRow0 = BEGIN ? 0 : kTileRows;  // the tile's first row in the stage
+        const char* ta0 = tile_at(rb_cur, kRow0 + j);
+        const char* ta1 = tile_at(rb_cur, kRow0 + 32 + j);
         float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
         // H16 (two MFMAs a group, too few to cover an LDS read): each group's A operands and
-        // norms are read a group ahead, before the group's MFMAs and tests
-        Frag xa0 = an0, xa1 = an1;
-        float4 nvn = make_float4(0.f, 0.f, 0.f, 0.f);
-        if constexpr (H16 && TEST && L2) {
-            if (!keys_ready) nvn = *reinterpret_cast<const float4*>(tn + 4 * h);
+        // norms are read two groups ahead (xa, nvn: group g + 1; xb, nvb: g + 2)
+        Frag xa0 = an0, xa1 = an1, xb0 = an0, xb1 = an1;
+        float4 nvn = make_float4(0.f, 0.f, 0.f, 0.f), nvb = nvn;
+        if constexpr (H16) {
+            xb0 = *reinterpret_cast<const Frag*>(ta0 + 32);
+            xb1 = *reinterpret_cast<const Frag*>(ta1 + 32);
+            if constexpr (TEST && L2) {
+                if (!keys_ready) {
+                    nvn = *reinterpret_cast<const float4*>(tn + 4 * h);
+                    nvb = *reinterpret_cast<const float4*>(tn + 8 + 4 * h);
+                }
+            }
         }
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
@@ -351,9 +375,11 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
                 if constexpr (H16) {
                     x0 = xa0;
                     x1 = xa1;
-                    if (g + 1 < NG) {
-                        xa0 = *reinterpret_cast<const Frag*>(ta0 + (g + 1) * 32);
-                        xa1 = *reinterpret_cast<const Frag*>(ta1 + (g + 1) * 32);
+                    xa0 = xb0;
+                    xa1 = xb1;
+                    if (g + 2 < NG) {
+                        xb0 = *reinterpret_cast<const Frag*>(ta0 + (g + 2) * 32);
+                        xb1 = *reinterpret_cast<const Frag*>(ta1 + (g + 2) * 32);
                     }
                 } else {
                     x0 = g == 0 ? an0 : *reinterpret_cast<const Frag*>(ta0 + g * 32);
@@ -379,8 +405,9 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
                         // rows 4g .. 4g + 3: norms at 8 g + 4 h (rb = g / 4, r = 4 (g % 4))
                         if (L2) {
                             nv = nvn;
-                            if (g + 1 < NG)
-                                nvn = *reinterpret_cast<const float4*>(tn + 8 * (g + 1) + 4 * h);
+                            nvn = nvb;
+                            if (g + 2 < NG)
+                                nvb = *reinterpret_cast<const float4*>(tn + 8 * (g + 2) + 4 * h);
                         }
                     } else if (L2 && (r & 3) == 0) {
                         nv = *reinterpret_cast<const float4*>(tn + rb * 32 + 8 * (r >> 2) + 4 * h);
@@ -432,6 +459,15 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
             }
             if (a.dense) dense_write(prev, row0 + (t - 1) * kTileRows, kTileRows);
         }
+        if (H16 && BEGIN && t + 1 < ntiles) {
+            // the stage's second tile: its first A operands from the same buffer, no sync
+            an0 = *reinterpret_cast<const Frag*>(tile_at(rb_cur, kTileRows + j));
+            an1 = *reinterpret_cast<const Frag*>(tile_at(rb_cur, kTileRows + 32 + j));
+            if constexpr (DYN) {
+                if (pub_now) atomicMin(gbest + (split & 31), cpub);
+            }
+            return;
+        }
         // the next stage's first A operands and this wave's part of stage s + 2, once every
         // wave has committed stage s + 1
         wait_committed(s + 1);
@@ -452,17 +488,20 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         ++s;
     };
     // a tile: its first stage tests the previous tile (TEST), its other chunks do not
-    auto run_tile = [&](auto test_tag, auto first_tag, int t, f32x16 (&cur)[2],
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    auto run_tile = [&](auto test_tag, auto first_tag, auto par_tag, int t, f32x16 (&cur)[2],
                         f32x16 (&prev)[2]) __attribute__((always_inline)) {
-        stage(test_tag, first_tag, t, 0, cur, prev);
-        for (int c = 1; c < nch; ++c) stage(std::false_type{}, std::false_type{}, t, c, cur, prev);
+        stage(test_tag, first_tag, par_tag, t, 0, cur, prev);
+        for (int c = 1; c < nch; ++c)
+            stage(std::false_type{}, std::false_type{}, par_tag, t, c, cur, prev);
     };
     // tile 0; tile 1 (its first stage tests tile 0, the split's first); then pairs
-    run_tile(std::false_type{}, std::false_type{}, 0, accA, accB);
-    if (ntiles > 1) run_tile(std::true_type{}, std::true_type{}, 1, accB, accA);
+    run_tile(std::false_type{}, std::false_type{}, P0{}, 0, accA, accB);
+    if (ntiles > 1) run_tile(std::true_type{}, std::true_type{}, P1{}, 1, accB, accA);
     for (int t = 2; t < ntiles; t += 2) {
-        run_tile(std::true_type{}, std::false_type{}, t, accA, accB);
-        if (t + 1 < ntiles) run_tile(std::true_type{}, std::false_type{}, t + 1, accB, accA);
+        run_tile(std::true_type{}, std::false_type{}, P0{}, t, accA, accB);
+        if (t + 1 < ntiles) run_tile(std::true_type{}, std::false_type{}, P1{}, t + 1, accB, accA);
     }
 
     // the last tile's keys: all at once, with no MFMAs to hide behind
@@ -470,7 +509,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         const int tl = ntiles - 1;
         const int t0 = row0 + tl * kTileRows;
         const int rem = min(row1 - t0, kTileRows);
-        all_keys(acc, tnorm[tl & (kNormBufs - 1)]);
+        all_keys(acc, tnorm[tl & (kNB - 1)]);
         if (a.dense) {
             dense_write(acc, t0, rem);
             return;

@@ -17,6 +17,11 @@ its part of stage s + 2; C = s + 2. After the last stage a wave with queries rea
 (nstages - 1) % 4. The prologue writes stages 0 and 1 and sets every C = 1 before its one
 barrier.
 
+The fp16 variant of flat_collect_kernel stages two tiles at a time: its stage s holds tiles
+2s and 2s + 1 and their norms (slots 2s, 2s + 1 of eight, a pair per stage: pair slot s % 4),
+and during stage s a wave also reads the norms of stage s itself (tile 2s's keys, tested
+during tile 2s + 1's MFMAs), so its reads are pair slots (s - 1) % 4 and s % 4.
+
 The model runs the eight waves of a workgroup under random interleavings, with every read
 an interval that other waves' steps may fall inside, and checks that no wave waits forever,
 that every read finds the stage it expects in every wave's part, and that no write lands on
@@ -34,7 +39,7 @@ class Violation(AssertionError):
     pass
 
 
-def _wave_program(s_count, live, c_off=0, write_first=False):
+def _wave_program(s_count, live, c_off=0, write_first=False, pairs=False):
     """The steps of one wave: ('read'|'end'|'write'|'set'|'wait', ...) in program order."""
     prog = []
     for s in range(s_count):
@@ -42,6 +47,8 @@ def _wave_program(s_count, live, c_off=0, write_first=False):
             prog.append(("read", "buf", s % STAGE_BUFS, s))          # MFMAs of stage s
             if s > 0:
                 prog.append(("read", "norm", (s - 1) % NORM_BUFS, s - 1))
+            if pairs:  # two tiles a stage: the first tile's norms, tested during the second
+                prog.append(("read", "norm", s % NORM_BUFS, s))
             prog.append(("end",))
         if write_first:
             prog.append(("write", s + 2))
@@ -111,14 +118,16 @@ def run_schedule(s_count, live_waves, seed, max_steps=10**6, **variant):
     raise Violation("no progress: a wave waits forever")
 
 
+@pytest.mark.parametrize("pairs", [False, True])
 @pytest.mark.parametrize("live_waves", [8, 2, 1])
 @pytest.mark.parametrize("stages", [1, 2, 3, 7, 24])
-def test_protocol_holds(stages, live_waves):
+def test_protocol_holds(stages, live_waves, pairs):
     for seed in range(60):
-        run_schedule(stages, live_waves, seed)
+        run_schedule(stages, live_waves, seed, pairs=pairs)
 
 
-@pytest.mark.parametrize("variant", [dict(c_off=-1), dict(write_first=True)])
+@pytest.mark.parametrize("variant", [dict(c_off=-1), dict(write_first=True),
+                                     dict(c_off=-1, pairs=True), dict(write_first=True, pairs=True)])
 def test_broken_variants_are_caught(variant):
     # a wait for C >= s lets a wave read stage s + 1's buffer before every wave has written
     # its part; writing stage s + 2 before the wait overwrites stage s - 1's buffer while a
