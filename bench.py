@@ -233,6 +233,11 @@ TRAFFIC_PROFILES = {
     (2, 100_000, 1_000, 10, "lists"): "flat_scan_kernel_ip_100kx384_q1k_k10.md",
 }
 
+# the same for the fp16 collect scan (rows and queries exact in fp16), by the same keys
+F16_PROFILES = {
+    (3, 1_000_000, 10_000, 10, "collect-bounded"): "flat_collect_scan_f16_l2_1Mx128_q10k_k10.md",
+}
+
 HEADLINE_METRIC = "exact kNN QPS (1M\u00d7128 fp32, k=10, 10k-query batch); % fp32 MFMA / HBM peak"
 
 
@@ -343,11 +348,18 @@ def bench_flat(args, dev):
                    "kernel_ms": float(np.mean(scan16)), "pipeline_ms": float(np.mean(total16)),
                    "achieved_tflops": fl16, "peak_tflops": FP16_MFMA_PEAK_TFLOPS,
                    "frac": fl16 / FP16_MFMA_PEAK_TFLOPS, "collect_rounds": info16["collect_rounds"],
+                   "traffic": read_traffic(F16_PROFILES.get((c, n, nq, k, info16["path"]), ""),
+                                           not args.sift),
                    "same_results_as_fp32_scan": bool(
                        np.array_equal(ids16, ids) and
                        np.array_equal(d16.view(np.uint32), dists.view(np.uint32)))}
             log(f"[bench] fp16 scan: {f16['ms_per_step']:.3f} ms a batch, {f16['value']:.0f} QPS, "
                 f"scan {f16['kernel_ms']:.3f} ms, same results {f16['same_results_as_fp32_scan']}")
+            ctr16 = read_counters(F16_PROFILES.get((c, n, nq, k, info16["path"]), ""), not args.sift)
+            if ctr16 and "mfma_busy_frac" in ctr16:
+                f16["mfma_busy"] = {"frac": ctr16["mfma_busy_frac"],
+                                    "lds_busy_frac": ctr16.get("lds_busy_frac"),
+                                    "source": ctr16["source"]}
         idx._scan_f16(False)
 
     flops = 2.0 * nq * n_eff * dim

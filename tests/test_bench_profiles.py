@@ -15,8 +15,8 @@ import pytest
 import bench
 
 PROFILES = Path(__file__).resolve().parent.parent / "profiles"
-NAMES = sorted(set(bench.TRAFFIC_PROFILES.values()) | {"pq_scan_kernel_l2_1Mx16_q10k_k10.md",
-                                                        "pq_scan_kernel_l2_1Mx16_q10k_k10_mask50.md"})
+NAMES = sorted(set(bench.TRAFFIC_PROFILES.values()) | set(bench.F16_PROFILES.values()) |
+               {"pq_scan_kernel_l2_1Mx16_q10k_k10.md", "pq_scan_kernel_l2_1Mx16_q10k_k10_mask50.md"})
 
 
 @pytest.mark.parametrize("name", NAMES)
@@ -58,6 +58,15 @@ def test_mfma_counter_profile_is_complete(name):
     assert 0 < ctr["mfma_busy_frac"] < 1 and ctr["mfma_flop_per_launch"] > 0
     assert 1.0 < ctr["shader_clock_ghz"] < 2.5
     assert bench.read_counters(name, False) is None
+
+
+@pytest.mark.parametrize("name", sorted(set(bench.F16_PROFILES.values())))
+def test_f16_counter_profile_is_complete(name):
+    text = (PROFILES / name).read_text()
+    assert "rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES" in text and "rocprofv3 --pmc SQ_INSTS_LDS" in text
+    ctr = bench.read_counters(name, True)
+    assert 0 < ctr["mfma_busy_frac"] < 1 and 0 < ctr["lds_busy_frac"] < 1
+    assert 1.0 < ctr["shader_clock_ghz"] < 2.5
 
 
 def test_lds_counter_profile_is_complete():
