@@ -810,8 +810,11 @@ __device__ __forceinline__ float sum8_lanes(float v) {
 // sit in LDS and every lane of a row group reads the same address (a broadcast). A row at
 // or below a slot's threshold (key, then position) is appended to the slot's region of
 // this split through an LDS counter; with dense set, every key goes to cand_keys
-// [slot][n_eff] instead (the threshold sample of a few-query batch).
-template <int NQ, bool L2, bool FILT>
+// [slot][n_eff] instead (the threshold sample of a few-query batch). H16: the rows are read
+// from their fp16 copy (FlatScanArgs::corpus_h, 128-dim rows whose every value is exact in
+// fp16), half the bytes, and widened to fp32 in registers: the same values in the same
+// arithmetic, so the keys are bit-identical to the fp32 rows'.
+template <int NQ, bool L2, bool FILT, bool H16>
 __global__ __launch_bounds__(512) void flat_vcollect_kernel(FlatScanArgs a) {
     extern __shared__ __attribute__((aligned(16))) float sq[];  // [NQ][dp]
     __shared__ float s_thr[NQ];
@@ -852,6 +855,7 @@ __global__ __launch_bounds__(512) void flat_vcollect_kernel(FlatScanArgs a) {
         bool vr[R];
         int ir[R];
         const float* xr[R];
+        const unsigned short* xh[R];
         float d[R][NQ];
 #pragma unroll
         for (int u = 0; u < R; ++u) {
@@ -860,6 +864,7 @@ __global__ __launch_bounds__(512) void flat_vcollect_kernel(FlatScanArgs a) {
             const int64_t pp = vr[u] ? pr[u] : row0;
             ir[u] = FILT ? a.rowidx[pp] : (int)pp;
             xr[u] = a.corpus + (int64_t)ir[u] * dp;
+            xh[u] = H16 ? a.corpus_h + (int64_t)ir[u] * kChunk : nullptr;
 #pragma unroll
             for (int qq = 0; qq < NQ; ++qq) d[u][qq] = 0.f;
         }
@@ -868,8 +873,15 @@ __global__ __launch_bounds__(512) void flat_vcollect_kernel(FlatScanArgs a) {
             // the corpus is read once: nontemporal loads keep it from evicting the rest
             f32x4v v[R];
 #pragma unroll
-            for (int u = 0; u < R; ++u)
-                v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(xr[u] + c));
+            for (int u = 0; u < R; ++u) {
+                if constexpr (H16) {
+                    const f16x4v w =
+                        __builtin_nontemporal_load(reinterpret_cast<const f16x4v*>(xh[u] + c));
+                    v[u] = f32x4v{(float)w[0], (float)w[1], (float)w[2], (float)w[3]};
+                } else {
+                    v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(xr[u] + c));
+                }
+            }
 #pragma unroll
             for (int qq = 0; qq < NQ; ++qq) {
                 const float4 qv = *reinterpret_cast<const float4*>(sq + qq * dp + c);
@@ -924,17 +936,23 @@ __global__ __launch_bounds__(512) void flat_vcollect_kernel(FlatScanArgs a) {
     if (!a.dense && tid < a.nq) a.cand_count[(int64_t)tid * a.splits + split] = s_cnt[tid];
 }
 
-template <int NQ>
-static void launch_vcollect_n(const FlatScanArgs& a, hipStream_t s) {
+template <int NQ, bool H16>
+static void launch_vcollect_h(const FlatScanArgs& a, hipStream_t s) {
     const dim3 grid((unsigned)a.splits), block(512);
     const size_t lds = sizeof(float) * NQ * a.dp;  // at most 64 KB (checked by the caller)
     if (a.metric == 0) {
-        if (a.rowidx) hipLaunchKernelGGL((flat_vcollect_kernel<NQ, true, true>), grid, block, lds, s, a);
-        else hipLaunchKernelGGL((flat_vcollect_kernel<NQ, true, false>), grid, block, lds, s, a);
+        if (a.rowidx) hipLaunchKernelGGL((flat_vcollect_kernel<NQ, true, true, H16>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((flat_vcollect_kernel<NQ, true, false, H16>), grid, block, lds, s, a);
     } else {
-        if (a.rowidx) hipLaunchKernelGGL((flat_vcollect_kernel<NQ, false, true>), grid, block, lds, s, a);
-        else hipLaunchKernelGGL((flat_vcollect_kernel<NQ, false, false>), grid, block, lds, s, a);
+        if (a.rowidx) hipLaunchKernelGGL((flat_vcollect_kernel<NQ, false, true, H16>), grid, block, lds, s, a);
+        else hipLaunchKernelGGL((flat_vcollect_kernel<NQ, false, false, H16>), grid, block, lds, s, a);
     }
+}
+
+template <int NQ>
+static void launch_vcollect_n(const FlatScanArgs& a, hipStream_t s) {
+    if (a.corpus_h) launch_vcollect_h<NQ, true>(a, s);
+    else launch_vcollect_h<NQ, false>(a, s);
 }
 
 hipError_t launch_flat_vcollect(const FlatScanArgs& a, hipStream_t s) {
@@ -942,7 +960,7 @@ hipError_t launch_flat_vcollect(const FlatScanArgs& a, hipStream_t s) {
     int np = 1;
     while (np < a.nq) np <<= 1;
     if (a.nq < 1 || a.nq > kVecQueries || a.dp > kVecMaxDp ||
-        (int64_t)np * a.dp > kVecMaxQueryFloats)
+        (int64_t)np * a.dp > kVecMaxQueryFloats || (a.corpus_h && a.dp != kChunk))
         return hipErrorInvalidValue;
     if (a.nq == 1) launch_vcollect_n<1>(a, s);
     else if (a.nq == 2) launch_vcollect_n<2>(a, s);

@@ -965,7 +965,11 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         PX_TRY(read_back_int(ws.count.as<int>(), ws.h_count, ws.h_count_dev, s));
         if (*ws.h_count == 0) qh = ws.qh.as<unsigned short>();
     }
-    f->last_f16 = qh != nullptr;
+    // the vector-ALU scan of a few queries reads the fp16 copy of the rows (half the bytes)
+    // and widens it: the same values, whatever the queries hold
+    const unsigned short* vh =
+        f->scan_f16 && f->d_xh && f->dp == 128 && vec_collect(nq, f->dp) ? f->d_xh : nullptr;
+    f->last_f16 = qh != nullptr || vh != nullptr;
     CollectJob j;
     j.ws = &ws;
     j.stream = s;
@@ -1000,6 +1004,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             a.metric = f->smetric;
             a.cand_keys = ws.cand_k.as<float>();
             a.dense = 1;
+            a.corpus_h = vh;
             PX_HIP(px::launch_flat_vcollect(a, s));
             px::LadderArgs la{};
             la.keys = a.cand_keys;
@@ -1097,6 +1102,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             a.cand_pos = ws.cand_p.as<int>();
             a.cand_count = ws.cand_n.as<int>();
             a.cap = (int)*cap;
+            a.corpus_h = vh;
             j.sel_dmin = nullptr;
             PX_HIP(px::launch_flat_vcollect(a, s));
             if (round == 0) {

@@ -8,6 +8,7 @@ namespace px {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4v __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4v __attribute__((ext_vector_type(4)));
 
 constexpr int kTileRows = 64;            // corpus rows per tile: two 32-row MFMA blocks
 constexpr int kChunk = 128;              // dims per staged K-chunk (16 groups of 8)

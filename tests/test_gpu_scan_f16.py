@@ -167,3 +167,26 @@ def test_exact_rows_added_later_keep_the_fp16_copy(gpu):
     o_ids, o_d, _ = oracle.flat_search(both, q, 150, oracle.L2)
     assert np.array_equal(ids, o_ids)
     assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+
+
+@pytest.mark.parametrize("nq", [1, 5, 16])
+def test_few_queries_read_the_fp16_rows(gpu, nq):
+    # batches of at most 16 queries take the vector-ALU scan; with the fp16 copy of the rows
+    # it reads half the bytes and widens them to the same fp32 values: bit-identical keys,
+    # whatever the queries hold (here not exact in fp16)
+    data = datagen.sift_like(150_000, 128, 771)
+    q = (datagen.sift_like(nq, 128, 772) + 0.37).astype(np.float32)
+    mask = datagen.mask(150_000, 0.4, 773)
+    for metric in (oracle.L2, oracle.IP):
+        idx = _index(data, metric)
+        for k, m in ((10, None), (100, None), (10, mask)):
+            print(f"case few queries nq={nq} k={k} metric={metric} mask={m is not None}", flush=True)
+            ids, d, info = _run(idx, q, k, m)
+            assert info["path"] == "vector" and info["scan_f16"]
+            o_ids, o_d, _ = oracle.flat_search(data, q, k, metric, mask=m)
+            assert_parity(ids, d, o_ids, o_d, _key_of(data, q, metric))
+            idx._scan_f16(False)
+            ids32, d32, info32 = _run(idx, q, k, m)
+            idx._scan_f16(True)
+            assert not info32["scan_f16"]
+            assert _same(ids, d, ids32, d32)
