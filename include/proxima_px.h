@@ -205,15 +205,17 @@ int px_flat_last_rounds(const px_flat* idx, int* rounds);
 #define PX_PATH_VECTOR 3
 #define PX_PATH_FULL_SORT 4 /* k past PX_MAX_K: every key computed and sorted */
 int px_flat_last_path(const px_flat* idx, int* path);
-/* Arithmetic of the collect scan over 128-dim rows. When every value of the rows and of a
- * batch's queries is exactly an fp16 zero or normal number (integer-valued descriptors such
- * as SIFT's are), each product is exact in fp16 as in fp32, and the scan multiplies on the
- * fp16 matrix cores with fp32 accumulation; its candidates are re-ranked in the reference's
- * arithmetic as on fp32. enable = 0 keeps the scan on fp32 (default 1). The fp16 copy of
- * the rows (2 bytes a value) is kept from the first px_flat_add while every row added is
- * exact. Diagnostic and tuning; no counterpart in the reference. */
+/* Use of the fp16 copy of 128-dim rows. The copy (2 bytes a value) is kept from the first
+ * px_flat_add while every row added is exactly an fp16 zero or normal number (integer-valued
+ * descriptors such as SIFT's are). With it, a collect batch whose queries are exact too
+ * multiplies on the fp16 matrix cores with fp32 accumulation (each product is exact in fp16
+ * as in fp32; the candidates are re-ranked in the reference's arithmetic as on fp32), and the
+ * vector-ALU scan of batches of at most 16 queries reads the copy and widens it to the same
+ * fp32 values. enable = 0 keeps both scans on the fp32 rows (default 1). Diagnostic and
+ * tuning; no counterpart in the reference. */
 int px_flat_set_scan_f16(px_flat* idx, int enable);
-/* *used = 1 if the handle's last search ran its collect scans in fp16, else 0. */
+/* *used = 1 if the handle's last search read the fp16 copy of the rows (either scan), else
+ * 0. */
 int px_flat_last_scan_f16(const px_flat* idx, int* used);
 /* The same for PqIndex searches (k <= 128: per-wave lists; above: threshold-collect). */
 int px_pq_last_rounds(const px_pq* idx, int* rounds);

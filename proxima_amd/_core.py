@@ -267,8 +267,9 @@ class FlatIndex:
         _check(self._lib.px_flat_set_timing(self._h, 1 if enable else 0))
 
     def _scan_f16(self, enable: bool = True) -> None:
-        """Let the collect scan multiply in fp16 when rows and queries are exact in fp16
-        (default on); off keeps it on fp32. Diagnostic; no counterpart in the reference."""
+        """Use the fp16 copy of rows exact in fp16 (default on): the collect scan multiplies
+        in fp16 where the queries are exact too, the few-query vector scan reads the copy;
+        off keeps both on the fp32 rows. Diagnostic; no counterpart in the reference."""
         _check(self._lib.px_flat_set_scan_f16(self._h, 1 if enable else 0))
 
     def _last_timing(self) -> dict:
