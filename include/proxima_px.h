@@ -207,11 +207,12 @@ int px_flat_last_rounds(const px_flat* idx, int* rounds);
 int px_flat_last_path(const px_flat* idx, int* path);
 /* Use of the fp16 copy of 128-dim rows. The copy (2 bytes a value) is kept from the first
  * px_flat_add while every row added is exactly an fp16 zero or normal number (integer-valued
- * descriptors such as SIFT's are). With it, a collect batch whose queries are exact too
- * multiplies on the fp16 matrix cores with fp32 accumulation (each product is exact in fp16
- * as in fp32; the candidates are re-ranked in the reference's arithmetic as on fp32), and the
- * vector-ALU scan of batches of at most 16 queries reads the copy and widens it to the same
- * fp32 values. enable = 0 keeps both scans on the fp32 rows (default 1). Diagnostic and
+ * descriptors such as SIFT's are). With it, a batch whose queries are exact too multiplies
+ * on the fp16 matrix cores with fp32 accumulation in the collect scan, and in the per-split
+ * list scan on at least 65,536 rows (each product is exact in fp16 as in fp32; the
+ * candidates are re-ranked in the reference's arithmetic as on fp32), and the vector-ALU
+ * scan of batches of at most 16 queries reads the copy and widens it to the same fp32
+ * values. enable = 0 keeps both scans on the fp32 rows (default 1). Diagnostic and
  * tuning; no counterpart in the reference. */
 int px_flat_set_scan_f16(px_flat* idx, int enable);
 /* *used = 1 if the handle's last search read the fp16 copy of the rows (either scan), else

@@ -130,14 +130,21 @@ __device__ __forceinline__ void first_tile_lists(const float (&key)[32], int64_t
 // appends need no cross-lane step; flat_collect_select_kernel takes it from there. The
 // threshold tests of a tile run during the next tile's MFMAs (both waves of a SIMD reach
 // the epilogue together, so an epilogue of its own would leave the matrix unit idle).
-template <int KP, int WAVES, bool L2, bool MULTI, bool FILT, bool COLLECT = false>
+template <int KP, int WAVES, bool L2, bool MULTI, bool FILT, bool COLLECT = false, bool H16 = false>
 __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     if (a.abort && *a.abort == a.abort_seq) return;
     constexpr int NT = WAVES * 64;
-    constexpr int kF4PerRow = kChunk / 4;                  // 32 float4 per staged row
+    // H16 (list mode, rows of exactly 128 dims): rows and queries as fp16 (FlatScanArgs::
+    // corpus_h, queries_h; every value exact in fp16), 16 dims a MFMA, 256-byte rows in LDS
+    // at a 272-byte pitch; else fp32 rows at kLdsStride floats
+    constexpr int kRowBytes = H16 ? kChunk * 2 : kChunk * 4;
+    constexpr int kPitch = H16 ? kRowBytes + 16 : kLdsStride * 4;
+    constexpr int kF4PerRow = kRowBytes / 16;              // 16-byte pieces per staged row
     constexpr int kRowStep = NT / kF4PerRow;               // rows between a thread's loads
-    constexpr int kPF = kTileRows / kRowStep;              // float4 per thread per stage
+    constexpr int kPF = kTileRows / kRowStep;              // pieces per thread per stage
+    constexpr int NG = H16 ? 8 : 16;                       // MFMA dim groups per chunk
     static_assert(NT % kF4PerRow == 0 && kTileRows % kRowStep == 0, "uneven stage split");
+    static_assert(!H16 || (!MULTI && !COLLECT), "fp16 rows: the one-chunk list scan");
     // Stage buffers and norm slots. Collect mode and lists of 32: three buffers and four
     // norm slots, no barrier per stage (the stage sync of px_collect.hip's scan: a wave may
     // run a stage ahead of the slowest, so that one wave's list insertions or appends do not
@@ -353,9 +360,15 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         pvalid = 0;
 #pragma unroll
         for (int u = 0; u < kPF; ++u) {
-            pf[u] = *reinterpret_cast<const float4*>(
-                a.corpus + (int64_t)max(rid[u], 0) * a.dp + c * kChunk + min(cc, f4r - 1) * 4);
-            pvalid |= (rid[u] >= 0 && cc < f4r) ? 1u << u : 0u;
+            if constexpr (H16) {
+                pf[u] = *reinterpret_cast<const float4*>(a.corpus_h + (int64_t)max(rid[u], 0) * kChunk +
+                                                         cc * 8);
+                pvalid |= rid[u] >= 0 ? 1u << u : 0u;
+            } else {
+                pf[u] = *reinterpret_cast<const float4*>(
+                    a.corpus + (int64_t)max(rid[u], 0) * a.dp + c * kChunk + min(cc, f4r - 1) * 4);
+                pvalid |= (rid[u] >= 0 && cc < f4r) ? 1u << u : 0u;
+            }
         }
         if (L2) {
             pn = a.norms[max(pid, 0)];
@@ -364,10 +377,10 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     };
     // stage buffer sb, chunk c, tile parity tp
     auto commit = [&](int sb, int c, int tp) {
-        float* tb = tile[sb];
+        char* tb = reinterpret_cast<char*>(tile[sb]);
 #pragma unroll
         for (int u = 0; u < kPF; ++u)
-            *reinterpret_cast<float4*>(tb + (rr0 + u * kRowStep) * kLdsStride + cc * 4) =
+            *reinterpret_cast<float4*>(tb + (rr0 + u * kRowStep) * kPitch + cc * 16) =
                 zero_unless((pvalid >> u) & 1u, pf[u]);
         if (L2 && c == 0 && tid < kTileRows)
             tnorm[tp][tid] = (pvalid >> kPF) & 1u ? pn : 0.f;
@@ -378,10 +391,19 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         tn = cn == 0 ? t + 1 : t;
     };
 
-    float4 b[16];
-    load_b(0, b);
+    // B operands: query chunk 0 (H16: dims 16 g + 8 h .. + 7 in fp16; zero for padding slots)
+    using Frag = std::conditional_t<H16, f16x8, float4>;
+    Frag b[NG];
+    if constexpr (H16) {
+        const unsigned short* qh = a.queries_h + (int64_t)(qvalid ? q : 0) * kChunk + h * 8;
 #pragma unroll
-    for (int g = 0; g < 16; ++g) b[g] = zero_unless(b_valid(0, g), b[g]);
+        for (int g = 0; g < NG; ++g)
+            b[g] = qvalid ? *reinterpret_cast<const f16x8*>(qh + g * 16) : f16x8{};
+    } else {
+        load_b(0, b);
+#pragma unroll
+        for (int g = 0; g < 16; ++g) b[g] = zero_unless(b_valid(0, g), b[g]);
+    }
     if (nstages > 0) {
         tile_ids(0);
         fetch(0);
@@ -475,17 +497,18 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             acc0 = (f32x16){0.f};
             acc1 = (f32x16){0.f};
         }
-        const int ng = wave_live ? min(kChunk, a.dp - c * kChunk) >> 3 : 0;
+        const int ng = !wave_live ? 0 : H16 ? NG : min(kChunk, a.dp - c * kChunk) >> 3;
         const int sb = RELAXED ? rb : (int)(s & 1);
-        const float* ta0 = tile[sb] + j * kLdsStride + h * 4;
-        const float* ta1 = tile[sb] + (32 + j) * kLdsStride + h * 4;
+        // rows j and 32 + j, the lane's 16 bytes of each 32-byte dim group
+        const char* ta0 = reinterpret_cast<const char*>(tile[sb]) + j * kPitch + h * 16;
+        const char* ta1 = ta0 + 32 * kPitch;
 #pragma unroll
-        for (int g = 0; g < 16; ++g) {
+        for (int g = 0; g < NG; ++g) {
             if (g < ng) {
-                const float4 a0 = *reinterpret_cast<const float4*>(ta0 + g * 8);
-                const float4 a1 = *reinterpret_cast<const float4*>(ta1 + g * 8);
-                acc0 = mfma4(a0, b[g], acc0);
-                acc1 = mfma4(a1, b[g], acc1);
+                const Frag a0 = *reinterpret_cast<const Frag*>(ta0 + g * 32);
+                const Frag a1 = *reinterpret_cast<const Frag*>(ta1 + g * 32);
+                acc0 = mfma_group(a0, b[g], acc0);
+                acc1 = mfma_group(a1, b[g], acc1);
             }
             if constexpr (MULTI)
                 b[g] = *reinterpret_cast<const float4*>(qrow + cn * kChunk +
@@ -499,7 +522,11 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                 }
             }
             if constexpr (LDEFER) {
-                if (pend) list_x(16 + g);
+                // the previous tile's rows 16 .. 31, one (H16: two) a group
+                if (pend) {
+                    list_x(16 + (16 / NG) * g);
+                    if constexpr (H16) list_x(17 + 2 * g);
+                }
             }
         }
         if constexpr (COLLECT) pend = false;
@@ -756,14 +783,14 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     }
 }
 
-template <int KP, int WAVES, bool L2, bool MULTI>
+template <int KP, int WAVES, bool L2, bool MULTI, bool H16 = false>
 static void launch_scan_f(const FlatScanArgs& a, dim3 grid, hipStream_t s) {
     if (a.rowidx)
-        hipLaunchKernelGGL((flat_scan_kernel<KP, WAVES, L2, MULTI, true>), grid, dim3(WAVES * 64),
-                           0, s, a);
+        hipLaunchKernelGGL((flat_scan_kernel<KP, WAVES, L2, MULTI, true, false, H16>), grid,
+                           dim3(WAVES * 64), 0, s, a);
     else
-        hipLaunchKernelGGL((flat_scan_kernel<KP, WAVES, L2, MULTI, false>), grid, dim3(WAVES * 64),
-                           0, s, a);
+        hipLaunchKernelGGL((flat_scan_kernel<KP, WAVES, L2, MULTI, false, false, H16>), grid,
+                           dim3(WAVES * 64), 0, s, a);
 }
 
 template <int KP, int WAVES>
@@ -774,7 +801,13 @@ static hipError_t launch_scan_t(const FlatScanArgs& a, hipStream_t s) {
     // several chunks: the grid is padded to a multiple of the 8 XCDs (see flat_scan_kernel)
     const bool xm = multi && a.xcd_major;
     const dim3 grid((unsigned)(xm ? (qtiles * a.splits + 7) / 8 * 8 : qtiles * a.splits));
-    if (a.metric == 0) {
+    // fp16 rows and queries (both or neither): rows of exactly 128 dims
+    if ((a.corpus_h == nullptr) != (a.queries_h == nullptr) || (a.corpus_h && a.dp != kChunk))
+        return hipErrorInvalidValue;
+    if (a.corpus_h) {
+        if (a.metric == 0) launch_scan_f<KP, WAVES, true, false, true>(a, grid, s);
+        else launch_scan_f<KP, WAVES, false, false, true>(a, grid, s);
+    } else if (a.metric == 0) {
         if (multi) launch_scan_f<KP, WAVES, true, true>(a, grid, s);
         else launch_scan_f<KP, WAVES, true, false>(a, grid, s);
     } else {
@@ -1760,7 +1793,7 @@ hipError_t launch_nonfinite_check(const float* x, int64_t count, int* flag, hipS
 // subnormals are excluded so that no MFMA input depends on subnormal handling). count is a
 // multiple of 4; x and out are 16- and 8-byte aligned.
 __global__ __launch_bounds__(256) void to_f16_kernel(const float4* x, int64_t count4,
-                                                     ushort4* out, int* inexact) {
+                                                     ushort4* out, int* inexact, int bit) {
     bool bad = false;
     auto one = [&](float v) -> unsigned short {
         const _Float16 hv = (_Float16)v;
@@ -1772,11 +1805,11 @@ __global__ __launch_bounds__(256) void to_f16_kernel(const float4* x, int64_t co
         const float4 v = x[i];
         out[i] = make_ushort4(one(v.x), one(v.y), one(v.z), one(v.w));
     }
-    if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(inexact, 1);
+    if (__ballot(bad) != 0 && (threadIdx.x & 63) == 0) atomicOr(inexact, bit);
 }
 
 hipError_t launch_to_f16(const float* x, int64_t count, unsigned short* out, int* inexact,
-                         hipStream_t s) {
+                         hipStream_t s, int bit) {
     if (count % 4 != 0 || ((uintptr_t)x & 15) != 0 || ((uintptr_t)out & 7) != 0)
         return hipErrorInvalidValue;
     if (count <= 0) return hipSuccess;
@@ -1784,7 +1817,7 @@ hipError_t launch_to_f16(const float* x, int64_t count, unsigned short* out, int
     const int64_t blocks = std::min<int64_t>((count4 + 255) / 256, 4096);
     hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
                        reinterpret_cast<const float4*>(x), count4,
-                       reinterpret_cast<ushort4*>(out), inexact);
+                       reinterpret_cast<ushort4*>(out), inexact, bit);
     return hipGetLastError();
 }
 

@@ -642,6 +642,9 @@ int flat_sync(px_flat* f) {
 // sample pass and no host round trip. The PX_FLAT_COLLECT_FROM_K environment variable
 // overrides the k (read once).
 constexpr int64_t kCollectMinQueries = 256;
+// Fewest rows on which the per-split list path takes the fp16 scan (its exactness check
+// costs one read-back of the stream).
+constexpr int64_t kF16ListMinRows = 65536;
 int64_t collect_from_k() {
     static const int64_t v = [] {
         const char* e = std::getenv("PX_FLAT_COLLECT_FROM_K");
@@ -1267,10 +1270,11 @@ struct ListBufs {
 // The per-split list path: fused MFMA scan with per-split lists, then the merge (re-rank in
 // the reference's arithmetic, finish, pad). Waits for the stream. timed: record the
 // handle's HIP events (created beforehand).
+// qh: the queries in fp16 when they and the rows are exact in fp16 (the fp16 scan), or null.
 int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t n_eff,
                    const int* rowidx, const ListPlan& lp, int kl, const ListBufs& b,
                    int64_t* d_ids, float* d_out, int raw_keys, bool timed,
-                   const PendingCheck* chk = nullptr) {
+                   const PendingCheck* chk = nullptr, const unsigned short* qh = nullptr) {
     hipStream_t s = f->stream;
     const int splits = lp.splits;
     const int64_t rps = lp.rps, groups = lp.groups;
@@ -1308,6 +1312,8 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     a.abort = d_flag;
     a.abort_seq = seq;
     a.xcd_major = xcd_major_for(a, px::flat_queries_per_block(kl), std::max(f->dev.cus, 1));
+    a.corpus_h = qh ? f->d_xh : nullptr;
+    a.queries_h = qh;
     if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[1], s));
 
@@ -1405,6 +1411,29 @@ int flat_run_paths(px_flat* f, const float* d_q, int64_t nq, int64_t k, const ui
     }
 
     const int kl = (int)std::min<int64_t>(px::kMaxList, k + kReRankMargin);
+    // the fp16 scan where the rows are exact in fp16 and so are the queries: one pass
+    // converts them and flags any value that is not exact (and, with a finiteness check
+    // still pending, any that is not finite), its verdict read back before the scan. On
+    // fewer rows the read-back would cost about what the fp16 scan saves.
+    const unsigned short* qh = nullptr;
+    if (f->scan_f16 && f->d_xh && f->dp == 128 && n_eff >= kF16ListMinRows &&
+        ((uintptr_t)d_q & 15) == 0) {
+        PX_TRY(ws.qh.reserve(sizeof(unsigned short) * nq * 128));
+        PX_TRY(ws.count.reserve(sizeof(int)));
+        PX_TRY(ws.ensure_pinned());
+        int* flag = ws.count.as<int>();
+        if (chk) {
+            PX_HIP(px::launch_nonfinite_check(chk->x, chk->count, flag, s));  // bit 0
+            chk = nullptr;
+        } else {
+            PX_HIP(px::launch_fill_int(flag, 1, 0, s));
+        }
+        PX_HIP(px::launch_to_f16(d_q, nq * 128, ws.qh.as<unsigned short>(), flag, s, 2));
+        PX_TRY(read_back_int(flag, ws.h_count, ws.h_count_dev, s));
+        if (*ws.h_count & 1) return nonfinite_error();
+        if (!(*ws.h_count & 2)) qh = ws.qh.as<unsigned short>();
+    }
+    f->last_f16 = qh != nullptr;
     ListPlan lp;
     PX_TRY(plan_list_scan(n_eff, nq, kl, f->dev.cus, &lp, k));
     PX_TRY(ws.part_k.reserve(sizeof(float) * nq * lp.splits * kl));
@@ -1414,7 +1443,7 @@ int flat_run_paths(px_flat* f, const float* d_q, int64_t nq, int64_t k, const ui
     PX_TRY(f->timing.ensure());
     ListBufs b{ws.part_k.as<float>(), ws.part_i.as<int>(), ws.gtau.as<int>(), ws.gbest.as<int>()};
     return flat_run_lists(f, d_q, nq, k, n_eff, rowidx, lp, kl, b, d_ids, d_out, raw_keys,
-                          f->timing.enabled, chk);
+                          f->timing.enabled, chk, qh);
 }
 
 void host_padding(int metric, int64_t nq, int64_t k, int64_t* ids, float* out, int raw_keys) {

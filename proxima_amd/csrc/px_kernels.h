@@ -217,11 +217,11 @@ hipError_t launch_pad_rows(const float* src, int64_t rows, int dim, int dp, floa
 
 // *flag = 1 when any of x[0 .. count) is NaN or infinite, else 0 (the flag is cleared first).
 hipError_t launch_nonfinite_check(const float* x, int64_t count, int* flag, hipStream_t s);
-// out[0 .. count) = x as fp16 bit patterns; atomically ORs 1 into *inexact when any value is
-// not exactly an fp16 zero or normal number (the caller clears it). count % 4 == 0, x 16-byte
-// and out 8-byte aligned.
+// out[0 .. count) = x as fp16 bit patterns; atomically ORs bit into *inexact when any value
+// is not exactly an fp16 zero or normal number (the caller clears it). count % 4 == 0, x
+// 16-byte and out 8-byte aligned.
 hipError_t launch_to_f16(const float* x, int64_t count, unsigned short* out, int* inexact,
-                         hipStream_t s);
+                         hipStream_t s, int bit = 1);
 // The per-split list path's first kernel: *flag = max(*flag, seq) when any of count floats
 // of x is NaN or infinite (flag is never cleared: each search takes a larger seq), and
 // gtau[0..ngtau) and gbest[0..ngbest) filled with kTotalKeyInf. One launch where a flag

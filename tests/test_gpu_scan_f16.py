@@ -190,3 +190,91 @@ def test_few_queries_read_the_fp16_rows(gpu, nq):
             idx._scan_f16(True)
             assert not info32["scan_f16"]
             assert _same(ids, d, ids32, d32)
+
+
+@pytest.mark.parametrize("metric", [oracle.L2, oracle.IP])
+@pytest.mark.parametrize("nq,k", [(32, 10), (100, 1), (200, 40), (255, 100), (40, 120)])
+def test_list_path_in_fp16(gpu, metric, nq, k):
+    # batches of 17..255 queries (and other list-path cases) over at least 65,536 rows of
+    # 128 dims take the per-split lists in fp16 (each list capacity: k' = k + 8 of 32, 56,
+    # 120 and 128); results bit-identical to the oracle and to the fp32 lists
+    data = datagen.sift_like(120_000, 128, 781)
+    q = datagen.sift_like(nq, 128, 782)
+    idx = _index(data, metric)
+    print(f"case lists fp16 nq={nq} k={k} metric={metric}", flush=True)
+    ids, d, info = _run(idx, q, k)
+    assert info["path"] == "lists" and info["scan_f16"], info
+    o_ids, o_d, _ = oracle.flat_search(data, q, k, metric)
+    assert np.array_equal(ids, o_ids)
+    assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+    idx._scan_f16(False)
+    ids32, d32, info32 = _run(idx, q, k)
+    assert info32["path"] == "lists" and not info32["scan_f16"]
+    assert _same(ids, d, ids32, d32)
+
+
+def test_list_path_in_fp16_filtered_and_fallback(gpu):
+    data = datagen.sift_like(100_000, 128, 791)
+    q = datagen.sift_like(64, 128, 792)
+    mask = datagen.mask(100_000, 0.7, 793)
+    idx = _index(data, oracle.L2)
+    print("case lists fp16 filtered", flush=True)
+    ids, d, info = _run(idx, q, 10, mask)
+    assert info["path"] == "lists" and info["scan_f16"]
+    o_ids, o_d, _ = oracle.flat_search(data, q, 10, oracle.L2, mask=mask)
+    assert np.array_equal(ids, o_ids) and np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+    # queries not exact in fp16: the fp32 lists
+    qf = (q + 0.25).astype(np.float32)
+    qf[3, 7] += 0.001
+    ids, d, info = _run(idx, qf, 10)
+    assert info["path"] == "lists" and not info["scan_f16"]
+    o_ids, o_d, _ = oracle.flat_search(data, qf, 10, oracle.L2)
+    assert_parity(ids, d, o_ids, o_d, _key_of(data, qf, oracle.L2))
+    # fewer than 65,536 rows: the lists stay on fp32 (the exactness check would cost what
+    # the fp16 scan saves)
+    small = _index(data[:50_000], oracle.L2)
+    _, _, info = _run(small, q, 10)
+    assert info["path"] == "lists" and not info["scan_f16"]
+
+
+def test_list_path_fp16_device_nonfinite(gpu):
+    # the device form's finiteness check is answered by the fp16 pass's read-back on this
+    # path: a NaN or infinite query still fails with PX_ERR_NONFINITE, outputs unwritten
+    import ctypes
+    from proxima_amd import _lib
+    lib = _lib.load()
+    nq, k = 200, 10
+    data = datagen.sift_like(80_000, 128, 801)
+    q = datagen.sift_like(nq, 128, 802)
+    idx = _index(data, oracle.L2)
+    ptrs = []
+
+    def dev(arr):
+        p = ctypes.c_void_p()
+        assert lib.px_dev_alloc(ctypes.byref(p), max(arr.nbytes, 1)) == 0
+        ptrs.append(p)
+        assert lib.px_dev_upload(p, arr.ctypes.data, arr.nbytes) == 0
+        return p
+
+    try:
+        sentinel_i = np.full((nq, k), 1234567, dtype=np.int64)
+        sentinel_d = np.full((nq, k), 7.5, dtype=np.float32)
+        di, dd = dev(sentinel_i), dev(sentinel_d)
+        for bad in (np.nan, np.inf):
+            qb = q.copy()
+            qb[nq // 2, 17] = bad
+            print(f"case fp16 lists device nonfinite {bad}", flush=True)
+            rc = lib.px_flat_search_device(idx._h, dev(qb), nq, k, None, di, dd)
+            assert rc == _lib.PX_ERR_NONFINITE, (rc, _lib.last_error())
+            got_i = np.empty_like(sentinel_i)
+            assert lib.px_dev_download(got_i.ctypes.data, di, got_i.nbytes) == 0
+            assert np.array_equal(got_i, sentinel_i)
+        assert lib.px_flat_search_device(idx._h, dev(q), nq, k, None, di, dd) == 0, _lib.last_error()
+        assert idx._last_timing()["path"] == "lists" and idx._last_timing()["scan_f16"]
+        ids = np.empty_like(sentinel_i)
+        assert lib.px_dev_download(ids.ctypes.data, di, ids.nbytes) == 0
+        o_ids, _, _ = oracle.flat_search(data, q, k, oracle.L2)
+        assert np.array_equal(ids, o_ids)
+    finally:
+        for p in ptrs:
+            lib.px_dev_free(p)
