@@ -23,6 +23,13 @@
 // tile's row norms (L2) sit in one of four small LDS buffers, kept until its keys are
 // computed a tile later.
 //
+// H16 (FlatScanArgs::corpus_h / queries_h: rows and queries whose every value is exact in
+// fp16): the same scan on v_mfma_f32_32x32x16_f16 with fp32 accumulation. Each product is
+// exact in fp16 as in fp32, so the keys are the fp32 scan's up to the rounding of the sums.
+// A group of 16 dims is only two MFMAs, so a stage holds two tiles (one stage sync per 32
+// MFMAs of a wave), norms sit in eight slots (one a tile), and each group's A operands and
+// norms are read two groups ahead.
+//
 // Appends go to one of two regions per (query slot, split), one per lane of the pair that
 // holds the query (lanes l and l ^ 32 hold the two halves of the query's 64 rows of a
 // tile), each with its own counter, so appends need no cross-lane step. dense: no

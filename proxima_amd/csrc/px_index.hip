@@ -178,7 +178,7 @@ struct Workspace {
     // collect path (k' past the lists)
     DevBuf thr_k, thr_p, lad_k, lad_p, rung, status, cand_k, cand_p, cand_n, samp_row, qlist;
     DevBuf cand_d;           // smallest dropped key of each overflowing region
-    DevBuf qh;               // a collect batch's queries as fp16 (px_flat::d_xh)
+    DevBuf qh;               // a batch's queries as fp16 (the fp16 scans; px_flat::d_xh)
     DevBuf fflag;            // finiteness verdicts of list-path searches (next_finite_seq)
     int fseq = 0;
     DevBuf dbgw;             // debug build: the debug word of the kernels' index checks ...
@@ -506,13 +506,14 @@ struct px_flat {
     float* d_norm = nullptr;       // [cap]
     int64_t d_rows = 0, d_cap = 0;
     // 128-dim rows: their fp16 mirror [cap][128], kept while every value mirrored so far is
-    // exactly an fp16 zero or normal number (integer descriptors such as SIFT's are); the
-    // collect scan then multiplies in fp16 for a batch whose queries are exact too. Dropped
-    // for good at the first row that is not (or if its memory cannot be had).
+    // exactly an fp16 zero or normal number (integer descriptors such as SIFT's are). The
+    // collect and list scans multiply in fp16 for a batch whose queries are exact too; the
+    // vector-ALU scan of a few queries reads it widened. Dropped for good at the first row
+    // that is not exact (or if its memory cannot be had).
     unsigned short* d_xh = nullptr;
     bool xh_exact = true;
     bool scan_f16 = true;          // px_flat_set_scan_f16
-    bool last_f16 = false;         // the last search's collect scan multiplied in fp16
+    bool last_f16 = false;         // the last search read d_xh (px_flat_last_scan_f16)
     Workspace ws;
     Timing timing;
     int last_path = PX_PATH_LISTS; // selection path of the last search
