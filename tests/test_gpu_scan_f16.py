@@ -278,3 +278,38 @@ def test_list_path_fp16_device_nonfinite(gpu):
     finally:
         for p in ptrs:
             lib.px_dev_free(p)
+
+
+def test_knn_seam_and_reload_in_fp16(gpu, tmp_path):
+    # the reference's C seam (knn_gpu_create / knn_gpu_search, raw keys, metric per call)
+    # and a FlatIndex saved and loaded again both keep the fp16 copy of exact rows: raw
+    # keys equal to the oracle's for both metrics on one handle, and a reloaded index's
+    # search takes the fp16 scan with the same results
+    from proxima_amd import _lib
+    lib = _lib.load()
+    data = datagen.sift_like(70_000, 128, 811)
+    q = datagen.sift_like(300, 128, 812)
+    k = 10
+    g = lib.knn_gpu_create(_lib.f32p(data), 70_000, 128)
+    assert g
+    try:
+        for metric in (oracle.L2, oracle.IP):
+            print(f"case knn seam fp16 metric={metric}", flush=True)
+            ids = np.zeros((300, k), dtype=np.int64)
+            keys = np.zeros((300, k), dtype=np.float32)
+            rc = lib.knn_gpu_search(g, _lib.f32p(q), 300, k, metric, _lib.i64p(ids), _lib.f32p(keys))
+            assert rc == 0, _lib.last_error()
+            o_ids, _, o_keys = oracle.flat_search(data, q, k, metric)
+            assert np.array_equal(ids, o_ids)
+            assert np.array_equal(keys, o_keys)
+    finally:
+        lib.knn_gpu_free(g)
+    idx = _index(data, oracle.L2)
+    path = str(tmp_path / "flat.sfidx")
+    idx.save(path)
+    back = FlatIndex.load(path)
+    print("case reloaded index fp16", flush=True)
+    ids, d, info = _run(back, q, 100)
+    assert info["scan_f16"]
+    ids0, d0, _ = _run(idx, q, 100)
+    assert _same(ids, d, ids0, d0)
