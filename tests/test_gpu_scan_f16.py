@@ -1,11 +1,13 @@
-"""GPU parity of the fp16 collect scan (flat_collect_kernel with fp16 operands).
+"""GPU parity of the scans that use the fp16 copy of exact rows.
 
 When every value of the rows and of a batch's queries is exactly an fp16 zero or normal
 number -- integer-valued descriptors such as the SIFT-like workload's are -- every product
-q_i * x_i is exact in fp16 as in fp32, so the collect scan multiplies on the fp16 matrix
-cores with fp32 accumulation; the candidates it collects are re-ranked in the reference's
-arithmetic (distance.rs:3-39) exactly as on the fp32 scan. Results must equal the oracle's
-(flat.rs:106-148) bit for bit on integer data, equal the fp32 scan's, and the scan must fall
+q_i * x_i is exact in fp16 as in fp32, so the collect scan (flat_collect_kernel) and the
+per-split list scan (flat_scan_kernel, on at least 65,536 rows) multiply on the fp16 matrix
+cores with fp32 accumulation; their candidates are re-ranked in the reference's arithmetic
+(distance.rs:3-39) exactly as on the fp32 scans. The vector-ALU scan of at most 16 queries
+reads the copy widened to the same fp32 values. Results must equal the oracle's
+(flat.rs:106-148) bit for bit on integer data and the fp32 scans', and the scans must fall
 back to fp32 whenever a row or a query is not exact in fp16 (rounded, past 65504, or an fp16
 subnormal).
 """
