@@ -315,3 +315,30 @@ def test_knn_seam_and_reload_in_fp16(gpu, tmp_path):
     assert info["scan_f16"]
     ids0, d0, _ = _run(idx, q, 100)
     assert _same(ids, d, ids0, d0)
+
+
+def test_padded_dims_and_large_integers(gpu):
+    # 125 dims pad to 128 with zero columns (exact in fp16): the copy and both scans hold
+    rng = np.random.default_rng(821)
+    d125 = rng.integers(0, 256, size=(80_000, 125)).astype(np.float32)
+    q125 = rng.integers(0, 256, size=(400, 125)).astype(np.float32)
+    idx = _index(d125, oracle.L2)
+    for k, nq in ((100, 400), (10, 100)):
+        print(f"case 125 dims k={k} nq={nq}", flush=True)
+        ids, d, info = _run(idx, q125[:nq], k)
+        assert info["scan_f16"]
+        o_ids, o_d, _ = oracle.flat_search(d125, q125[:nq], k, oracle.L2)
+        assert np.array_equal(ids, o_ids)
+        assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+    # integers up to 2047 are exact in fp16, but their sums pass 2^24: fp32 accumulation
+    # rounds, in the fp16 MFMA's order as in the fp32 one's -- the parity rule, with its
+    # near-tie exemption, as for any rounded data
+    big = rng.integers(0, 2048, size=(70_000, 128)).astype(np.float32)
+    qb = rng.integers(0, 2048, size=(300, 128)).astype(np.float32)
+    for metric in (oracle.L2, oracle.IP):
+        idx = _index(big, metric)
+        print(f"case integers to 2047 metric={metric}", flush=True)
+        ids, d, info = _run(idx, qb, 50)
+        assert info["scan_f16"]
+        o_ids, o_d, _ = oracle.flat_search(big, qb, 50, metric)
+        assert_parity(ids, d, o_ids, o_d, _key_of(big, qb, metric))
