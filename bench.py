@@ -353,8 +353,18 @@ def bench_flat(args, dev):
                    "same_results_as_fp32_scan": bool(
                        np.array_equal(ids16, ids) and
                        np.array_equal(d16.view(np.uint32), dists.view(np.uint32)))}
+            # from host arrays through the Python surface, as host_buffer above
+            if mask is not None:
+                hb16, (hi16, hd16) = host_buffer_qps(
+                    lambda: idx.search_batch_filtered(queries, mask, k=k), nq)
+            else:
+                hb16, (hi16, hd16) = host_buffer_qps(lambda: idx.search_batch(queries, k=k), nq)
+            hb16["same_results_as_device_form"] = bool(
+                np.array_equal(hi16, ids16) and np.array_equal(hd16.view(np.uint32), d16.view(np.uint32)))
+            f16["host_buffer"] = hb16
             log(f"[bench] fp16 scan: {f16['ms_per_step']:.3f} ms a batch, {f16['value']:.0f} QPS, "
-                f"scan {f16['kernel_ms']:.3f} ms, same results {f16['same_results_as_fp32_scan']}")
+                f"scan {f16['kernel_ms']:.3f} ms, same results {f16['same_results_as_fp32_scan']}; "
+                f"host-buffer {hb16['ms_median']:.3f} ms")
             ctr16 = read_counters(F16_PROFILES.get((c, n, nq, k, info16["path"]), ""), not args.sift)
             if ctr16 and "mfma_busy_frac" in ctr16:
                 f16["mfma_busy"] = {"frac": ctr16["mfma_busy_frac"],
