@@ -55,8 +55,20 @@ int fail(int code, const std::string& msg) {
     } while (0)
 
 bool all_finite(const float* x, int64_t len) {
-    for (int64_t i = 0; i < len; ++i)
-        if (!std::isfinite(x[i])) return false;
+    // blocks of 4,096 values, the exponent bits of each compared and OR-ed with no early
+    // exit inside a block, so that the loop vectorizes (a value is NaN or infinite exactly
+    // when its exponent bits are all ones)
+    constexpr int64_t kBlock = 4096;
+    for (int64_t b = 0; b < len; b += kBlock) {
+        const int64_t e = std::min(len, b + kBlock);
+        uint32_t bad = 0;
+        for (int64_t i = b; i < e; ++i) {
+            uint32_t u;
+            std::memcpy(&u, x + i, sizeof(u));
+            bad |= (uint32_t)((u & 0x7f800000u) == 0x7f800000u);
+        }
+        if (bad) return false;
+    }
     return true;
 }
 
@@ -259,15 +271,18 @@ int upload_queries(Workspace& ws, const float* queries, int64_t nq, int64_t dim,
                    hipStream_t s, const float** d_q) {
     const size_t bytes = sizeof(float) * (size_t)(nq * dim);
     PX_TRY(Workspace::ensure_host(ws.h_in, ws.h_in_cap, bytes));
-    std::memcpy(ws.h_in, queries, bytes);
     PX_TRY(ws.q.reserve(sizeof(float) * nq * dp));
-    if (dp == dim) {
-        PX_HIP(hipMemcpyAsync(ws.q.p, ws.h_in, bytes, hipMemcpyHostToDevice, s));
-    } else {
-        PX_TRY(ws.qraw.reserve(bytes));
-        PX_HIP(hipMemcpyAsync(ws.qraw.p, ws.h_in, bytes, hipMemcpyHostToDevice, s));
-        PX_HIP(px::launch_pad_rows(ws.qraw.as<float>(), nq, (int)dim, (int)dp, ws.q.as<float>(), s));
+    if (dp != dim) PX_TRY(ws.qraw.reserve(bytes));
+    char* dst = static_cast<char*>(dp == dim ? ws.q.p : ws.qraw.p);
+    // staged in 1 MB pieces: the copy engine moves one while the host stages the next
+    constexpr size_t kPiece = (size_t)1 << 20;
+    for (size_t off = 0; off < bytes; off += kPiece) {
+        const size_t n = std::min(kPiece, bytes - off);
+        std::memcpy(ws.h_in + off, reinterpret_cast<const char*>(queries) + off, n);
+        PX_HIP(hipMemcpyAsync(dst + off, ws.h_in + off, n, hipMemcpyHostToDevice, s));
     }
+    if (dp != dim)
+        PX_HIP(px::launch_pad_rows(ws.qraw.as<float>(), nq, (int)dim, (int)dp, ws.q.as<float>(), s));
     *d_q = ws.q.as<float>();
     return PX_OK;
 }
