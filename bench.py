@@ -344,6 +344,8 @@ def bench_flat(args, dev):
             d16 = dev.get(dd, np.empty((nq, k), dtype=np.float32))
             fl16 = 2.0 * nq * n_eff * dim / (np.mean(scan16) * 1e-3) / 1e12
             f16 = {"value": nq * args.steps / el16, "unit": "queries/s",
+                   "dtype": "f16 operands (every value exact in fp16), f32 accumulation; "
+                            "f32 re-rank",
                    "ms_per_step": el16 / args.steps * 1e3,
                    "kernel_ms": float(np.mean(scan16)), "pipeline_ms": float(np.mean(total16)),
                    "achieved_tflops": fl16, "peak_tflops": FP16_MFMA_PEAK_TFLOPS,
