@@ -54,6 +54,29 @@ int fail(int code, const std::string& msg) {
         if (rc_ != PX_OK) return rc_; \
     } while (0)
 
+// all_finite, and in the same pass whether every value is exactly an fp16 zero or normal
+// number (*f16_exact): zero, or an exponent in fp16's normal range (2^-14 .. 2^15) with the
+// 13 low mantissa bits clear -- what to_f16_kernel checks on the device.
+bool finite_and_f16(const float* x, int64_t len, bool* f16_exact) {
+    constexpr int64_t kBlock = 4096;
+    uint32_t inexact = 0;
+    for (int64_t b = 0; b < len; b += kBlock) {
+        const int64_t e = std::min(len, b + kBlock);
+        uint32_t bad = 0;
+        for (int64_t i = b; i < e; ++i) {
+            uint32_t u;
+            std::memcpy(&u, x + i, sizeof(u));
+            const uint32_t ex = (u >> 23) & 0xffu;
+            bad |= (uint32_t)(ex == 0xffu);
+            inexact |= (uint32_t)((u & 0x7fffffffu) != 0 &&
+                                  (ex < 113u || ex > 142u || (u & 0x1fffu) != 0));
+        }
+        if (bad) return false;
+    }
+    *f16_exact = inexact == 0;
+    return true;
+}
+
 bool all_finite(const float* x, int64_t len) {
     // blocks of 4,096 values, the exponent bits of each compared and OR-ed with no early
     // exit inside a block, so that the loop vectorizes (a value is NaN or infinite exactly
@@ -529,6 +552,8 @@ struct px_flat {
     bool xh_exact = true;
     bool scan_f16 = true;          // px_flat_set_scan_f16
     bool last_f16 = false;         // the last search read d_xh (px_flat_last_scan_f16)
+    int q_f16 = -1;                // host-array search in progress: its queries are exact in
+                                   // fp16 (1) or not (0), checked on the host; -1: unknown
     Workspace ws;
     Timing timing;
     int last_path = PX_PATH_LISTS; // selection path of the last search
@@ -972,17 +997,22 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     const int cus = std::max(f->dev.cus, 1);
     // the fp16 scan: rows exact in fp16 (d_xh) and so are this batch's queries (one
     // conversion pass, its verdict read back)
+    // (queries checked on the host: no read-back, or no conversion at all)
     const unsigned short* qh = nullptr;
     if (f->scan_f16 && f->d_xh && f->dp == 128 && !vec_collect(nq, f->dp) &&
-        ((uintptr_t)d_q & 15) == 0) {
+        ((uintptr_t)d_q & 15) == 0 && f->q_f16 != 0) {
         PX_TRY(ws.qh.reserve(sizeof(unsigned short) * nq * 128));
         PX_TRY(ws.count.reserve(sizeof(int)));
         PX_TRY(ws.ensure_pinned());
         PX_HIP(px::launch_fill_int(ws.count.as<int>(), 1, 0, s));
         PX_HIP(px::launch_to_f16(d_q, nq * 128, ws.qh.as<unsigned short>(), ws.count.as<int>(),
                                  s));
-        PX_TRY(read_back_int(ws.count.as<int>(), ws.h_count, ws.h_count_dev, s));
-        if (*ws.h_count == 0) qh = ws.qh.as<unsigned short>();
+        if (f->q_f16 == 1) {
+            qh = ws.qh.as<unsigned short>();
+        } else {
+            PX_TRY(read_back_int(ws.count.as<int>(), ws.h_count, ws.h_count_dev, s));
+            if (*ws.h_count == 0) qh = ws.qh.as<unsigned short>();
+        }
     }
     // the vector-ALU scan of a few queries reads the fp16 copy of the rows (half the bytes)
     // and widens it: the same values, whatever the queries hold
@@ -1433,11 +1463,12 @@ int flat_run_paths(px_flat* f, const float* d_q, int64_t nq, int64_t k, const ui
     // fewer rows the read-back would cost about what the fp16 scan saves.
     const unsigned short* qh = nullptr;
     if (f->scan_f16 && f->d_xh && f->dp == 128 && n_eff >= kF16ListMinRows &&
-        ((uintptr_t)d_q & 15) == 0) {
+        ((uintptr_t)d_q & 15) == 0 && f->q_f16 != 0) {
         PX_TRY(ws.qh.reserve(sizeof(unsigned short) * nq * 128));
         PX_TRY(ws.count.reserve(sizeof(int)));
         PX_TRY(ws.ensure_pinned());
         int* flag = ws.count.as<int>();
+        const bool pending = chk != nullptr;
         if (chk) {
             PX_HIP(px::launch_nonfinite_check(chk->x, chk->count, flag, s));  // bit 0
             chk = nullptr;
@@ -1445,9 +1476,13 @@ int flat_run_paths(px_flat* f, const float* d_q, int64_t nq, int64_t k, const ui
             PX_HIP(px::launch_fill_int(flag, 1, 0, s));
         }
         PX_HIP(px::launch_to_f16(d_q, nq * 128, ws.qh.as<unsigned short>(), flag, s, 2));
-        PX_TRY(read_back_int(flag, ws.h_count, ws.h_count_dev, s));
-        if (*ws.h_count & 1) return nonfinite_error();
-        if (!(*ws.h_count & 2)) qh = ws.qh.as<unsigned short>();
+        if (f->q_f16 == 1 && !pending) {
+            qh = ws.qh.as<unsigned short>();  // checked on the host: no read-back
+        } else {
+            PX_TRY(read_back_int(flag, ws.h_count, ws.h_count_dev, s));
+            if (*ws.h_count & 1) return nonfinite_error();
+            if (!(*ws.h_count & 2)) qh = ws.qh.as<unsigned short>();
+        }
     }
     f->last_f16 = qh != nullptr;
     ListPlan lp;
@@ -1482,10 +1517,17 @@ int check_search_args(const void* idx, const void* queries, int64_t nq, int64_t 
 // Host-pointer search: upload, run, download.
 int flat_search_host(px_flat* f, int metric, const float* queries, int64_t nq, int64_t k,
                      const uint8_t* mask, int64_t* out_ids, float* out_d, int raw_keys) {
-    if (!all_finite(queries, nq * f->dim))
+    bool f16_exact = false;
+    if (!finite_and_f16(queries, nq * f->dim, &f16_exact))
         return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
     std::lock_guard<std::mutex> lock(f->mu);
     f->smetric = metric;
+    // the fp16 scans need no read-back of their device check for these queries
+    struct HintReset {
+        px_flat* f;
+        ~HintReset() { f->q_f16 = -1; }
+    } hint_reset{f};
+    f->q_f16 = f16_exact ? 1 : 0;
     if (f->n == 0) {
         host_padding(metric, nq, k, out_ids, out_d, raw_keys);
         return PX_OK;
@@ -1988,10 +2030,13 @@ int px_flat_add(px_flat* f, const float* vectors, int64_t n) {
 int px_flat_search(const px_flat* cf, const float* queries, int64_t nq, int64_t k,
                    const uint8_t* mask, int64_t* out_ids, float* out_dists) {
     PX_TRY(check_search_args(cf, queries, nq, k, out_ids, out_dists));
-    // crates/py/src/lib.rs:127-128 validates the queries before the k == 0 early return
-    if (queries && !all_finite(queries, nq * cf->dim))
-        return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
-    if (k == 0 || nq == 0) return PX_OK;
+    // crates/py/src/lib.rs:127-128 validates the queries before the k == 0 early return (a
+    // search proper checks them in flat_search_host, in the same pass as their fp16 test)
+    if (k == 0 || nq == 0) {
+        if (queries && !all_finite(queries, nq * cf->dim))
+            return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
+        return PX_OK;
+    }
     return flat_search_host(const_cast<px_flat*>(cf), cf->metric, queries, nq, k, mask, out_ids,
                             out_dists, 0);
 }
