@@ -55,23 +55,25 @@ int fail(int code, const std::string& msg) {
     } while (0)
 
 // all_finite, and in the same pass whether every value is exactly an fp16 zero or normal
-// number (*f16_exact): zero, or an exponent in fp16's normal range (2^-14 .. 2^15) with the
-// 13 low mantissa bits clear -- what to_f16_kernel checks on the device.
+// number (*f16_exact): zero, or a magnitude in [2^-14, 2^16) with the 13 low mantissa bits
+// clear -- what to_f16_kernel checks on the device. About 2.5 times all_finite's cost, so
+// used on small batches only (where it spares a device read-back that costs more).
 bool finite_and_f16(const float* x, int64_t len, bool* f16_exact) {
     constexpr int64_t kBlock = 4096;
     uint32_t inexact = 0;
     for (int64_t b = 0; b < len; b += kBlock) {
         const int64_t e = std::min(len, b + kBlock);
-        uint32_t bad = 0;
+        uint32_t bad = 0, inx = 0;
         for (int64_t i = b; i < e; ++i) {
             uint32_t u;
             std::memcpy(&u, x + i, sizeof(u));
-            const uint32_t ex = (u >> 23) & 0xffu;
-            bad |= (uint32_t)(ex == 0xffu);
-            inexact |= (uint32_t)((u & 0x7fffffffu) != 0 &&
-                                  (ex < 113u || ex > 142u || (u & 0x1fffu) != 0));
+            const uint32_t a = u & 0x7fffffffu;
+            bad |= (uint32_t)(a >= 0x7f800000u);
+            inx |= (uint32_t)(a != 0) &
+                   ((uint32_t)(a - 0x38800000u >= 0x0f000000u) | (uint32_t)((a & 0x1fffu) != 0));
         }
         if (bad) return false;
+        inexact |= inx;
     }
     *f16_exact = inexact == 0;
     return true;
@@ -553,7 +555,8 @@ struct px_flat {
     bool scan_f16 = true;          // px_flat_set_scan_f16
     bool last_f16 = false;         // the last search read d_xh (px_flat_last_scan_f16)
     int q_f16 = -1;                // host-array search in progress: its queries are exact in
-                                   // fp16 (1) or not (0), checked on the host; -1: unknown
+                                   // fp16 (1) or not (0), checked on the host (batches of at
+                                   // most 65,536 values); -1: unknown
     Workspace ws;
     Timing timing;
     int last_path = PX_PATH_LISTS; // selection path of the last search
@@ -1517,8 +1520,12 @@ int check_search_args(const void* idx, const void* queries, int64_t nq, int64_t 
 // Host-pointer search: upload, run, download.
 int flat_search_host(px_flat* f, int metric, const float* queries, int64_t nq, int64_t k,
                      const uint8_t* mask, int64_t* out_ids, float* out_d, int raw_keys) {
+    // small batches test fp16 exactness in the finiteness pass (a few microseconds), sparing
+    // the fp16 scans' device read-back; on large ones that pass would cost more than it
     bool f16_exact = false;
-    if (!finite_and_f16(queries, nq * f->dim, &f16_exact))
+    const bool small = nq * f->dim <= 65536;
+    if (!(small ? finite_and_f16(queries, nq * f->dim, &f16_exact)
+                : all_finite(queries, nq * f->dim)))
         return fail(PX_ERR_NONFINITE, "query must not contain NaN or infinite values");
     std::lock_guard<std::mutex> lock(f->mu);
     f->smetric = metric;
@@ -1527,7 +1534,7 @@ int flat_search_host(px_flat* f, int metric, const float* queries, int64_t nq, i
         px_flat* f;
         ~HintReset() { f->q_f16 = -1; }
     } hint_reset{f};
-    f->q_f16 = f16_exact ? 1 : 0;
+    f->q_f16 = small ? (f16_exact ? 1 : 0) : -1;
     if (f->n == 0) {
         host_padding(metric, nq, k, out_ids, out_d, raw_keys);
         return PX_OK;
