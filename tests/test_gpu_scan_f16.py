@@ -342,3 +342,60 @@ def test_padded_dims_and_large_integers(gpu):
         assert info["scan_f16"]
         o_ids, o_d, _ = oracle.flat_search(big, qb, 50, metric)
         assert_parity(ids, d, o_ids, o_d, _key_of(big, qb, metric))
+
+
+# values at the edges of "exact in fp16" (zero, or a normal fp16 number: magnitude in
+# [2^-14, 65504] with at most 11 significant bits), and just past them
+_EDGE_EXACT = {
+    "-0.0": -0.0,
+    "2^-14, the smallest normal": 2.0 ** -14,
+    "2^-14 (1 + 2^-10), its last significant bit": 2.0 ** -14 * (1 + 2.0 ** -10),
+    "65504, the largest": 65504.0,
+    "-65504": -65504.0,
+}
+_EDGE_INEXACT = {
+    "1 + 2^-11, twelve significant bits": 1 + 2.0 ** -11,
+    "65520, rounds past 65504": 65520.0,
+    "65536 = 2^16": 65536.0,
+    "2^-15, an fp16 subnormal": 2.0 ** -15,
+}
+
+
+def test_exactness_edges(gpu):
+    edges = {**_EDGE_EXACT, **_EDGE_INEXACT}
+    # the table itself against numpy's fp16: round trip, and not subnormal
+    for name, v in edges.items():
+        v32 = np.float32(v)
+        with np.errstate(over="ignore"):  # 65520 and 65536 become fp16 infinities
+            r = np.float16(v32).astype(np.float32)
+        fits = bool(r == v32) and (v32 == 0 or abs(v32) >= 2.0 ** -14)
+        assert fits == (name in _EDGE_EXACT), name
+    rng = np.random.default_rng(851)
+    base = rng.integers(0, 256, size=(40_000, 128)).astype(np.float32)
+    q = rng.integers(0, 256, size=(1000, 128)).astype(np.float32)
+    k = 100
+    # one edge value in one row of an integer corpus (the copy is made on the device)
+    for name, v in edges.items():
+        data = base.copy()
+        data[17, 3] = v
+        idx = _index(data, oracle.L2)
+        ids, d, info = _run(idx, q[:400], k)
+        print(f"case row edge {name}: path {info['path']}, f16 {info['scan_f16']}", flush=True)
+        assert info["path"].startswith("collect")
+        assert info["scan_f16"] == (name in _EDGE_EXACT), name
+        o_ids, o_d, _ = oracle.flat_search(data, q[:400], k, oracle.L2)
+        assert_parity(ids, d, o_ids, o_d, _key_of(data, q[:400], oracle.L2))
+    # one edge value in the last query of a batch: 400 x 128 values are tested on the
+    # host, 1000 x 128 on the device
+    idx = _index(base, oracle.L2)
+    for nq in (400, 1000):
+        for name, v in edges.items():
+            qq = q[:nq].copy()
+            qq[nq - 1, 5] = v
+            ids, d, info = _run(idx, qq, k)
+            print(f"case query edge {name}, nq={nq}: path {info['path']}, f16 {info['scan_f16']}",
+                  flush=True)
+            assert info["path"].startswith("collect")
+            assert info["scan_f16"] == (name in _EDGE_EXACT), (name, nq)
+            o_ids, o_d, _ = oracle.flat_search(base, qq, k, oracle.L2)
+            assert_parity(ids, d, o_ids, o_d, _key_of(base, qq, oracle.L2))
