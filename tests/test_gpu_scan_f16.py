@@ -399,3 +399,49 @@ def test_exactness_edges(gpu):
             assert info["scan_f16"] == (name in _EDGE_EXACT), (name, nq)
             o_ids, o_d, _ = oracle.flat_search(base, qq, k, oracle.L2)
             assert_parity(ids, d, o_ids, o_d, _key_of(base, qq, oracle.L2))
+
+
+def test_exactness_edges_on_the_lists(gpu):
+    # the per-split lists (200 queries, k = 10, 80,000 rows): host arrays are tested on the
+    # host, the device form by the lists' own pass (finiteness and fp16 exactness in one
+    # read-back)
+    import ctypes
+    from proxima_amd import _lib
+    lib = _lib.load()
+    nq, k = 200, 10
+    data = datagen.sift_like(80_000, 128, 861)
+    q = datagen.sift_like(nq, 128, 862)
+    idx = _index(data, oracle.L2)
+    ptrs = []
+
+    def dev(arr):
+        p = ctypes.c_void_p()
+        assert lib.px_dev_alloc(ctypes.byref(p), max(arr.nbytes, 1)) == 0
+        ptrs.append(p)
+        assert lib.px_dev_upload(p, arr.ctypes.data, arr.nbytes) == 0
+        return p
+
+    try:
+        di = dev(np.zeros((nq, k), dtype=np.int64))
+        dd = dev(np.zeros((nq, k), dtype=np.float32))
+        for name, v in {**_EDGE_EXACT, **_EDGE_INEXACT}.items():
+            qq = q.copy()
+            qq[nq - 1, 9] = v
+            o_ids, o_d, _ = oracle.flat_search(data, qq, k, oracle.L2)
+            ids, d, info = _run(idx, qq, k)
+            print(f"case lists query edge {name}: host f16 {info['scan_f16']}", flush=True)
+            assert info["path"] == "lists" and info["scan_f16"] == (name in _EDGE_EXACT), name
+            assert_parity(ids, d, o_ids, o_d, _key_of(data, qq, oracle.L2))
+            rc = lib.px_flat_search_device(idx._h, dev(qq), nq, k, None, di, dd)
+            assert rc == 0, _lib.last_error()
+            info = idx._last_timing()
+            print(f"  device form f16 {info['scan_f16']}", flush=True)
+            assert info["path"] == "lists" and info["scan_f16"] == (name in _EDGE_EXACT), name
+            ids = np.empty((nq, k), dtype=np.int64)
+            d = np.empty((nq, k), dtype=np.float32)
+            assert lib.px_dev_download(ids.ctypes.data, di, ids.nbytes) == 0
+            assert lib.px_dev_download(d.ctypes.data, dd, d.nbytes) == 0
+            assert_parity(ids, d, o_ids, o_d, _key_of(data, qq, oracle.L2))
+    finally:
+        for p in ptrs:
+            lib.px_dev_free(p)
