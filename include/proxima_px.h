@@ -37,8 +37,9 @@ extern "C" {
 #define PX_ERR_ARG (-5)        /* null handle/pointer, negative size, bad metric or params */
 #define PX_ERR_UNTRAINED (-6)  /* PQ index used before train (crates/py/src/lib.rs:492-504) */
 #define PX_ERR_DEVICE (-7)     /* no usable gfx950 device, or a device-side failure of the search
-                                  (a collect scan whose workgroup stage sync gave up: no
-                                  results; px_last_error names it) */
+                                  (a collect or list scan whose workgroup stage sync gave
+                                  up: no results, the outputs unwritten; px_last_error
+                                  names it) */
 
 /* Largest k of the reference's GPU seam (knn_gpu_search). px_flat_search* and
  * px_pq_search* take any k >= 0, as the reference's FlatIndex and PqIndex do
@@ -218,6 +219,13 @@ int px_flat_set_scan_f16(px_flat* idx, int enable);
 /* *used = 1 if the handle's last search read the fp16 copy of the rows (either scan), else
  * 0. */
 int px_flat_last_scan_f16(const px_flat* idx, int* used);
+/* Polls a stage-sync wait of the barrier-free scans (the collect scans; lists of k + 8 <= 32)
+ * makes before it gives up; 0 (the default) keeps the kernels' own, 2^16 polls, about 5 ms.
+ * A wait that gives up lets its wave go on (every kernel still ends) and is reported: the
+ * merge or select writes nothing and the search fails with PX_ERR_DEVICE, its outputs
+ * unwritten. A handle's later searches are unaffected. Test hook (a small limit forces the
+ * give-up); no counterpart in the reference. */
+int px_flat_set_spin_limit(px_flat* idx, int polls);
 /* The same for PqIndex searches (k <= 128: per-wave lists; above: threshold-collect). */
 int px_pq_last_rounds(const px_pq* idx, int* rounds);
 int px_pq_set_timing(px_pq* idx, int enable);

@@ -8,7 +8,10 @@ the line-by-line map and the canonical (key, id) tie order).
 Parity status of every function: pinned (tests/test_oracle.py) by the reference's known
 answers and structural tests, numpy float64 brute force, integer-exact closed forms
 (sums below 2^24 are exact in any order), hand-computed lane orders, and for PQ training
-by an independent pure-Python restatement on tiny inputs. The one detail no check can pin
+by hand-derived known answers (the reciprocal-multiply mean of pq.rs:185-188 and the
+empty-cluster re-seed of pq.rs:180-183 from published SplitMix64 draws), the Lloyd-step
+invariant, distinct-row initialisation and bit equality with the product's own trainer
+(tests/test_oracle.py). The one detail no check can pin
 -- which of several exactly equal keys Rust's BinaryHeap keeps at the k-boundary -- is
 exempt under the parity rule (exact ties differ by 0 < 1e-5 relative).
 """

@@ -272,6 +272,12 @@ class FlatIndex:
         off keeps both on the fp32 rows. Diagnostic; no counterpart in the reference."""
         _check(self._lib.px_flat_set_scan_f16(self._h, 1 if enable else 0))
 
+    def _spin_limit(self, polls: int = 0) -> None:
+        """Polls a stage-sync wait of the barrier-free scans makes before it gives up (0: the
+        kernels' own, about 5 ms). A give-up fails the search with RuntimeError and writes no
+        outputs. Test hook; no counterpart in the reference."""
+        _check(self._lib.px_flat_set_spin_limit(self._h, int(polls)))
+
     def _last_timing(self) -> dict:
         scan, total = ctypes.c_float(), ctypes.c_float()
         splits, blocks = ctypes.c_int(), ctypes.c_int()

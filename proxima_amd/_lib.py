@@ -80,6 +80,7 @@ SIGNATURES = {
     "px_flat_last_path": (c_int, [c_void_p, POINTER(c_int)]),
     "px_flat_set_scan_f16": (c_int, [c_void_p, c_int]),
     "px_flat_last_scan_f16": (c_int, [c_void_p, POINTER(c_int)]),
+    "px_flat_set_spin_limit": (c_int, [c_void_p, c_int]),
     "px_pq_last_rounds": (c_int, [c_void_p, POINTER(c_int)]),
     "px_hip_versions": (c_int, [POINTER(c_int), POINTER(c_int)]),
     "px_pq_set_timing": (c_int, [c_void_p, c_int]),

@@ -183,14 +183,15 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     // s waits until every wave has committed stage s + 1 (acquire loads) before it reads
     // stage s + 1's buffer and writes stage s + 2's. A wave commits stage s + 1 only after
     // all its reads of stage s - 1, whose buffer and norm slot the writes of stage s + 2
-    // reuse, so the one wait covers both. A wait gives up after kSpinLimit polls (about
-    // 5 ms) and reports it (a.spin_fail), so that a wave always finishes.
+    // reuse, so the one wait covers both. A wait gives up after a.spin_limit polls
+    // (kSpinLimit, about 5 ms, unless a test lowers it) and reports it (a.spin_fail), so
+    // that a wave always finishes.
     auto publish = [&](int v) __attribute__((always_inline)) {
         stage_publish(committed, wave, lane, v);
     };
     const unsigned caddr = (unsigned)(uintptr_t)(committed + (lane & 7));
     auto wait_committed = [&](int ct) __attribute__((always_inline)) {
-        if (stage_wait(caddr, ct) >= kSpinLimit && a.spin_fail && lane == 0)
+        if (stage_wait(caddr, ct, a.spin_limit) >= a.spin_limit && a.spin_fail && lane == 0)
             atomicOr(a.spin_fail, 1);
     };
 
@@ -567,14 +568,15 @@ hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s) {
     if (dyn && a.dense) return hipErrorInvalidValue;
     if ((a.corpus_h == nullptr) != (a.queries_h == nullptr)) return hipErrorInvalidValue;
     const bool h16 = a.corpus_h != nullptr;
+    const FlatScanArgs b = with_spin_limit(a);
 #define PX_COLLECT(L2, FILT, DYN)                                                              \
     do {                                                                                       \
         if (h16)                                                                               \
             hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true, true>), grid,   \
-                               block, 0, s, a);                                                \
+                               block, 0, s, b);                                                \
         else                                                                                   \
             hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true, false>), grid,  \
-                               block, 0, s, a);                                                \
+                               block, 0, s, b);                                                \
     } while (0)
     if (a.metric == 0) {
         if (a.rowidx) {

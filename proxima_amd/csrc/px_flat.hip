@@ -445,7 +445,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     next_stage(c2, t2, c3, t3);
                     fetch(c2);
                     tile_ids(t3);
-                    if (stage_wait(caddr, (int)(s + 1)) >= kSpinLimit && a.spin_fail && lane == 0)
+                    if (stage_wait(caddr, (int)(s + 1), a.spin_limit) >= a.spin_limit &&
+                        a.spin_fail && lane == 0)
                         atomicOr(a.spin_fail, 1);
                     commit(rb == 0 ? 2 : rb - 1, c2, (int)(t2 & (kNorms - 1)));
                     stage_publish(committed, wave, lane, (int)(s + 2));
@@ -734,7 +735,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         if constexpr (RELAXED) {
             // every wave has committed stage s + 1 (so none still reads stage s - 1, whose
             // buffer and norm slot stage s + 2 takes), then this wave's part of stage s + 2
-            if (stage_wait(caddr, (int)(s + 1)) >= kSpinLimit && a.spin_fail && lane == 0)
+            if (stage_wait(caddr, (int)(s + 1), a.spin_limit) >= a.spin_limit && a.spin_fail &&
+                lane == 0)
                 atomicOr(a.spin_fail, 1);
             pair_priority(__hip_atomic_load(committed + (wave ^ 4), __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_WORKGROUP),
@@ -817,7 +819,8 @@ static hipError_t launch_scan_t(const FlatScanArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s) {
+hipError_t launch_flat_scan(const FlatScanArgs& a0, hipStream_t s) {
+    const FlatScanArgs a = with_spin_limit(a0);
     switch (flat_list_capacity(a.kl)) {
         case 32: return launch_scan_t<32, flat_waves(32)>(a, s);
         case 56: return launch_scan_t<56, flat_waves(56)>(a, s);
@@ -1003,7 +1006,8 @@ hipError_t launch_flat_vcollect(const FlatScanArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_flat_collect_v1(const FlatScanArgs& a, hipStream_t s) {
+hipError_t launch_flat_collect_v1(const FlatScanArgs& a0, hipStream_t s) {
+    const FlatScanArgs a = with_spin_limit(a0);
     constexpr int kWaves = 8;
     const int64_t qtiles = (a.nq + 32 * kWaves - 1) / (32 * kWaves);
     const bool multi = a.dp > kChunk;
@@ -1140,10 +1144,14 @@ constexpr int kMergeFiltered = 256;
 // tail can be among the best kl. PQ lists publish no bounds; their kl-th smallest list
 // head serves instead.
 __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
-    if (a.abort) {
-        const int v = *a.abort;
-        if (a.verdict && blockIdx.x == 0 && threadIdx.x == 0) *a.verdict = v;
-        if (v == a.abort_seq) return;
+    if (a.abort || a.spin_fail) {
+        const int v = a.abort ? *a.abort : 0;
+        const int sf = a.spin_fail ? *a.spin_fail : 0;
+        if (a.verdict && blockIdx.x == 0 && threadIdx.x == 0) {
+            a.verdict[0] = v;
+            a.verdict[1] = sf;
+        }
+        if ((a.abort && v == a.abort_seq) || sf) return;
     }
     extern __shared__ __attribute__((aligned(16))) char msmem[];
     __shared__ int s_n;
@@ -1312,6 +1320,7 @@ hipError_t launch_merge(const MergeArgs& a, hipStream_t s) {
 //   holds (at least kk + 1 of them: the threshold drops below at least one candidate, and
 //   at least kk rows stay at or below it).
 __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelectArgs a) {
+    if (a.spin_fail && *a.spin_fail) return;
     extern __shared__ __attribute__((aligned(16))) char csmem[];
     float* sk = reinterpret_cast<float*>(csmem);
     int* si = reinterpret_cast<int*>(sk + a.lcap);
@@ -1824,9 +1833,10 @@ hipError_t launch_to_f16(const float* x, int64_t count, unsigned short* out, int
 __global__ __launch_bounds__(256) void list_prologue_kernel(const float* x, int64_t count,
                                                             int* flag, int seq, int* gtau,
                                                             int64_t ngtau, int* gbest,
-                                                            int64_t ngbest) {
+                                                            int64_t ngbest, int* zero) {
     const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    if (zero && i0 == 0) *zero = 0;
     bool bad = false;
     for (int64_t i = i0; i < count; i += step)
         bad |= (__float_as_uint(x[i]) & 0x7f800000u) == 0x7f800000u;
@@ -1836,11 +1846,13 @@ __global__ __launch_bounds__(256) void list_prologue_kernel(const float* x, int6
 }
 
 hipError_t launch_list_prologue(const float* x, int64_t count, int* flag, int seq, int* gtau,
-                                int64_t ngtau, int* gbest, int64_t ngbest, hipStream_t s) {
+                                int64_t ngtau, int* gbest, int64_t ngbest, int* zero,
+                                hipStream_t s) {
+    if (count > 0 && !flag) return hipErrorInvalidValue;
     const int64_t most = std::max<int64_t>({count, ngtau, ngbest, (int64_t)1});
     const int64_t blocks = std::min<int64_t>((most + 255) / 256, 2048);
     hipLaunchKernelGGL(list_prologue_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, count,
-                       flag, seq, gtau, ngtau, gbest, ngbest);
+                       flag, seq, gtau, ngtau, gbest, ngbest, zero);
     return hipGetLastError();
 }
 

@@ -217,6 +217,7 @@ struct Workspace {
     DevBuf cand_d;           // smallest dropped key of each overflowing region
     DevBuf qh;               // a batch's queries as fp16 (the fp16 scans; px_flat::d_xh)
     DevBuf fflag;            // finiteness verdicts of list-path searches (next_finite_seq)
+    DevBuf spinw;            // the list scans' stage-sync give-up word (FlatScanArgs::spin_fail)
     int fseq = 0;
     DevBuf dbgw;             // debug build: the debug word of the kernels' index checks ...
     int* dbg = nullptr;      // ... while a search runs (null in the product build)
@@ -225,7 +226,7 @@ struct Workspace {
     // Read-backs of the search path (pinned, mapped, coherent): written by a kernel
     // (launch_copy_to_host) through their device addresses *_dev, read by the host after
     // the stream drains
-    int* h_count = nullptr;      // one int
+    int* h_count = nullptr;      // two ints (one read-back, or a merge's two verdicts)
     int* h_count_dev = nullptr;
     int* h_status = nullptr;     // h_status_cap ints
     int* h_status_dev = nullptr;
@@ -257,7 +258,7 @@ struct Workspace {
         return PX_OK;
     }
     int ensure_pinned() {
-        if (!h_count) PX_TRY(mapped_ints(&h_count, &h_count_dev, 1));
+        if (!h_count) PX_TRY(mapped_ints(&h_count, &h_count_dev, 2));
         return PX_OK;
     }
     int ensure_status(int64_t n) {
@@ -274,7 +275,7 @@ struct Workspace {
                           &out_d, &gtau, &gbest, &thr_k, &thr_p, &lad_k, &lad_p, &rung, &status,
                           &cand_k, &cand_p, &cand_n, &cand_d, &qh, &samp_row, &qlist,
                           &sort_scratch,
-                          &fflag,
+                          &fflag, &spinw,
                           &dbgw})
             b->release();
         fseq = 0;
@@ -553,6 +554,8 @@ struct px_flat {
     unsigned short* d_xh = nullptr;
     bool xh_exact = true;
     bool scan_f16 = true;          // px_flat_set_scan_f16
+    int spin_limit = 0;            // stage-sync polls before a give-up, 0: the kernels' own
+                                   // (px_flat_set_spin_limit; FlatScanArgs::spin_limit)
     bool last_f16 = false;         // the last search read d_xh (px_flat_last_scan_f16)
     int q_f16 = -1;                // host-array search in progress: its queries are exact in
                                    // fp16 (1) or not (0), checked on the host (batches of at
@@ -603,12 +606,23 @@ int flat_sync(px_flat* f) {
     const int64_t need = f->d_rows + add;
     if (need > f->d_cap) {
         const int64_t cap = std::max<int64_t>({need, f->d_cap * 2, 1024});
-        float *nx = nullptr, *nn = nullptr;
+        // the new buffers, freed on every early return below (the index keeps its old ones)
+        // unless they have been adopted
+        struct Fresh {
+            float* x = nullptr;
+            float* n = nullptr;
+            unsigned short* h = nullptr;
+            ~Fresh() {
+                dev_free(x);
+                dev_free(n);
+                dev_free(h);
+            }
+        } fresh;
+        float*& nx = fresh.x;
+        float*& nn = fresh.n;
         PX_HIP(dev_malloc(&nx, sizeof(float) * cap * f->dp));
-        if (dev_malloc(&nn, sizeof(float) * cap) != hipSuccess) {
-            dev_free(nx);
+        if (dev_malloc(&nn, sizeof(float) * cap) != hipSuccess)
             return fail(hipErrorOutOfMemory, "device allocation of the corpus norms failed");
-        }
         if (f->d_rows) {
             PX_HIP(hipMemcpyAsync(nx, f->d_x, sizeof(float) * f->d_rows * f->dp,
                                   hipMemcpyDeviceToDevice, f->stream));
@@ -616,7 +630,7 @@ int flat_sync(px_flat* f) {
                                   hipMemcpyDeviceToDevice, f->stream));
         }
         // the fp16 mirror grows with them, or is dropped if its memory cannot be had
-        unsigned short* nxh = nullptr;
+        unsigned short*& nxh = fresh.h;
         if (f->dp == 128 && f->xh_exact) {
             if (dev_malloc(&nxh, sizeof(unsigned short) * cap * 128) != hipSuccess) {
                 (void)hipGetLastError();
@@ -635,6 +649,8 @@ int flat_sync(px_flat* f) {
         f->d_norm = nn;
         f->d_xh = nxh;
         f->d_cap = cap;
+        fresh.x = fresh.n = nullptr;  // adopted
+        fresh.h = nullptr;
     }
     float* dst = f->d_x + f->d_rows * f->dp;
     if (f->dp == f->dim) {
@@ -880,6 +896,8 @@ int run_collect(CollectJob& j) {
             c.kk = (int)kk;
             c.gbest = j.sel_gbest;
             c.cand_dmin = j.sel_dmin;
+            // a scan's stage sync that gave up (status[nq]): the select writes nothing
+            c.spin_fail = ws.status.as<int>() + nq;
             PX_HIP(px::launch_collect_select(c, (int)take, s));
             if (round == 0 && j.timing->enabled) PX_HIP(hipEventRecord(j.timing->ev[2], s));
             done += take;
@@ -1100,6 +1118,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.dense = 1;
         a.dense_ld = ld;
         a.spin_fail = ws.status.as<int>() + nq;
+        a.spin_limit = f->spin_limit;
         a.corpus_h = qh ? f->d_xh : nullptr;
         a.queries_h = qh;
         a.xcd_major = xcd_major_for(a, 256, std::max(f->dev.cus, 1));
@@ -1208,6 +1227,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         a.cand_dmin = keeps_dmin ? ws.cand_d.as<int>() : nullptr;
         j.sel_dmin = a.cand_dmin;
         a.spin_fail = ws.status.as<int>() + j.nq;
+        a.spin_limit = f->spin_limit;
         a.corpus_h = qh ? f->d_xh : nullptr;
         a.queries_h = qh;
         // the shared bound needs k' publishing slots (one per split, at most 32); it is
@@ -1308,12 +1328,18 @@ int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_
 }
 
 // Device buffers of a list scan: split lists [nq][splits][kl] (key, position), the shared
-// bounds gtau [nq] and gbest [nq][32] (cleared here by fill kernels).
+// bounds gtau [nq] and gbest [nq][32] and the scan's stage-sync give-up word spin (all
+// cleared by the list prologue); verdict_h / verdict_dev: two mapped host ints where the
+// merge stores the search's finiteness and give-up verdicts, or null (no pinned memory: the
+// give-up word is read back by a copy).
 struct ListBufs {
     float* part_k;
     int* part_i;
     int* gtau;
     int* gbest;
+    int* spin;
+    int* verdict_h;
+    int* verdict_dev;
 };
 
 // The per-split list path: fused MFMA scan with per-split lists, then the merge (re-rank in
@@ -1328,16 +1354,13 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     const int splits = lp.splits;
     const int64_t rps = lp.rps, groups = lp.groups;
     int seq = 0;
-    const int* d_flag = nullptr;
+    int* d_flag = nullptr;
     if (chk) {
         PX_TRY(next_finite_seq(f->ws, s, &seq));
         d_flag = f->ws.fflag.as<int>();
-        PX_HIP(px::launch_list_prologue(chk->x, chk->count, f->ws.fflag.as<int>(), seq, b.gtau,
-                                        nq, b.gbest, nq * 32, s));
-    } else {
-        PX_HIP(px::launch_fill_int(b.gtau, nq, px::kTotalKeyInf, s));
-        PX_HIP(px::launch_fill_int(b.gbest, nq * 32, px::kTotalKeyInf, s));
     }
+    PX_HIP(px::launch_list_prologue(chk ? chk->x : nullptr, chk ? chk->count : 0, d_flag, seq,
+                                    b.gtau, nq, b.gbest, nq * 32, b.spin, s));
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[0], s));
 
     px::FlatScanArgs a{};
@@ -1360,6 +1383,8 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     a.gbest = b.gbest;
     a.abort = d_flag;
     a.abort_seq = seq;
+    a.spin_fail = b.spin;
+    a.spin_limit = f->spin_limit;
     a.xcd_major = xcd_major_for(a, px::flat_queries_per_block(kl), std::max(f->dev.cus, 1));
     a.corpus_h = qh ? f->d_xh : nullptr;
     a.queries_h = qh;
@@ -1389,11 +1414,22 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     mg.raw_keys = raw_keys;
     mg.abort = d_flag;
     mg.abort_seq = seq;
-    mg.verdict = d_flag ? f->ws.h_count_dev : nullptr;
+    mg.spin_fail = b.spin;
+    mg.verdict = b.verdict_dev;
     PX_HIP(px::launch_merge(mg, s));
     if (timed) PX_HIP(hipEventRecord(f->timing.ev[2], s));
     PX_HIP(hipStreamSynchronize(s));
-    if (d_flag && *f->ws.h_count == seq) return nonfinite_error();
+    // a failed check made the scan and merge no-ops; a stage wait that gave up, the merge
+    int gave_up = 0;
+    if (b.verdict_h) {
+        if (d_flag && b.verdict_h[0] == seq) return nonfinite_error();
+        gave_up = b.verdict_h[1];
+    } else {
+        if (d_flag) return fail(PX_ERR_ARG, "internal: a pending check needs the verdicts");
+        PX_TRY(read_back_int(b.spin, &gave_up, nullptr, s));
+    }
+    if (gave_up)
+        return fail(PX_ERR_DEVICE, "a list scan's stage sync timed out (no results)");
     if (timed) {
         PX_HIP(hipEventElapsedTime(&f->timing.scan_ms, f->timing.ev[0], f->timing.ev[1]));
         PX_HIP(hipEventElapsedTime(&f->timing.total_ms, f->timing.ev[0], f->timing.ev[2]));
@@ -1494,8 +1530,12 @@ int flat_run_paths(px_flat* f, const float* d_q, int64_t nq, int64_t k, const ui
     PX_TRY(ws.part_i.reserve(sizeof(int) * nq * lp.splits * kl));
     PX_TRY(ws.gtau.reserve(sizeof(int) * nq));
     PX_TRY(ws.gbest.reserve(sizeof(int) * nq * 32));
+    PX_TRY(ws.spinw.reserve(sizeof(int)));
+    PX_TRY(ws.ensure_pinned());
     PX_TRY(f->timing.ensure());
-    ListBufs b{ws.part_k.as<float>(), ws.part_i.as<int>(), ws.gtau.as<int>(), ws.gbest.as<int>()};
+    ListBufs b{ws.part_k.as<float>(), ws.part_i.as<int>(), ws.gtau.as<int>(),
+               ws.gbest.as<int>(),    ws.spinw.as<int>(),  ws.h_count,
+               ws.h_count_dev};
     return flat_run_lists(f, d_q, nq, k, n_eff, rowidx, lp, kl, b, d_ids, d_out, raw_keys,
                           f->timing.enabled, chk, qh);
 }
@@ -2096,7 +2136,7 @@ int px_flat_search_device_noalloc(const px_flat* cf, const float* d_queries, int
     // the fixed pieces, then the split lists in what remains
     auto fixed = [&](ScratchLayout& L, int** flag, float** q, int** rowidx, int** cscr,
                      int** gtau, int** gbest) {
-        *flag = L.take<int>(2);
+        *flag = L.take<int>(3);  // finiteness, kept count, the scan's give-up word
         *q = pad ? L.take<float>((size_t)(nq * f->dp)) : nullptr;
         *rowidx = masked ? L.take<int>((size_t)n) : nullptr;
         *cscr = masked ? L.take<int>((size_t)px::mask_compact_scratch(n)) : nullptr;
@@ -2130,7 +2170,8 @@ int px_flat_search_device_noalloc(const px_flat* cf, const float* d_queries, int
         PX_TRY(compact_mask_into(d_mask, n, rowidx, cscr, flag + 1, &h, nullptr, s, &n_eff));
     ListPlan lp;
     PX_TRY(plan_list_scan(n_eff, nq, kl, f->dev.cus, &lp, k, max_splits));
-    ListBufs b{L.take<float>((size_t)(nq * lp.splits * kl)), nullptr, gtau, gbest};
+    ListBufs b{L.take<float>((size_t)(nq * lp.splits * kl)), nullptr, gtau, gbest, flag + 2,
+               nullptr, nullptr};
     b.part_i = L.take<int>((size_t)(nq * lp.splits * kl));
     if (L.used > kNoAllocScratchBytes)
         return fail(PX_ERR_ARG, "internal: scratch layout past its end");  // unreachable
@@ -2210,6 +2251,14 @@ int px_flat_set_scan_f16(px_flat* f, int enable) {
     if (!f) return fail(PX_ERR_ARG, "null index handle");
     std::lock_guard<std::mutex> lock(f->mu);
     f->scan_f16 = enable != 0;
+    return PX_OK;
+}
+
+int px_flat_set_spin_limit(px_flat* f, int polls) {
+    if (!f) return fail(PX_ERR_ARG, "null index handle");
+    if (polls < 0) return fail(PX_ERR_ARG, "spin limit must be >= 0");
+    std::lock_guard<std::mutex> lock(f->mu);
+    f->spin_limit = polls;
     return PX_OK;
 }
 

@@ -66,9 +66,13 @@ struct FlatScanArgs {
     // rows of several 128-dim chunks over several rounds of workgroups: XCD-major block order
     // (flat_scan_kernel), the grid padded to a multiple of 8
     int xcd_major;
-    // optional (launch_flat_collect, 128-dim rows): set nonzero if a stage-sync wait of the
-    // scan gave up (a bug: the results of that launch are not to be used)
+    // optional: set nonzero if a stage-sync wait of the scan gave up (the barrier-free
+    // scans: collect mode, the collect scan of 128-dim rows, lists of 32); the results of
+    // that launch are not to be used, and the merge or select after it writes nothing
     int* spin_fail;
+    // polls before a stage-sync wait gives up; 0: kSpinLimit (about 5 ms). Tests lower it
+    // to force a give-up (px_flat_set_spin_limit)
+    int spin_limit;
     // optional (launch_flat_collect, 128-dim rows), both or neither: the corpus [n][128] and
     // the queries [nq][128] as fp16 bit patterns, given only when every value of both is
     // exactly representable in fp16; the scan then multiplies in fp16 (exact products,
@@ -140,6 +144,9 @@ struct CollectSelectArgs {
     float* out_dists;
     int raw_keys;
     int* dbg;                // debug build: as FlatScanArgs::dbg
+    // optional: the scan's FlatScanArgs::spin_fail; nonzero, the launch writes nothing (no
+    // outputs, no status words: the host fails the search)
+    const int* spin_fail;
 };
 hipError_t launch_collect_select(const CollectSelectArgs& a, int slots, hipStream_t s);
 // Threshold ladder from the dense keys of a collect scan over a row sample: per query,
@@ -204,8 +211,11 @@ struct MergeArgs {
     int raw_keys;            // 1: write raw keys (FLT_MAX padding) instead of distances
     const int* abort;        // optional, as FlatScanArgs::abort: equal to abort_seq, nothing
     int abort_seq;           // is written
-    // optional (with abort): workgroup 0 stores *abort here (a mapped host int's device
-    // address), so the host reads the search's finiteness verdict with no copy of its own
+    // optional: the scan's FlatScanArgs::spin_fail; nonzero, nothing is written either
+    const int* spin_fail;
+    // optional: workgroup 0 stores *abort (0 without abort) to verdict[0] and *spin_fail (0
+    // without it) to verdict[1] (two mapped host ints' device address), so the host reads
+    // the search's finiteness and stage-sync verdicts with no copy of its own
     int* verdict;
     int* dbg;                // debug build: as FlatScanArgs::dbg
 };
@@ -223,11 +233,13 @@ hipError_t launch_nonfinite_check(const float* x, int64_t count, int* flag, hipS
 hipError_t launch_to_f16(const float* x, int64_t count, unsigned short* out, int* inexact,
                          hipStream_t s, int bit = 1);
 // The per-split list path's first kernel: *flag = max(*flag, seq) when any of count floats
-// of x is NaN or infinite (flag is never cleared: each search takes a larger seq), and
-// gtau[0..ngtau) and gbest[0..ngbest) filled with kTotalKeyInf. One launch where a flag
-// fill, the check and two fills took four.
+// of x is NaN or infinite (flag is never cleared: each search takes a larger seq; count 0:
+// no check, flag may be null), gtau[0..ngtau) and gbest[0..ngbest) filled with
+// kTotalKeyInf, and *zero (optional: the scan's spin_fail word) cleared. One launch where a
+// flag fill, the check and three fills took five.
 hipError_t launch_list_prologue(const float* x, int64_t count, int* flag, int seq, int* gtau,
-                                int64_t ngtau, int* gbest, int64_t ngbest, hipStream_t s);
+                                int64_t ngtau, int* gbest, int64_t ngbest, int* zero,
+                                hipStream_t s);
 
 // Ordered compaction of a keep-mask (nonzero = keep) into ascending row ids.
 // scratch must hold mask_compact_scratch(n) ints; *d_count receives the kept count.

@@ -3,6 +3,7 @@
 #pragma once
 
 #include "px_device.h"
+#include "px_kernels.h"
 
 namespace px {
 
@@ -31,19 +32,27 @@ __device__ __forceinline__ f32x16 mfma4(float4 a, float4 b, f32x16 c) {
 // waits with stage_wait until every wave has committed a given stage (acquire).
 constexpr int kSpinLimit = 1 << 16;  // polls of a stage wait (each one s_sleep 1: ~5 ms)
 
+// The launch's arguments with FlatScanArgs::spin_limit in force: kSpinLimit where it is 0.
+inline FlatScanArgs with_spin_limit(const FlatScanArgs& a) {
+    FlatScanArgs b = a;
+    if (b.spin_limit <= 0) b.spin_limit = kSpinLimit;
+    return b;
+}
+
 __device__ __forceinline__ void stage_publish(int* committed, int wave, int lane, int v) {
     if (lane == 0)
         __hip_atomic_store(committed + wave, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // Polls until every word of the 8-word array is >= ct; addr: the LDS address of word
-// lane & 7. Returns the number of polls, kSpinLimit if it gave up (the caller reports it).
+// lane & 7. Gives up after lim polls (lim >= 1; FlatScanArgs::spin_limit, normally
+// kSpinLimit) and returns the number of polls: lim if it gave up (the caller reports it).
 // One asm block: as a compiled loop in the middle of an unrolled stage it split the
 // schedule and cost register spills. Its s_waitcnt makes the load acquire (LDS at workgroup
 // scope needs no more), and the "memory" clobber keeps the stage buffer accesses after it.
 // The poll count is early-clobber ("+&s"): as a plain in-out operand it may share a
 // register with an equal input (it was given ct's, and each poll then raised the target).
-__device__ __forceinline__ int stage_wait(unsigned addr, int ct) {
+__device__ __forceinline__ int stage_wait(unsigned addr, int ct, int lim) {
     int v, spins = 0;
     unsigned long long m;
     asm volatile(
@@ -60,7 +69,7 @@ __device__ __forceinline__ int stage_wait(unsigned addr, int ct) {
         "  s_branch .Lpx_poll%=\n"
         ".Lpx_done%=:\n"
         : [v] "=&v"(v), [m] "=&s"(m), [sp] "+&s"(spins)
-        : [addr] "v"(addr), [ct] "s"(ct), [lim] "s"(kSpinLimit)
+        : [addr] "v"(addr), [ct] "s"(ct), [lim] "s"(lim)
         : "memory", "scc");
     return spins;
 }

@@ -22,6 +22,12 @@ The fp16 variant of flat_collect_kernel stages two tiles at a time: its stage s 
 and during stage s a wave also reads the norms of stage s itself (tile 2s's keys, tested
 during tile 2s + 1's MFMAs), so its reads are pair slots (s - 1) % 4 and s % 4.
 
+The per-split list scan of lists of 32 (flat_scan_kernel, px_flat.hip) and that kernel's
+collect mode use the same waits in another order: stage s reads buffer s % 3 for its MFMAs
+and then, in the stage's own epilogue, the keys of tile s from norm slot s % 4 (the list
+insertions, or the keys kept for the next stage's tests); after the wait there is no read,
+only the write of stage s + 2 (the next stage's A operands are read at its start).
+
 The model runs the eight waves of a workgroup under random interleavings, with every read
 an interval that other waves' steps may fall inside, and checks that no wave waits forever,
 that every read finds the stage it expects in every wave's part, and that no write lands on
@@ -39,13 +45,17 @@ class Violation(AssertionError):
     pass
 
 
-def _wave_program(s_count, live, c_off=0, write_first=False, pairs=False):
-    """The steps of one wave: ('read'|'end'|'write'|'set'|'wait', ...) in program order."""
+def _wave_program(s_count, live, c_off=0, write_first=False, pairs=False, lists=False):
+    """The steps of one wave: ('read'|'end'|'write'|'set'|'wait', ...) in program order.
+    lists: flat_scan_kernel's order (tile s's norms read in stage s's epilogue, no read after
+    the wait)."""
     prog = []
     for s in range(s_count):
         if live:
             prog.append(("read", "buf", s % STAGE_BUFS, s))          # MFMAs of stage s
-            if s > 0:
+            if lists:
+                prog.append(("read", "norm", s % NORM_BUFS, s))      # the stage's epilogue
+            elif s > 0:
                 prog.append(("read", "norm", (s - 1) % NORM_BUFS, s - 1))
             if pairs:  # two tiles a stage: the first tile's norms, tested during the second
                 prog.append(("read", "norm", s % NORM_BUFS, s))
@@ -53,13 +63,13 @@ def _wave_program(s_count, live, c_off=0, write_first=False, pairs=False):
         if write_first:
             prog.append(("write", s + 2))
         prog.append(("wait", s + 1 + c_off))
-        if live and s + 1 < s_count:
+        if live and not lists and s + 1 < s_count:
             prog.append(("read", "buf", (s + 1) % STAGE_BUFS, s + 1))  # next A operands
             prog.append(("end",))
         if not write_first:
             prog.append(("write", s + 2))
         prog.append(("set", s + 2))
-    if live:
+    if live and not lists:
         prog.append(("read", "norm", (s_count - 1) % NORM_BUFS, s_count - 1))
         prog.append(("end",))
     return prog
@@ -118,16 +128,17 @@ def run_schedule(s_count, live_waves, seed, max_steps=10**6, **variant):
     raise Violation("no progress: a wave waits forever")
 
 
-@pytest.mark.parametrize("pairs", [False, True])
+@pytest.mark.parametrize("order", ["collect", "pairs", "lists"])
 @pytest.mark.parametrize("live_waves", [8, 2, 1])
 @pytest.mark.parametrize("stages", [1, 2, 3, 7, 24])
-def test_protocol_holds(stages, live_waves, pairs):
+def test_protocol_holds(stages, live_waves, order):
     for seed in range(60):
-        run_schedule(stages, live_waves, seed, pairs=pairs)
+        run_schedule(stages, live_waves, seed, pairs=order == "pairs", lists=order == "lists")
 
 
 @pytest.mark.parametrize("variant", [dict(c_off=-1), dict(write_first=True),
-                                     dict(c_off=-1, pairs=True), dict(write_first=True, pairs=True)])
+                                     dict(c_off=-1, pairs=True), dict(write_first=True, pairs=True),
+                                     dict(c_off=-1, lists=True), dict(write_first=True, lists=True)])
 def test_broken_variants_are_caught(variant):
     # a wait for C >= s lets a wave read stage s + 1's buffer before every wave has written
     # its part; writing stage s + 2 before the wait overwrites stage s - 1's buffer while a

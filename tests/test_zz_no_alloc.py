@@ -126,3 +126,63 @@ def test_noalloc_limits(dev):
     ids = dev.get(di, (4, 10), np.int64)
     o_ids, _, _ = oracle.flat_search(data, datagen.gaussian(4, 16, 822), 10, oracle.L2)
     assert np.array_equal(ids, o_ids)
+
+
+def test_noalloc_fresh_handle_allocates_nothing(dev):
+    # On a fresh handle (rows added, no search yet, so no workspace exists) the entry point
+    # must not need one: the library's own device allocations are capped at 1 byte
+    # (PX_DEVICE_BUDGET, checked at every allocation it makes), so any allocation on the
+    # way would fail the call. The caller's buffers (px_dev_alloc) are not counted.
+    import os
+
+    lib = dev.lib
+    data = datagen.sift_like(60_000, 128, 831)
+    q = datagen.sift_like(200, 128, 832)
+    mask = datagen.mask(60_000, 0.3, 833)
+    o = {m is not None: oracle.flat_search(data, q, 10, oracle.L2, mask=m)[:2]
+         for m in (None, mask)}
+    idx = FlatIndex(128, Metric.L2)
+    idx.add(data)
+    dq = dev.put(q)
+    dm = dev.put(mask.view(np.uint8))
+    di, dd = dev.empty(200 * 10 * 8), dev.empty(200 * 10 * 4)
+    os.environ["PX_DEVICE_BUDGET"] = "1"
+    try:
+        for m, dmask in ((False, None), (True, dm)):
+            print(f"no-alloc fresh handle under a 1-byte budget mask={m}", flush=True)
+            rc = lib.px_flat_search_device_noalloc(idx._h, dq, 200, 10, dmask, di, dd)
+            assert rc == 0, _lib.last_error()
+            ids, d = dev.get(di, (200, 10), np.int64), dev.get(dd, (200, 10), np.float32)
+            assert np.array_equal(ids, o[m][0]) and np.array_equal(d, o[m][1]), m
+        # the allocating entry point does need its workspace: refused under the same cap
+        assert lib.px_flat_search_device(idx._h, dq, 200, 10, None, di, dd) != 0
+    finally:
+        del os.environ["PX_DEVICE_BUDGET"]
+
+
+def test_noalloc_nonfinite_query(dev):
+    # same checks as px_flat_search_device (flat.rs:114-117): a NaN or infinite query value
+    # fails with PX_ERR_NONFINITE before any output is written
+    lib = dev.lib
+    data = datagen.gaussian(20_000, 64, 841)
+    q = datagen.gaussian(50, 64, 842)
+    idx = FlatIndex(64, Metric.L2)
+    idx.add(data)
+    for bad in (np.nan, np.inf, -np.inf):
+        qb = q.copy()
+        qb[17, 5] = bad
+        dq = dev.put(qb)
+        di = dev.put(np.full((50, 10), 777, dtype=np.int64))
+        dd = dev.put(np.full((50, 10), 7.5, dtype=np.float32))
+        print(f"no-alloc non-finite query value {bad}", flush=True)
+        assert lib.px_flat_search_device_noalloc(idx._h, dq, 50, 10, None, di, dd) == \
+            _lib.PX_ERR_NONFINITE
+        assert (dev.get(di, (50, 10), np.int64) == 777).all()
+        assert (dev.get(dd, (50, 10), np.float32) == 7.5).all()
+    # and the handle still serves finite queries
+    dq = dev.put(q)
+    di, dd = dev.empty(50 * 10 * 8), dev.empty(50 * 10 * 4)
+    assert lib.px_flat_search_device_noalloc(idx._h, dq, 50, 10, None, di, dd) == 0
+    o_ids, o_d, _ = oracle.flat_search(data, q, 10, oracle.L2)
+    assert_parity(dev.get(di, (50, 10), np.int64), dev.get(dd, (50, 10), np.float32), o_ids, o_d,
+                  _key_of(data, q, oracle.L2))
