@@ -98,17 +98,20 @@ def host_cpu() -> dict:
     return {"nproc": nproc, "cpu_model": model}
 
 
-def cpu_baseline(data, queries, k, metric, gpu_ids, gpu_d, budget_s, mask=None, pq=None):
+def cpu_baseline(data, queries, k, metric, gpu_ids, gpu_d, budget_s, mask=None, pq=None,
+                 warm_mt=64, warm_st=8, single=True, max_queries=None):
     """The oracle (the reference's per-query scan restated in C, one query per OpenMP task
     as rayon's par_chunks_mut in flat.rs:173-181) timed as bench/harness.py:256-265 times
     the reference: a 64-query warmup, then the median of 7 timed batches. Done twice, on all
     the host's OpenMP threads and on one thread, each within about budget_s / 2 of CPU
     time: the batch size comes from the warmup's rate. The 7 batches of each mode are
     consecutive, distinct query chunks, and every query timed is also checked against the
-    GPU's results (ids exact, distances relative)."""
+    GPU's results (ids exact, distances relative). warm_mt / warm_st: the warmups (queries);
+    single=False skips the one-thread mode; max_queries bounds the sample to the first
+    queries of the batch (a corpus too large to stream many queries through in seconds)."""
     import oracle
 
-    nq = len(queries)
+    nq = len(queries) if max_queries is None else min(len(queries), max_queries)
 
     def run(qs, threads):
         t0 = time.perf_counter()
@@ -120,10 +123,13 @@ def cpu_baseline(data, queries, k, metric, gpu_ids, gpu_d, budget_s, mask=None, 
         return time.perf_counter() - t0, r
 
     par = {"queries_checked": 0, "id_mismatches": 0, "max_rel_dist_err": 0.0}
+    seen = set()
 
     def check(rows, o_ids, o_d):
         g_ids, g_d = gpu_ids[rows], gpu_d[rows]
         par["queries_checked"] += len(rows)
+        seen.update(int(r) for r in rows)
+        par["distinct_queries"] = len(seen)
         par["id_mismatches"] += int((g_ids != o_ids).sum())
         ok = o_ids >= 0
         if ok.any():
@@ -138,11 +144,11 @@ def cpu_baseline(data, queries, k, metric, gpu_ids, gpu_d, budget_s, mask=None, 
         nxt = (nxt + size) % nq
         return rows
 
-    def mode(threads, warm):
+    def mode(threads, warm, share):
         rows = chunk(warm)
         t, _ = run(queries[rows], threads)
         per_query = t / warm
-        size = int(max(8, min(nq, (budget_s / 2.0 / 7.0) / max(per_query, 1e-9))))
+        size = int(max(8, min(nq, (budget_s * share / 7.0) / max(per_query, 1e-9))))
         times = []
         for _ in range(7):
             rows = chunk(size)
@@ -153,16 +159,21 @@ def cpu_baseline(data, queries, k, metric, gpu_ids, gpu_d, budget_s, mask=None, 
         return size / med, size, med
 
     threads = oracle.max_threads()
-    mt_qps, mt_size, mt_med = mode(threads, min(64, nq))
-    st_qps, st_size, st_med = mode(1, min(8, nq))
+    mt_qps, mt_size, mt_med = mode(threads, min(warm_mt, nq), 0.5 if single else 1.0)
     host = host_cpu()
-    return {"value": mt_qps, "unit": "queries/s", "cores": threads, "kind": "port",
-            "sample": f"median of 7 batches of {mt_size} queries ({mt_med:.2f} s each) after "
-                      f"a 64-query warmup, full corpus, {threads} OpenMP threads",
-            "single_thread": {"value": st_qps, "unit": "queries/s", "cores": 1,
-                              "sample": f"median of 7 batches of {st_size} queries "
-                                        f"({st_med:.2f} s each) after an 8-query warmup"},
-            "host": {**host, "omp_threads": threads}}, par
+    out = {"value": mt_qps, "unit": "queries/s", "cores": threads, "kind": "port",
+           "sample": f"median of 7 batches of {mt_size} queries ({mt_med:.2f} s each) after "
+                     f"a {min(warm_mt, nq)}-query warmup, full corpus, {threads} OpenMP threads"
+                     + (f", queries drawn from the first {nq} of the batch"
+                        if nq < len(queries) else ""),
+           "host": {**host, "omp_threads": threads}}
+    if single:
+        st_qps, st_size, st_med = mode(1, min(warm_st, nq), 0.5)
+        out["single_thread"] = {"value": st_qps, "unit": "queries/s", "cores": 1,
+                                "sample": f"median of 7 batches of {st_size} queries "
+                                          f"({st_med:.2f} s each) after a "
+                                          f"{min(warm_st, nq)}-query warmup"}
+    return out, par
 
 
 def read_traffic(name: str, default_workload: bool):
@@ -207,7 +218,44 @@ COUNTER_PROFILES = {
     (5, 10_000_000, 16_384, 100, "collect-sampled"):
         "flat_collect_scan_ip_10Mx384_q16k_k100_mask10_mfma_counters.md",
 }
-PQ_COUNTER_PROFILE = "pq_scan_kernel_l2_1Mx16_q10k_k10_lds_counters.md"
+# the PQ scan's (traffic, counter) summaries, unfiltered and with the 50% filter
+PQ_PROFILES = {
+    False: ("pq_scan_kernel_l2_1Mx16_q10k_k10.md", "pq_scan_kernel_l2_1Mx16_q10k_k10_lds_counters.md"),
+    True: ("pq_scan_kernel_l2_1Mx16_q10k_k10_mask50.md",
+           "pq_scan_kernel_l2_1Mx16_q10k_k10_mask50_lds_counters.md"),
+}
+
+
+# bench/harness.py:21-23: single-query latency samples and the seed of their picks
+LATENCY_SAMPLES = 10_000
+LATENCY_SEED = 20240917
+
+
+def single_query_latency(index, queries, k, samples, batch_ids):
+    """Single-query latency as bench/harness.py:238-253 measures it: `samples` calls of
+    index.search on one query each (from a numpy row: upload, search, download and the Python
+    surface's checks), the queries picked at random (seeded), each call timed on its own;
+    p50, p99 and mean in ms. One untimed call first (the handle's one-query workspace). Every
+    call's ids are compared with the batch search's afterwards."""
+    rng = np.random.default_rng(LATENCY_SEED)
+    picks = rng.integers(0, len(queries), size=samples)
+    times = np.empty(samples, dtype=np.float64)
+    got = np.empty((samples, k), dtype=np.int64)
+    index.search(queries[picks[0]], k=k)
+    for i, qi in enumerate(picks):
+        q = queries[qi]
+        t0 = time.perf_counter()
+        ids, _ = index.search(q, k=k)
+        times[i] = (time.perf_counter() - t0) * 1e3
+        got[i] = ids
+    same = bool(np.array_equal(got, batch_ids[picks]))
+    out = {"p50_ms": float(np.percentile(times, 50)), "p99_ms": float(np.percentile(times, 99)),
+           "mean_ms": float(times.mean()), "samples": int(samples), "seed": LATENCY_SEED,
+           "form": "index.search(query, k) from a numpy row, one call per query",
+           "same_ids_as_batch_search": same}
+    log(f"[bench] single-query latency over {samples} calls: p50 {out['p50_ms']:.3f} ms, "
+        f"p99 {out['p99_ms']:.3f} ms, mean {out['mean_ms']:.3f} ms, same ids {same}")
+    return out
 
 
 def host_buffer_qps(search, nq, reps=7):
@@ -231,6 +279,8 @@ TRAFFIC_PROFILES = {
     (3, 1_000_000, 10_000, 10, "lists"): "flat_scan_kernel_l2_1Mx128_q10k_k10.md",
     (3, 1_000_000, 10_000, 10, "collect-bounded"): "flat_collect_scan_bounded_l2_1Mx128_q10k_k10.md",
     (2, 100_000, 1_000, 10, "lists"): "flat_scan_kernel_ip_100kx384_q1k_k10.md",
+    (5, 10_000_000, 16_384, 100, "collect-sampled"):
+        "flat_collect_scan_ip_10Mx384_q16k_k100_mask10.md",
 }
 
 # the same for the fp16 collect scan (rows and queries exact in fp16), by the same keys
@@ -331,6 +381,9 @@ def bench_flat(args, dev):
                                                              dists.view(np.uint32)))
     log(f"[bench] host-buffer search_batch: {hb['ms_median']:.3f} ms median of 7, "
         f"{hb['value']:.0f} QPS")
+    latency = None
+    if args.latency > 0 and mask is None:
+        latency = single_query_latency(idx, queries, k, args.latency, ids)
 
     # the same searches with the collect scan multiplying in fp16, where every value of the
     # rows and queries is exact in fp16 (the products are then exact either way)
@@ -414,6 +467,8 @@ def bench_flat(args, dev):
     }
     if f16 is not None:
         result["f16_exact_scan"] = f16
+    if latency is not None:
+        result["latency_single_query"] = latency
     ctr = read_counters(COUNTER_PROFILES.get((c, n, nq, k, info["path"]), ""), not args.sift)
     if ctr and "mfma_busy_frac" in ctr:
         result["roofline"]["mfma_busy"] = {
@@ -436,19 +491,23 @@ def bench_flat(args, dev):
         import oracle
 
         cb, par = cpu_baseline(data, queries, k, oracle.L2 if l2 else oracle.IP, ids, dists,
-                               args.cpu_seconds, mask=mask)
+                               args.cpu_seconds, mask=mask, **getattr(args, "cpu_opts", {}))
         result["cpu_baseline"] = cb
         result["parity_sample"] = par
     return result
 
 
-def bench_pq(args, dev):
+def bench_pq(args, dev, variants=None):
+    """PqIndex ADC scan (workload 4): 1M x 128 N(0,1) rows encoded as m = 16 x 8-bit codes
+    (codebooks from the reference's k-means, 25 iterations on a 50,000-row sample, seed
+    24301), 10,000 queries, k = 10. variants: mask settings to measure on the one trained
+    index (False: unfiltered, True: the 50%-density filter); default: --mask's. Returns the
+    result of the first variant, or the list of them when variants is given."""
     n, dim, m = args.n or 1_000_000, 128, 16
     nq, k = args.nq or 10_000, args.k or 10
     log(f"[bench] generating PQ corpus {n} x {dim} N(0,1), training m={m}")
     data = datagen.gaussian(n, dim, 4001)
     queries = datagen.gaussian(nq, dim, 4002)
-    mask = datagen.mask(n, 0.5, 4003) if args.mask else None
     pq = PqIndex(dim, Metric.L2, m=m, nbits=8, train_iters=25, train_sample=50_000)
     t0 = time.perf_counter()
     pq.train(data)
@@ -458,6 +517,20 @@ def bench_pq(args, dev):
     pq.add(data)
     add_s = time.perf_counter() - t0
     log(f"[bench] encode + upload {add_s:.2f} s")
+    del data
+    out = []
+    for masked in (variants if variants is not None else (args.mask,)):
+        mask = datagen.mask(n, 0.5, 4003) if masked else None
+        res = pq_measure(args, dev, pq, queries, mask, n, m, nq, k)
+        res["build_seconds"] = {"train": train_s, "encode_and_upload": add_s}
+        out.append(res)
+        dev.free()
+    if variants is None:
+        return out[0]
+    return out
+
+
+def pq_measure(args, dev, pq, queries, mask, n, m, nq, k):
     lib = dev.lib
     dq = dev.put(queries)
     dm = dev.put(mask.view(np.uint8)) if mask is not None else None
@@ -479,12 +552,13 @@ def bench_pq(args, dev):
     pq._timing(True)
     for _ in range(args.warmup):
         step()
-    scan_ms = []
+    scan_ms, total_ms = [], []
     t0 = time.perf_counter()
     for _ in range(args.steps):
         step()
         read_timing(*timing_args)
         scan_ms.append(ev_scan.value)
+        total_ms.append(ev_total.value)
     elapsed = time.perf_counter() - t0
     ids = dev.get(di, np.empty((nq, k), dtype=np.int64))
     dists = dev.get(dd, np.empty((nq, k), dtype=np.float32))
@@ -498,34 +572,40 @@ def bench_pq(args, dev):
     n_eff = int(mask.sum()) if mask is not None else n
     algo_bytes = nq * (n_eff * m + ((n + 7) // 8 if mask is not None else 0)) + nq * m * 256 * 4
     achieved = algo_bytes / (np.mean(scan_ms) * 1e-3) / 1e9
+    headline_shape = (n, nq, k) == (1_000_000, 10_000, 10)
+    log(f"[bench] PQ scan{' (50% mask)' if mask is not None else ''}: "
+        f"{elapsed / args.steps * 1e3:.3f} ms a batch, scan {np.mean(scan_ms):.3f} ms, "
+        f"{achieved:.0f} GB/s algorithmic")
     result = {
-        "metric": "PqIndex ADC scan QPS (1M x m=16 x 8-bit codes, k=10, 10k-query batch); "
-                  "% HBM peak",
+        "metric": "PqIndex ADC scan QPS (1M x m=16 x 8-bit codes, k=10, 10k-query batch"
+                  + (", 50%-density filter" if mask is not None else "") + "); % HBM peak",
         "value": nq * args.steps / elapsed,
         "unit": "queries/s",
         "ms_per_step": elapsed / args.steps * 1e3,
         "dtype": "f32",
-        "build_seconds": {"train": train_s, "encode_and_upload": add_s},
         "config": {"workload": f"PqIndex ADC L2, {n} codes x m={m} x 8 bit, {nq}-query batch, "
                                f"k={k}, mask={'50%' if mask is not None else 'none'}",
-                   "n": n, "m": m, "nq": nq, "k": k},
+                   "n": n, "m": m, "nq": nq, "k": k, "n_eff": n_eff,
+                   "queries_resident_in_hbm": True},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": read_traffic("pq_scan_kernel_l2_1Mx16_q10k_k10.md"
-                                             if mask is None else
-                                             "pq_scan_kernel_l2_1Mx16_q10k_k10_mask50.md",
-                                             (n, nq, k) == (1_000_000, 10_000, 10)),
+                     "traffic": read_traffic(PQ_PROFILES[mask is not None][0], headline_shape),
                      "kernel": "pq_scan_kernel", "kernel_ms": float(np.mean(scan_ms)),
                      "algorithmic_bytes_per_launch": algo_bytes},
+        "pipeline_ms": float(np.mean(total_ms)),
         "host_buffer": hb,
     }
-    ctr = read_counters(PQ_COUNTER_PROFILE,
-                        mask is None and (n, nq, k) == (1_000_000, 10_000, 10))
+    ctr = read_counters(PQ_PROFILES[mask is not None][1], headline_shape)
     if ctr:
         result["roofline"]["lds"] = {
             "busy_frac": ctr.get("lds_busy_frac"),
             "bank_conflict_cycles_per_lds_cycle": ctr.get("lds_bank_conflict_per_cycle"),
-            "valu_busy_frac": ctr.get("valu_busy_frac"), "source": ctr["source"]}
+            "valu_busy_frac": ctr.get("valu_busy_frac"),
+            "lds_roofline_frac": ctr.get("lds_roofline_frac"),
+            "source": ctr["source"]}
+    if args.latency > 0 and mask is None:
+        result["latency_single_query"] = single_query_latency(pq, queries, k, args.latency,
+                                                              ids)
     if args.cpu_seconds > 0:
         import oracle
 
@@ -583,7 +663,19 @@ def main():
                     help="also write a schema_version 1 results envelope to this path")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="CPU oracle budget for the baseline (0 disables)")
+    ap.add_argument("--latency", type=int, default=None,
+                    help="single-query latency samples (bench/harness.py:238-253); default "
+                         f"{LATENCY_SAMPLES} on the default run's flat and PQ workloads, else 0")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="default run: skip the other workloads measured after the headline")
     args = ap.parse_args()
+    # the default invocation (the headline workload, no overrides) also measures the other
+    # workloads of the scope: the PQ ADC scan with and without its filter, the 100k x 384
+    # and 10M x 384 FlatIndex workloads, and single-query latency
+    default_run = (args.workload == "flat" and args.config == 3 and args.k is None and
+                   args.n is None and args.nq is None and args.sift is None)
+    if args.latency is None:
+        args.latency = LATENCY_SAMPLES if default_run and not args.no_extras else 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this backend runs the whole search on a "
               "single MI355X and has no multi-GPU path (a sharded search would split the "
@@ -594,9 +686,13 @@ def main():
         print("bench.py needs a gfx950 GPU (none visible)", file=sys.stderr)
         sys.exit(1)
     dev = Dev()
+    extras = {}
     try:
         run = {"flat": bench_flat, "pq": bench_pq, "copy": bench_copy}[args.workload]
         res = run(args, dev)
+        dev.free()
+        if default_run and not args.no_extras:
+            extras = bench_extras(args, dev)
     finally:
         dev.free()
     out = {"metric": res.pop("metric"), "value": res.pop("value"), "unit": res.pop("unit"),
@@ -606,10 +702,51 @@ def main():
            "data": res.pop("data", "synthetic (seeded SplitMix64)"),
            "config": res.pop("config")}
     out.update(res)
+    out.update(extras)
     out["device"] = _lib.device_info(0)
     if args.envelope and args.workload != "copy":
         write_bench_envelope(args.envelope, out)
     print(json.dumps(out), flush=True)
+
+
+def bench_extras(args, dev) -> dict:
+    """The other workloads of the scope, each as its own object of the default run's line
+    (its own QPS, kernel time and roofline fraction, CPU baseline and parity sample):
+    the PQ ADC scan (workload 4) unfiltered and with its 50% filter, FlatIndex inner product
+    on 100k x 384 (workload 2: the reference's own `make bench` shape) and on 10M x 384 with
+    a 10% filter, k = 100 (workload 5; the CPU oracle times a sample of its first 128
+    queries, each of which streams the ~1M kept rows)."""
+    import argparse
+
+    def sub(**kw):
+        a = argparse.Namespace(**vars(args))
+        a.sift = a.envelope = None
+        a.n = a.nq = a.k = None
+        a.no_f16 = True
+        for key, v in kw.items():
+            setattr(a, key, v)
+        return a
+
+    extras = {}
+    t0 = time.perf_counter()
+    pq_u, pq_m = bench_pq(sub(workload="pq", cpu_seconds=min(args.cpu_seconds, 6.0)), dev,
+                          variants=(False, True))
+    extras["pq_adc_scan"] = pq_u
+    extras["pq_adc_scan_mask50"] = pq_m
+    log(f"[bench] PQ workloads in {time.perf_counter() - t0:.1f} s")
+    t0 = time.perf_counter()
+    extras["flat_ip_100kx384"] = bench_flat(
+        sub(config=2, steps=max(args.steps, 100), latency=0,
+            cpu_seconds=min(args.cpu_seconds, 6.0)), dev)
+    dev.free()
+    log(f"[bench] workload 2 in {time.perf_counter() - t0:.1f} s")
+    t0 = time.perf_counter()
+    extras["flat_ip_10Mx384_mask10_k100"] = bench_flat(
+        sub(config=5, latency=0, cpu_seconds=min(args.cpu_seconds, 8.0),
+            cpu_opts={"warm_mt": 16, "single": False, "max_queries": 128}), dev)
+    dev.free()
+    log(f"[bench] workload 5 in {time.perf_counter() - t0:.1f} s")
+    return extras
 
 
 def write_bench_envelope(path: str, out: dict) -> None:

@@ -16,7 +16,7 @@ import bench
 
 PROFILES = Path(__file__).resolve().parent.parent / "profiles"
 NAMES = sorted(set(bench.TRAFFIC_PROFILES.values()) | set(bench.F16_PROFILES.values()) |
-               {"pq_scan_kernel_l2_1Mx16_q10k_k10.md", "pq_scan_kernel_l2_1Mx16_q10k_k10_mask50.md"})
+               {traffic for traffic, _ in bench.PQ_PROFILES.values()})
 
 
 @pytest.mark.parametrize("name", NAMES)
@@ -70,9 +70,10 @@ def test_f16_counter_profile_is_complete(name):
 
 
 def test_lds_counter_profile_is_complete():
-    text = (PROFILES / bench.PQ_COUNTER_PROFILE).read_text()
+    name = bench.PQ_PROFILES[False][1]
+    text = (PROFILES / name).read_text()
     assert "rocprofv3 --pmc SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT" in text
-    ctr = bench.read_counters(bench.PQ_COUNTER_PROFILE, True)
+    ctr = bench.read_counters(name, True)
     assert 0 < ctr["lds_busy_frac"] < 1 and ctr["lds_bank_conflict_per_cycle"] > 0
 
 
