@@ -595,14 +595,27 @@ def pq_measure(args, dev, pq, queries, mask, n, m, nq, k):
         "pipeline_ms": float(np.mean(total_ms)),
         "host_buffer": hb,
     }
+    # the scan's real limit: its LUT gathers, one 16-byte LDS read per (row, 4 queries,
+    # subspace), against the measured LDS read rates (profiles/lds_gather_rate.md)
+    qpb = 4
+    gather_bytes = ((nq + qpb - 1) // qpb) * n_eff * m * 16
+    g_ach = gather_bytes / (np.mean(scan_ms) * 1e-3) / 1e9
+    lds = read_counters(LDS_PROFILE, True) or {}
+    result["lds_roofline"] = {
+        "bound": "lds", "achieved": g_ach, "unit": "GB/s",
+        "gather_bytes_per_launch": gather_bytes,
+        "peak": lds.get("lds_conflict_free_gbs"),
+        "frac": g_ach / lds["lds_conflict_free_gbs"] if lds.get("lds_conflict_free_gbs") else None,
+        "random_gather_ceiling": lds.get("lds_random_gather_gbs"),
+        "frac_of_random_gather_ceiling": (g_ach / lds["lds_random_gather_gbs"]
+                                          if lds.get("lds_random_gather_gbs") else None),
+        "source": lds.get("source")}
     ctr = read_counters(PQ_PROFILES[mask is not None][1], headline_shape)
     if ctr:
-        result["roofline"]["lds"] = {
-            "busy_frac": ctr.get("lds_busy_frac"),
+        result["lds_roofline"]["counters"] = {
+            "lds_busy_frac": ctr.get("lds_busy_frac"),
             "bank_conflict_cycles_per_lds_cycle": ctr.get("lds_bank_conflict_per_cycle"),
-            "valu_busy_frac": ctr.get("valu_busy_frac"),
-            "lds_roofline_frac": ctr.get("lds_roofline_frac"),
-            "source": ctr["source"]}
+            "valu_busy_frac": ctr.get("valu_busy_frac"), "source": ctr["source"]}
     if args.latency > 0 and mask is None:
         result["latency_single_query"] = single_query_latency(pq, queries, k, args.latency,
                                                               ids)
@@ -640,12 +653,51 @@ def bench_copy(args, dev):
                          "kernel": "copy_kernel", "kernel_ms": float(np.mean(times))}}
 
 
+LDS_PROFILE = "lds_gather_rate.md"
+
+
+def bench_lds(args, dev):
+    """LDS read-rate calibration, the PQ scan's roofline: 1,024 workgroups of 512 threads read
+    16-byte slots of a 64 KB LDS table, 16 reads a loop iteration as the ADC scan issues its
+    gathers, with no bank conflict and at uniform random slots (the scan's pattern on uniform
+    codes). value = the conflict-free rate; random_gather = the other."""
+    lib = dev.lib
+    blocks, iters = 1024, 2048
+    rates = {}
+    for random in (0, 1):
+        ms, nbytes = ctypes.c_float(), ctypes.c_double()
+        times = []
+        for i in range(args.warmup + args.steps):
+            if lib.px_dev_lds_gather(random, blocks, iters, ctypes.byref(ms), ctypes.byref(nbytes)):
+                raise RuntimeError(_lib.last_error())
+            if i >= args.warmup:
+                times.append(ms.value)
+        rates[random] = (nbytes.value / (np.mean(times) * 1e-3) / 1e9, float(np.mean(times)),
+                         nbytes.value)
+    info = _lib.device_info(0)
+    clk = info.get("clock_khz", 0) * 1e3
+    cus = info.get("cus", 0)
+
+    def per_clk(gbs):
+        return gbs * 1e9 / (clk * cus) if clk and cus else None
+
+    log(f"[bench] LDS 16-byte reads: {rates[0][0]:.0f} GB/s conflict-free, "
+        f"{rates[1][0]:.0f} GB/s at random slots")
+    return {"metric": "LDS read rate, 16-byte reads from a 64 KB table, no bank conflicts",
+            "value": rates[0][0], "unit": "GB/s", "ms_per_step": rates[0][1], "dtype": "f32",
+            "config": {"workload": f"lds_gather_kernel, {blocks} workgroups x 512 threads x "
+                                   f"{iters} x 16 reads of 16 bytes", "bytes": rates[0][2]},
+            "bytes_per_clk_per_cu": per_clk(rates[0][0]),
+            "random_gather": {"value": rates[1][0], "unit": "GB/s", "ms": rates[1][1],
+                              "bytes_per_clk_per_cu": per_clk(rates[1][0])}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", choices=["flat", "pq", "copy"], default="flat")
+    ap.add_argument("--workload", choices=["flat", "pq", "copy", "lds"], default="flat")
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 5],
                     help="flat: which FlatIndex workload (3, the headline, by default)")
     ap.add_argument("--k", type=int, default=None, help="override the workload's k")
@@ -688,7 +740,8 @@ def main():
     dev = Dev()
     extras = {}
     try:
-        run = {"flat": bench_flat, "pq": bench_pq, "copy": bench_copy}[args.workload]
+        run = {"flat": bench_flat, "pq": bench_pq, "copy": bench_copy,
+               "lds": bench_lds}[args.workload]
         res = run(args, dev)
         dev.free()
         if default_run and not args.no_extras:
@@ -704,7 +757,7 @@ def main():
     out.update(res)
     out.update(extras)
     out["device"] = _lib.device_info(0)
-    if args.envelope and args.workload != "copy":
+    if args.envelope and args.workload in ("flat", "pq"):
         write_bench_envelope(args.envelope, out)
     print(json.dumps(out), flush=True)
 

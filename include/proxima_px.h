@@ -239,6 +239,11 @@ int px_dev_upload(void* dst, const void* src, size_t bytes);
 int px_dev_download(void* dst, const void* src, size_t bytes);
 /* Streaming copy kernel of `bytes` (multiple of 16): calibrates HBM traffic counters. */
 int px_dev_copy_kernel(void* dst, const void* src, size_t bytes, float* ms);
+/* LDS read-rate calibration for the PQ scan's roofline: `blocks` workgroups of 512 threads,
+ * each thread `iters` x 16 reads of 16 bytes from a 64 KB LDS table, with no bank conflict
+ * (random = 0) or at uniform random slots (random = 1: the ADC scan's gathers). *ms: kernel
+ * time; *bytes: bytes read. No counterpart in the reference. */
+int px_dev_lds_gather(int random, int blocks, int iters, float* ms, double* bytes);
 
 #ifdef __cplusplus
 }

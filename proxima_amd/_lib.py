@@ -90,6 +90,7 @@ SIGNATURES = {
     "px_dev_upload": (c_int, [c_void_p, c_void_p, c_size_t]),
     "px_dev_download": (c_int, [c_void_p, c_void_p, c_size_t]),
     "px_dev_copy_kernel": (c_int, [c_void_p, c_void_p, c_size_t, _f32p]),
+    "px_dev_lds_gather": (c_int, [c_int, c_int, c_int, _f32p, POINTER(ctypes.c_double)]),
 }
 
 _lib = None

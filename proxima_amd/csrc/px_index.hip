@@ -1715,6 +1715,9 @@ int pq_run_collect_batch(px_pq* p, const float* d_q, int64_t nq, int64_t k, int6
     hipStream_t s = p->stream;
     const int cus = std::max(p->dev.cus, 1);
     const int waves = px::pq_lists_per_split();
+    // splits of whole blocks of rows (each wave of a workgroup takes 64 of every rg rows, so
+    // that a region of cap rps / waves can take all of its wave's rows)
+    const int64_t rg = px::pq_rows_per_block_step();
     const int64_t qpb = px::pq_queries_per_block((int)p->m, (int)p->ks);
     auto base_args = [&]() {
         px::PqScanArgs a{};
@@ -1735,7 +1738,7 @@ int pq_run_collect_batch(px_pq* p, const float* d_q, int64_t nq, int64_t k, int6
         *splits = std::min<int64_t>(choose_splits(rows, groups, waves, 1, cus, 4096),
                                     px::kMaxCollectRegions / waves);
         *rps = (rows + *splits - 1) / *splits;
-        *rps = std::max<int64_t>((*rps + 255) / 256 * 256, 256);
+        *rps = std::max<int64_t>((*rps + rg - 1) / rg * rg, rg);
         *splits = std::max<int64_t>(1, (rows + *rps - 1) / *rps);
     };
     CollectJob j;
@@ -1782,7 +1785,7 @@ int pq_run_collect_batch(px_pq* p, const float* d_q, int64_t nq, int64_t k, int6
         int64_t slots = *take, splits = 1, rps = 256;
         for (;;) {
             plan(n_eff, slots, &splits, &rps);
-            // one region per wave of a split; a wave takes 64 of every 256 rows
+            // one region per wave of a split; a wave takes 64 of every rg rows
             *regions = splits * waves;
             *cap = collect_cap(expect, *regions, round, j.kk, rps / waves);
             const int64_t per = *regions * *cap * 8;
@@ -1856,6 +1859,7 @@ int pq_run_paths(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_
     p->last_rounds = 0;
     if (k > PX_MAX_K) {
         const int waves = px::pq_lists_per_split();
+        const int64_t rg = px::pq_rows_per_block_step();
         const int64_t qpb = px::pq_queries_per_block((int)p->m, (int)p->ks);
         const int cus = std::max(p->dev.cus, 1);
         return run_full_sort(
@@ -1866,7 +1870,7 @@ int pq_run_paths(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_
                 int64_t splits = std::min<int64_t>(
                     choose_splits(n_eff, groups, waves, 1, cus, 4096), px::kMaxCollectRegions / waves);
                 int64_t rps = (n_eff + splits - 1) / splits;
-                rps = std::max<int64_t>((rps + 255) / 256 * 256, 256);
+                rps = std::max<int64_t>((rps + rg - 1) / rg * rg, rg);
                 splits = std::max<int64_t>(1, (n_eff + rps - 1) / rps);
                 px::PqScanArgs a{};
                 a.dbg = p->ws.dbg;
@@ -1894,11 +1898,12 @@ int pq_run_paths(px_pq* p, const float* d_q, int64_t nq, int64_t k, const uint8_
     if (k > px::kMaxList && n_eff > 0) return pq_run_collect(p, d_q, nq, k, n_eff, rowidx, d_ids, d_out);
     const int kl = (int)std::min<int64_t>(k, px::kMaxList);
     const int lists = px::pq_lists_per_split();
+    const int64_t rg = px::pq_rows_per_block_step();
     const int64_t qpb = px::pq_queries_per_block((int)p->m, (int)p->ks);
     const int64_t groups = (nq + qpb - 1) / qpb;
     int splits = choose_splits(n_eff, groups, lists, kl, p->dev.cus, 4096);
     int64_t rps = (n_eff + splits - 1) / splits;
-    rps = std::max<int64_t>((rps + 255) / 256 * 256, 256);
+    rps = std::max<int64_t>((rps + rg - 1) / rg * rg, rg);
     splits = (int)std::max<int64_t>(1, (n_eff + rps - 1) / rps);
     const int64_t width = (int64_t)splits * lists * kl;
 
@@ -2582,6 +2587,29 @@ int px_dev_copy_kernel(void* dst, const void* src, size_t bytes, float* ms) {
     if (ms) *ms = t;
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
+    return PX_OK;
+}
+
+int px_dev_lds_gather(int random, int blocks, int iters, float* ms, double* bytes) {
+    if (blocks <= 0 || iters <= 0) return fail(PX_ERR_ARG, "blocks and iters must be positive");
+    const int nt = px::lds_gather_threads();
+    float* out = nullptr;
+    PX_HIP(dev_malloc(&out, sizeof(float) * (size_t)blocks * nt));
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    float t = 0.f;
+    if (e == hipSuccess) e = hipEventRecord(e0, nullptr);
+    if (e == hipSuccess) e = px::launch_lds_gather(random, blocks, iters, out, nullptr);
+    if (e == hipSuccess) e = hipEventRecord(e1, nullptr);
+    if (e == hipSuccess) e = hipEventSynchronize(e1);
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, e0, e1);
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    dev_free(out);
+    PX_HIP(e);
+    if (ms) *ms = t;
+    if (bytes) *bytes = (double)blocks * nt * iters * 16.0 * 16.0;
     return PX_OK;
 }
 

@@ -277,6 +277,9 @@ struct PqScanArgs {
 };
 int pq_list_capacity(int kl);
 int pq_lists_per_split();
+// Rows a PQ workgroup's waves take per step (waves x 64): wave w takes rows 64 w .. 64 w + 63
+// of every step, so splits of a multiple of it give every wave the same share.
+int pq_rows_per_block_step();
 int pq_queries_per_block(int m, int ks);
 hipError_t launch_pq_scan(const PqScanArgs& a, hipStream_t s);
 hipError_t launch_pq_collect(const PqScanArgs& a, hipStream_t s);
@@ -306,5 +309,10 @@ hipError_t launch_full_sort(const float* keys, int64_t n_eff, int qc, const int*
                             hipStream_t s);
 // Plain streaming copy (calibrates HBM traffic counters against known bytes).
 hipError_t launch_copy(const float4* src, float4* dst, int64_t n4, hipStream_t s);
+// LDS read-rate calibration: blocks x lds_gather_threads() threads, each iters x 16 reads of
+// 16 bytes from a 64 KB table (random = 0: no bank conflicts; 1: uniform random slots, the
+// ADC scan's gathers); out holds one float per thread.
+int lds_gather_threads();
+hipError_t launch_lds_gather(int random, int blocks, int iters, float* out, hipStream_t s);
 
 }  // namespace px

@@ -69,12 +69,22 @@ def test_f16_counter_profile_is_complete(name):
     assert 1.0 < ctr["shader_clock_ghz"] < 2.5
 
 
-def test_lds_counter_profile_is_complete():
-    name = bench.PQ_PROFILES[False][1]
+@pytest.mark.parametrize("masked", [False, True])
+def test_lds_counter_profile_is_complete(masked):
+    name = bench.PQ_PROFILES[masked][1]
     text = (PROFILES / name).read_text()
     assert "rocprofv3 --pmc SQ_INSTS_LDS SQ_LDS_BANK_CONFLICT" in text
     ctr = bench.read_counters(name, True)
     assert 0 < ctr["lds_busy_frac"] < 1 and ctr["lds_bank_conflict_per_cycle"] > 0
+    assert 0 < ctr["lds_roofline_frac"] < 1
+
+
+def test_lds_rate_profile_is_complete():
+    # the PQ scan's roofline: the LDS read rates measured by bench.py --workload lds
+    text = (PROFILES / bench.LDS_PROFILE).read_text()
+    assert "python bench.py --workload lds" in text and "rocprofv3 --kernel-trace --stats" in text
+    ctr = bench.read_counters(bench.LDS_PROFILE, True)
+    assert ctr["lds_conflict_free_gbs"] > ctr["lds_random_gather_gbs"] > 0
 
 
 def test_host_cpu_names_the_host():
