@@ -765,10 +765,11 @@ def main():
 def bench_extras(args, dev) -> dict:
     """The other workloads of the scope, each as its own object of the default run's line
     (its own QPS, kernel time and roofline fraction, CPU baseline and parity sample):
-    the PQ ADC scan (workload 4) unfiltered and with its 50% filter, FlatIndex inner product
-    on 100k x 384 (workload 2: the reference's own `make bench` shape) and on 10M x 384 with
-    a 10% filter, k = 100 (workload 5; the CPU oracle times a sample of its first 128
-    queries, each of which streams the ~1M kept rows)."""
+    the PQ ADC scan (workload 4) unfiltered and with its 50% filter, the headline workload at
+    k = 100 (the threshold-collect path: sample scan, ladder, collect scan), FlatIndex inner
+    product on 100k x 384 (workload 2: the reference's own `make bench` shape) and on
+    10M x 384 with a 10% filter, k = 100 (workload 5; the CPU oracle times a sample of its
+    first 128 queries, each of which streams the ~1M kept rows)."""
     import argparse
 
     def sub(**kw):
@@ -787,6 +788,11 @@ def bench_extras(args, dev) -> dict:
     extras["pq_adc_scan"] = pq_u
     extras["pq_adc_scan_mask50"] = pq_m
     log(f"[bench] PQ workloads in {time.perf_counter() - t0:.1f} s")
+    t0 = time.perf_counter()
+    extras["flat_l2_1Mx128_k100"] = bench_flat(
+        sub(config=3, k=100, latency=0, cpu_seconds=min(args.cpu_seconds, 6.0)), dev)
+    dev.free()
+    log(f"[bench] workload 3 at k = 100 in {time.perf_counter() - t0:.1f} s")
     t0 = time.perf_counter()
     extras["flat_ip_100kx384"] = bench_flat(
         sub(config=2, steps=max(args.steps, 100), latency=0,
