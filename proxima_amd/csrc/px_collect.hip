@@ -28,7 +28,8 @@
 // exact in fp16 as in fp32, so the keys are the fp32 scan's up to the rounding of the sums.
 // A group of 16 dims is only two MFMAs, so a stage holds two tiles (one stage sync per 32
 // MFMAs of a wave), norms sit in eight slots (one a tile), and each group's A operands and
-// norms are read two groups ahead.
+// norms are read two groups ahead. Here it serves the dense keys of a threshold sample
+// only: thresholded and bounded fp16 scans run in px_collect16.hip (64 queries a wave).
 //
 // Appends go to one of two regions per (query slot, split), one per lane of the pair that
 // holds the query (lanes l and l ^ 32 hold the two halves of the query's 64 rows of a
@@ -220,7 +221,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
     float gbound = kInf;  // DYN: the shared bound as last refreshed
     float ctest = cthr;   // min(cthr, gbound): pre-screen of the key tests
     int ccount = 0;       // rows appended (or counted past the region's capacity)
-    int* gbest = DYN ? a.gbest + (int64_t)(qvalid ? q : 0) * 32 : nullptr;
+    int* gbest = DYN ? a.gbest + (qvalid ? q : 0) : nullptr;  // slot s at gbest[s * gbest_ld]
     int cpub = kTotalKeyInf;     // DYN: this lane's published running minimum
     int next_refresh = 0;        // DYN: tile index of the next refresh
     float* const creg_k = a.cand_keys + ((int64_t)slot * a.splits + split) * 2 * a.cap +
@@ -451,15 +452,8 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
                 cpub = pub_now ? tk : cpub;
                 if (t - 1 == next_refresh) {
                     // the query's 32 published slots; their kl-th smallest bounds its best kl
-                    const long long* src = reinterpret_cast<const long long*>(gbest + h * 16);
                     int v[16];
-#pragma unroll
-                    for (int u = 0; u < 8; ++u) {
-                        const long long w =
-                            __hip_atomic_load(src + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        v[2 * u] = (int)(w & 0xffffffffll);
-                        v[2 * u + 1] = (int)(w >> 32);
-                    }
+                    load_slots16(gbest, a.gbest_ld, h, v);
                     gbound = fminf(gbound, from_total_key(kth_smallest32(v, a.kl)));
                     next_refresh = (t - 1) + max(1, (t - 1) >> 1);
                 }
@@ -472,7 +466,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
             an0 = *reinterpret_cast<const Frag*>(tile_at(rb_cur, kTileRows + j));
             an1 = *reinterpret_cast<const Frag*>(tile_at(rb_cur, kTileRows + 32 + j));
             if constexpr (DYN) {
-                if (pub_now) atomicMin(gbest + (split & 31), cpub);
+                if (pub_now) atomicMin(gbest + (int64_t)(split & 31) * a.gbest_ld, cpub);
             }
             return;
         }
@@ -490,7 +484,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
         publish(s + 2);
         if constexpr (DYN) {
             // published after the commit, whose waits then do not wait for the atomic
-            if (pub_now) atomicMin(gbest + (split & 31), cpub);
+            if (pub_now) atomicMin(gbest + (int64_t)(split & 31) * a.gbest_ld, cpub);
         }
         rb_cur = rb_nxt;
         ++s;
@@ -533,7 +527,7 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
                 vmin = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? fminf(vmin, acc[x >> 4][x & 15])
                                                                  : vmin;
             const int tk = total_key(vmin);
-            if (qvalid && tk < cpub) atomicMin(gbest + (split & 31), tk);
+            if (qvalid && tk < cpub) atomicMin(gbest + (int64_t)(split & 31) * a.gbest_ld, tk);
         }
         const int pt0 = t0;
 #pragma unroll
@@ -568,15 +562,21 @@ hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s) {
     if (dyn && a.dense) return hipErrorInvalidValue;
     if ((a.corpus_h == nullptr) != (a.queries_h == nullptr)) return hipErrorInvalidValue;
     const bool h16 = a.corpus_h != nullptr;
+    // fp16 rows: thresholds or the shared bound take the 64-query-wave scan; the dense keys
+    // of a threshold sample stay here
+    if (h16 && !a.dense) return launch_flat_collect16(a, s);
     const FlatScanArgs b = with_spin_limit(a);
 #define PX_COLLECT(L2, FILT, DYN)                                                              \
     do {                                                                                       \
-        if (h16)                                                                               \
-            hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true, true>), grid,   \
-                               block, 0, s, b);                                                \
-        else                                                                                   \
-            hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true, false>), grid,  \
-                               block, 0, s, b);                                                \
+        if constexpr (!(DYN)) {                                                                \
+            if (h16) {                                                                         \
+                hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, false, true, true>),   \
+                                   grid, block, 0, s, b);                                      \
+                break;                                                                         \
+            }                                                                                  \
+        }                                                                                      \
+        hipLaunchKernelGGL((flat_collect_kernel<L2, false, FILT, DYN, true, false>), grid,      \
+                           block, 0, s, b);                                                    \
     } while (0)
     if (a.metric == 0) {
         if (a.rowidx) {

@@ -211,7 +211,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     const float* qrow = a.queries + (int64_t)(qvalid ? q : 0) * a.dp;
     int* gtau = COLLECT ? nullptr : a.gtau + (qvalid ? q : 0);
     // collect mode with a.gbest: a shared bound as well (below)
-    int* gbest = (COLLECT && !a.gbest) ? nullptr : a.gbest + (int64_t)(qvalid ? q : 0) * 32;
+    int* gbest = (COLLECT && !a.gbest) ? nullptr : a.gbest + (qvalid ? q : 0);
     // collect mode: this query's threshold (nothing passes -inf) and region
     float cthr = -kInf;
     int cpos = -1, ccount = 0;
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             }
             const int bk = total_key(lkeys[wave][j][pub_m - 1]);
             if (h == 0 && qvalid && bk < published_best) {
-                atomicMin(gbest + (split & 31), bk);
+                atomicMin(gbest + (int64_t)(split & 31) * a.gbest_ld, bk);
                 published_best = bk;
             }
         }
@@ -619,15 +619,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                     pub_now = qvalid && tk < cpub;
                     cpub = pub_now ? tk : cpub;
                     if (ti == next_refresh) {
-                        const long long* src = reinterpret_cast<const long long*>(gbest + h * 16);
                         int v[16];
-#pragma unroll
-                        for (int u = 0; u < 8; ++u) {
-                            const long long w = __hip_atomic_load(src + u, __ATOMIC_RELAXED,
-                                                                  __HIP_MEMORY_SCOPE_AGENT);
-                            v[2 * u] = (int)(w & 0xffffffffll);
-                            v[2 * u + 1] = (int)(w >> 32);
-                        }
+                        load_slots16(gbest, a.gbest_ld, h, v);
                         gbound = fminf(gbound, from_total_key(kth_smallest32(v, a.kl)));
                         // sparser than the lists' schedule: each refresh waits for its loads
                         // in the epilogue (t -> t + t/4: 21.73 ms a scan on 1M x 128, t + t/2:
@@ -658,15 +651,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             if (ti == next_refresh) {
                 // loaded here rather than ahead: refreshes are rare, and holding 16 more
                 // registers across the MFMAs would spill
-                const long long* src = reinterpret_cast<const long long*>(gbest + h * 16);
                 int v[16];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    const long long w =
-                        __hip_atomic_load(src + u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    v[2 * u] = (int)(w & 0xffffffffll);
-                    v[2 * u + 1] = (int)(w >> 32);
-                }
+                load_slots16(gbest, a.gbest_ld, h, v);
                 gbound = fminf(gbound, from_total_key(kth_smallest32(v, pub_rank)));
                 // t -> t + t/2: each refresh stalls both waves of a SIMD for its loads (on
                 // 100k x 384 x 1,000 queries, 25 tiles a split: 0.81 -> 0.80 ms against
@@ -752,7 +738,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             commit((int)((s + 1) & 1), c1, (int)(t1 & 1));
         }
         if (dyn && pub_now) {
-            atomicMin(gbest + (split & 31), cpub);
+            atomicMin(gbest + (int64_t)(split & 31) * a.gbest_ld, cpub);
             pub_now = false;
         }
         if constexpr (!RELAXED) __syncthreads();
@@ -1186,7 +1172,7 @@ __global__ __launch_bounds__(1024) void flat_merge_kernel(MergeArgs a) {
     if (a.gbest) {
         __shared__ int s_gb[32], s_kth;
         const int t = threadIdx.x;
-        if (t < 32) s_gb[t] = a.gbest[(int64_t)q * 32 + t];
+        if (t < 32) s_gb[t] = a.gbest[(int64_t)t * a.gbest_ld + q];
         __syncthreads();
         const int pm = (a.kl + min(a.splits, 32) - 1) / min(a.splits, 32);
         const int rank = (a.kl + pm - 1) / pm;  // <= min(splits, 32)
@@ -1418,7 +1404,7 @@ __global__ __launch_bounds__(1024) void flat_collect_select_kernel(CollectSelect
     int bound = kTotalKeyInf;
     if (a.gbest && finish) {
         __shared__ int s_gb[32], s_kth;
-        if (t < 32) s_gb[t] = a.gbest[(int64_t)q * 32 + t];
+        if (t < 32) s_gb[t] = a.gbest[(int64_t)t * a.gbest_ld + q];
         if (t == 0) s_kth = kTotalKeyInf;
         __syncthreads();
         if (t < 32) {

@@ -895,6 +895,7 @@ int run_collect(CollectJob& j) {
             c.status = ws.status.as<int>();
             c.kk = (int)kk;
             c.gbest = j.sel_gbest;
+            c.gbest_ld = j.nq;
             c.cand_dmin = j.sel_dmin;
             // a scan's stage sync that gave up (status[nq]): the select writes nothing
             c.spin_fail = ws.status.as<int>() + nq;
@@ -952,9 +953,11 @@ int64_t collect_cap(double expect, int64_t regions, int round, int64_t kk, int64
     return std::max<int64_t>(1, std::min<int64_t>((cap + 31) / 32 * 32, most));
 }
 
-// Splits and rows per split of an MFMA collect scan of `slots` query slots.
-void collect_splits(int64_t n_eff, int64_t slots, int cus, int64_t* splits, int64_t* rps) {
-    const int64_t groups = (slots + 255) / 256;
+// Splits and rows per split of an MFMA collect scan of `slots` query slots, qpb of them a
+// workgroup (256; the fp16 scan 512).
+void collect_splits(int64_t n_eff, int64_t slots, int cus, int64_t* splits, int64_t* rps,
+                    int64_t qpb = 256) {
+    const int64_t groups = (slots + qpb - 1) / qpb;
     int64_t sp = std::min<int64_t>(choose_flat_splits(n_eff, groups, 1, cus, false),
                                    px::kMaxCollectRegions / 2);
     int64_t r = (n_eff + sp - 1) / sp;
@@ -1040,6 +1043,8 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
     const unsigned short* vh =
         f->scan_f16 && f->d_xh && f->dp == 128 && vec_collect(nq, f->dp) ? f->d_xh : nullptr;
     f->last_f16 = qh != nullptr || vh != nullptr;
+    // query slots a workgroup of the (non-dense) MFMA collect scan
+    const int64_t qpb = qh ? px::flat_collect16_queries_per_block() : 256;
     CollectJob j;
     j.ws = &ws;
     j.stream = s;
@@ -1183,7 +1188,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             return PX_OK;
         }
         for (;;) {
-            collect_splits(n_eff, slots, cus, &splits, &rps);
+            collect_splits(n_eff, slots, cus, &splits, &rps, qpb);
             // two regions per split (one per lane of the pair holding a query), each of
             // which receives at most half the split's rows
             *regions = 2 * splits;
@@ -1238,6 +1243,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             PX_TRY(ws.gbest.reserve(sizeof(int) * j.nq * 32));
             PX_HIP(px::launch_fill_int(ws.gbest.as<int>(), j.nq * 32, px::kTotalKeyInf, s));
             a.gbest = ws.gbest.as<int>();
+            a.gbest_ld = j.nq;
             a.kl = (int)j.kk;
             j.sel_gbest = a.gbest;
         }
@@ -1245,7 +1251,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         PX_HIP(px::launch_flat_collect(a, s));
         if (round == 0) {
             f->timing.splits = (int)splits;
-            f->timing.blocks = (int)(((slots + 255) / 256) * splits);
+            f->timing.blocks = (int)(((slots + qpb - 1) / qpb) * splits);
         }
         return PX_OK;
     };
@@ -1258,7 +1264,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         j.bound_only = collect_bound_only(n_eff, nq, j.kk, f->dp, cus, rowidx != nullptr);
         if (j.bound_only) f->last_path = PX_PATH_COLLECT_BOUNDED;
         int64_t splits = 1, rps = 64;
-        collect_splits(n_eff, nq, cus, &splits, &rps);
+        collect_splits(n_eff, nq, cus, &splits, &rps, qpb);
         j.bound_expect = (double)(2 * splits) *
                          (double)std::max<int64_t>(2 * (j.kk + 48), 2 * j.kk + 1) / 3.0;
     }
@@ -1328,7 +1334,7 @@ int flat_run_collect(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_
 }
 
 // Device buffers of a list scan: split lists [nq][splits][kl] (key, position), the shared
-// bounds gtau [nq] and gbest [nq][32] and the scan's stage-sync give-up word spin (all
+// bounds gtau [nq] and gbest [32][nq] and the scan's stage-sync give-up word spin (all
 // cleared by the list prologue); verdict_h / verdict_dev: two mapped host ints where the
 // merge stores the search's finiteness and give-up verdicts, or null (no pinned memory: the
 // give-up word is read back by a copy).
@@ -1381,6 +1387,7 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     a.part_ids = b.part_i;
     a.gtau = b.gtau;
     a.gbest = b.gbest;
+    a.gbest_ld = nq;
     a.abort = d_flag;
     a.abort_seq = seq;
     a.spin_fail = b.spin;
@@ -1400,6 +1407,7 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     mg.width = n_eff > 0 ? splits * kl : 0;
     mg.bound = b.gtau;
     mg.gbest = b.gbest;
+    mg.gbest_ld = nq;
     mg.splits = splits;
     mg.nq = (int)nq;
     mg.kl = kl;

@@ -34,10 +34,14 @@ struct FlatScanArgs {
     float* part_keys;      // [nq][splits][kl]
     int* part_ids;         // compacted positions (row ids when unfiltered)
     int* gtau;             // [nq] shared per-query bound, total-order ints; starts at +inf
-    int* gbest;            // [nq][32] per-split published list keys, total-order ints; +inf.
-                           // Collect mode: optional (kl <= min(splits, 32), one 128-dim
-                           // chunk, no rowidx); each split publishes its smallest key and
+    int* gbest;            // [32][gbest_ld] per-split published keys, total-order ints
+                           // (slot s of query q at s * gbest_ld + q); +inf. Slot-major:
+                           // a wave's atomics and loads for consecutive queries share cache
+                           // lines, where a query's 32 slots in one line drew every split's
+                           // atomics to it. Collect mode: optional (kl <= min(splits, 32),
+                           // one 128-dim chunk); each split publishes its smallest key and
                            // rows above the kl-th smallest published key are not appended
+    int64_t gbest_ld;      // >= the queries indexed (nq, or the batch's with a qlist)
     // Collect mode (launch_flat_collect): no lists; every row whose (key, position) is at or
     // below its query's threshold is appended to the region of (query slot, split).
     const int* qlist;      // optional: query index of each of the nq slots
@@ -92,6 +96,11 @@ constexpr int kTotalKeyInf = 0x7f800000;
 // tight or too loose go round again.
 hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s);
 hipError_t launch_flat_collect_v1(const FlatScanArgs& a, hipStream_t s);
+// The collect scan of fp16 rows (corpus_h and queries_h given, dp 128, not dense): 64
+// queries a wave, flat_collect16_queries_per_block() query slots a workgroup; called by
+// launch_flat_collect.
+hipError_t launch_flat_collect16(const FlatScanArgs& a, hipStream_t s);
+int flat_collect16_queries_per_block();
 // The collect scan for a few query slots (nq <= kVecQueries, dp <= kVecMaxDp) on the
 // vector ALUs: the MFMA scan's 32-query tiles would be nearly all padding, so this one
 // streams the corpus at memory speed instead. One region per (slot, split):
@@ -133,10 +142,11 @@ struct CollectSelectArgs {
     int kk;                  // candidates re-ranked exactly (k + margin)
     int k;
     int metric;
-    // optional [queries][32]: the scan's shared-bound slots (FlatScanArgs::gbest). The
+    // optional [32][gbest_ld]: the scan's shared-bound slots (FlatScanArgs::gbest). The
     // kk-th smallest slot bounds the best kk, and every row at or below it was collected,
     // so a finishing query sorts only the candidates at or below it.
     const int* gbest;
+    int64_t gbest_ld;
     const float* corpus;     // nullptr: keys are exact already (PQ), no re-rank
     const float* queries;
     int dim, dp;
@@ -188,10 +198,11 @@ struct MergeArgs {
     // optional [nq] total-order key bounds (the scan's gtau): a split's full list tail, so
     // every candidate of the best kl has a key at or below it; +inf: no bound
     const int* bound;
-    // optional [nq][32] published split keys (the scan's gbest) and the scan's split count:
-    // slot i holds a key with m = ceil(kl / min(splits, 32)) candidates of one split at or
-    // below it, so the ceil(kl / m)-th smallest slot bounds the best kl as well
+    // optional [32][gbest_ld] published split keys (the scan's gbest) and the scan's split
+    // count: slot i holds a key with m = ceil(kl / min(splits, 32)) candidates of one split
+    // at or below it, so the ceil(kl / m)-th smallest slot bounds the best kl as well
     const int* gbest;
+    int64_t gbest_ld;
     int splits;
     // nonzero: the candidates are width / kl lists of kl, each in ascending order (PQ); with
     // no published bounds, the kl-th smallest list head bounds the best kl

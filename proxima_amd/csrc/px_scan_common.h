@@ -116,6 +116,23 @@ __device__ __forceinline__ f32x16 mfma_group(f16x8 a, f16x8 b, f32x16 c) { retur
 __device__ __forceinline__ f32x16 mfma_group_z(float4 a, float4 b) { return mfma4z(a, b); }
 __device__ __forceinline__ f32x16 mfma_group_z(f16x8 a, f16x8 b) { return mfma16z(a, b); }
 
+// Slots h * 16 .. h * 16 + 15 of a query's shared-bound slots (FlatScanArgs::gbest,
+// slot-major: q_slots = gbest + q, slot s at q_slots[s * ld]), relaxed device-scope loads
+// (other workgroups publish them with atomicMin). The addresses are stepped from a pointer
+// the empty asm makes opaque here: sixteen per-lane 64-bit offsets formed from h and ld
+// alone were hoisted out of the callers' scan loops and spilled.
+__device__ __forceinline__ void load_slots16(const int* q_slots, int64_t ld, int h,
+                                             int (&v)[16]) {
+    const int* p = q_slots;
+    asm volatile("" : "+v"(p));
+    p += (int64_t)h * 16 * ld;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+        v[u] = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        p += ld;
+    }
+}
+
 // rank-th smallest (1-based, rank <= 32) of the 32 ints held as v[0..15] by this lane and
 // by lane ^ 32; both lanes return it. Bitonic: sort 16 in registers, split the union into
 // its 16 smallest and 16 largest with the partner's list reversed, sort those halves.
