@@ -17,6 +17,13 @@
 // took the LDS as many cycles as the tile's MFMAs took the matrix units; here they take half,
 // and the corpus staged through LDS per query is halved too.
 //
+// Keys from the matrix unit. A tile's accumulators start from -||x||^2 / 2 of its rows (L2;
+// zero for IP), so the MFMAs leave D = q.x - ||x||^2 / 2 = key / f with f = -2 (L2) or D =
+// q.x = key / f with f = -1 (IP); every scaling is by a power of two, exact. The key tests
+// compare D with ctest / f (at or above it: f is negative) and only an appended row's key is
+// formed (f D), so no vector instruction a key is spent turning dot products into keys (on
+// integer data below 2^23 the sums, and so the keys, are exact as before).
+//
 // Pipeline (as flat_collect_kernel's): three LDS stage buffers of 128 rows (4 tiles); the
 // global loads of stage s + 2 are held in registers during stage s and written to its buffer
 // at the end of stage s, after a barrier-free stage sync (every wave has committed stage
@@ -54,17 +61,17 @@ constexpr int kBufs16 = 3;       // LDS stage buffers
 constexpr int kNormSlots16 = 16;  // norm slots, one a tile (tiles t - 1 .. t + 11 in use)
 
 // kl-th smallest (kl <= 32) key of the 32 rows a lane pair holds for one query block of a
-// split's first tile (acc[x]: row mfma_row(x, h)); rows at or past rem, and padding queries,
-// do not count; +inf when fewer than kl rows count. kl rounds of "smallest remaining" over
-// the pair, as first_tile_kth does for 64-row tiles.
-__device__ __forceinline__ float first_tile_kth16(const f32x16& acc, int rem, bool qvalid,
-                                                  int kl) {
+// split's first tile (keys f acc[x], row mfma_row(x, h)); rows at or past rem, and padding
+// queries, do not count; +inf when fewer than kl rows count. kl rounds of "smallest
+// remaining" over the pair, as first_tile_kth does for 64-row tiles.
+__device__ __forceinline__ float first_tile_kth16(const f32x16& acc, float f, int rem,
+                                                  bool qvalid, int kl) {
     constexpr int kNoKey = 0x7fffffff;
     const int h = lane_id() >> 5;
     int tk[16];
 #pragma unroll
     for (int x = 0; x < 16; ++x)
-        tk[x] = (qvalid && mfma_row(x, h) < rem) ? total_key(acc[x]) : kNoKey;
+        tk[x] = (qvalid && mfma_row(x, h) < rem) ? total_key(f * acc[x]) : kNoKey;
     int last = kNoKey;
     for (int r = 0; r < kl; ++r) {
         int bt = kNoKey, bx = 0;
@@ -92,6 +99,7 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
     constexpr int kRowStep = NT / kF4PerRow;     // rows between a thread's loads (32)
     constexpr int kPF = kStage16 / kRowStep;     // pieces a thread a stage (4)
     constexpr int NG = kChunk / 16;              // dim groups (8)
+    constexpr float kF = L2 ? -2.0f : -1.0f;     // key = kF * D (below)
     static_assert(kPF == 4 && NG == 8, "four staged pieces a thread, eight dim groups");
     __shared__ __attribute__((aligned(16))) char tile[kBufs16][kStage16 * kPitch16];
     __shared__ __attribute__((aligned(16))) float tnorm[kNormSlots16][kTile16];
@@ -157,9 +165,10 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         *reinterpret_cast<float4*>(tb + kRowStep * kPitch16) = pf1;
         *reinterpret_cast<float4*>(tb + 2 * kRowStep * kPitch16) = pf2;
         *reinterpret_cast<float4*>(tb + 3 * kRowStep * kPitch16) = pf3;
-        // the stage's four tiles' norms, one slot a tile
+        // the stage's four tiles' accumulator starts -||x||^2 / 2, one slot a tile
         if (L2 && tid < kStage16)
-            tnorm[(kTilesPerStage16 * st + (tid >> 5)) & (kNormSlots16 - 1)][tid & 31] = pn;
+            tnorm[(kTilesPerStage16 * st + (tid >> 5)) & (kNormSlots16 - 1)][tid & 31] =
+                -0.5f * pn;
     };
 
     // prologue: stages 0 and 1 in LDS, ids of stage 2
@@ -233,12 +242,13 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         return (((int64_t)opaque(slot0 + 32 * qb) * a.splits + split) * 2 + h) * a.cap;
     };
 
-    // one row at or below block qb's pre-screen: the exact test and append. Past the
-    // region's capacity the count still grows (the select sees the overflow); with cand_dmin
-    // the region keeps its first cap rows and dmin the smallest key of the rows it drops,
-    // else the last slot is rewritten.
-    auto test_row = [&](auto qb_tag, float kv, int pos) __attribute__((always_inline)) {
+    // one row at or below block qb's pre-screen (d: its D): the exact test of its key and the
+    // append. Past the region's capacity the count still grows (the select sees the
+    // overflow); with cand_dmin the region keeps its first cap rows and dmin the smallest
+    // key of the rows it drops, else the last slot is rewritten.
+    auto test_row = [&](auto qb_tag, float d, int pos) __attribute__((always_inline)) {
         constexpr int qb = decltype(qb_tag)::value;
+        const float kv = kF * d;
         if (((kv < cthr[qb]) | ((kv == cthr[qb]) & (pos <= cpos[qb]))) & (kv <= gbound[qb])) {
             PX_DCHECK(a.dbg, kDbgCollect, qvalid[qb] && pos >= row0 && pos < row1);
             if (ccount[qb] < a.cap || !a.cand_dmin) {
@@ -253,34 +263,21 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
     };
     using Q0 = std::integral_constant<int, 0>;
     using Q1 = std::integral_constant<int, 1>;
-    // L2 drops the per-query ||q||^2 (it does not change a query's order, and the select
-    // re-ranks exactly); IP negates
-    auto key_of = [&](float dot, float nrm) __attribute__((always_inline)) {
-        return L2 ? __builtin_fmaf(-2.0f, dot, nrm) : -dot;
-    };
-    // every key of a tile in place (acc[qb][x]: row mfma_row(x, h))
-    auto all_keys = [&](f32x16 (&acc)[2], const float* tn) __attribute__((always_inline)) {
-#pragma unroll
-        for (int m4 = 0; m4 < 4; ++m4) {
-            float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (L2) nv = *reinterpret_cast<const float4*>(tn + 8 * m4 + 4 * h);
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                acc[qb][4 * m4 + 0] = key_of(acc[qb][4 * m4 + 0], nv.x);
-                acc[qb][4 * m4 + 1] = key_of(acc[qb][4 * m4 + 1], nv.y);
-                acc[qb][4 * m4 + 2] = key_of(acc[qb][4 * m4 + 2], nv.z);
-                acc[qb][4 * m4 + 3] = key_of(acc[qb][4 * m4 + 3], nv.w);
-            }
-        }
-    };
+    // key = f D (L2: ||x||^2 - 2 q.x, without the per-query ||q||^2, which does not change a
+    // query's order, the select re-ranking exactly; IP: -q.x); a key is at or below ctest
+    // exactly when D is at or above nct = ctest / f
+    auto nct_of = [&](int qb) __attribute__((always_inline)) { return ctest[qb] * (1.0f / kF); };
+    float nct[2] = {nct_of(0), nct_of(1)};
     // DYN, a split's first tile (keys in place): its kl-th smallest key bounds the split,
     // taken where some query of the wave has no threshold
     auto first_tile_bound = [&](f32x16 (&acc)[2], int rem) __attribute__((always_inline)) {
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
             if (__ballot(qvalid[qb] && cthr[qb] == kInf)) {
-                gbound[qb] = fminf(gbound[qb], first_tile_kth16(acc[qb], rem, qvalid[qb], a.kl));
+                gbound[qb] =
+                    fminf(gbound[qb], first_tile_kth16(acc[qb], kF, rem, qvalid[qb], a.kl));
                 ctest[qb] = fminf(cthr[qb], gbound[qb]);
+                nct[qb] = nct_of(qb);
             }
         }
     };
@@ -303,13 +300,36 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
     auto tile_at = [&](int buf, int sub) __attribute__((always_inline)) {
         return tile[buf] + (sub * kTile16 + j) * kPitch16 + h * 16;
     };
+    // L2: tile t's accumulator starts, -||x||^2 / 2 of its rows in the MFMA result's layout
+    // (acc[x]: row mfma_row(x, h), so four contiguous values a 4-register group), the same for
+    // both query blocks. Read a tile ahead into the set the tile will use (it holds nothing
+    // live by then); the lane offset is opaque so that each block's copy is its own LDS
+    // read rather than one read and sixteen register copies.
+    auto load_start = [&](int t, f32x16 (&acc)[2]) __attribute__((always_inline)) {
+        if constexpr (L2) {
+            const float* slot = tnorm[t & (kNormSlots16 - 1)];
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                const float* tn = slot + opaque(4 * h);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    const float4 v = *reinterpret_cast<const float4*>(tn + 8 * m);
+                    acc[qb][4 * m + 0] = v.x;
+                    acc[qb][4 * m + 1] = v.y;
+                    acc[qb][4 * m + 2] = v.z;
+                    acc[qb][4 * m + 3] = v.w;
+                }
+            }
+        }
+    };
     f16x8 an = *reinterpret_cast<const f16x8*>(tile_at(0, 0));  // the next tile's group 0
+    load_start(0, accA);
     int rb_cur = 0;  // LDS buffer of the current stage
     int s = 0;       // stage index
 
-    // One tile t (sub = t % 4 of stage s): its MFMAs into cur; TEST (t > 0): the keys of
-    // tile t - 1, in prev, formed and tested between them. sub 0 begins the stage (its global
-    // loads); sub 3, or the split's last tile, ends it (the sync and commit).
+    // One tile t (sub = t % 4 of stage s): its MFMAs into cur; TEST (t > 0): tile t - 1's D
+    // values, in prev, tested between them. sub 0 begins the stage (its global loads); sub 3,
+    // or the split's last tile, ends it (the sync and commit).
     auto run_tile = [&](auto test_tag, auto first_tag, auto sub_tag, int t, f32x16 (&cur)[2],
                         f32x16 (&prev)[2]) __attribute__((always_inline)) {
         constexpr bool TEST = decltype(test_tag)::value;
@@ -320,27 +340,20 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
             fetch();
             stage_ids(s + 3);
         }
-        // DYN, the split's first tile (FIRST: t == 1): all its keys and its own bound first
-        constexpr bool keys_ready = DYN && TEST && decltype(first_tag)::value;
-        const float* tn = tnorm[(t - 1) & (kNormSlots16 - 1)];
-        if constexpr (keys_ready) {
-            all_keys(prev, tn);
-            first_tile_bound(prev, kTile16);
-        }
+        // DYN, the split's first tile (FIRST: t == 1): its own bound before its tests
+        constexpr bool first = DYN && TEST && decltype(first_tag)::value;
+        if constexpr (first) first_tile_bound(prev, kTile16);
         const int pt0 = row0 + (t - 1) * kTile16;  // first position of tile t - 1
-        float vmin0 = kInf, vmin1 = kInf;          // DYN: smallest key of tile t - 1, a block
+        float vmax0 = -kInf, vmax1 = -kInf;        // DYN: largest D of tile t - 1, a block
         const char* ta = tile_at(rb_cur, SUB);
-        // A operands are read two groups ahead (xa: group g + 1, xb: g + 2), norms one
-        // (nvn: the rows of group g + 1's keys, 8 m + 4 h .. + 3 with m = (g + 1) % 4)
+        // A operands are read two groups ahead (xa: group g + 1, xb: g + 2)
         f16x8 xa = an, xb = *reinterpret_cast<const f16x8*>(ta + 32);
-        float4 nv = make_float4(0.f, 0.f, 0.f, 0.f), nvn = nv;
-        if constexpr (TEST && L2 && !keys_ready) nvn = *reinterpret_cast<const float4*>(tn + 4 * h);
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             const f16x8 x = xa;
             xa = xb;
             if (g + 2 < NG) xb = *reinterpret_cast<const f16x8*>(ta + (g + 2) * 32);
-            if (g == 0) {
+            if (g == 0 && !L2) {
                 cur[0] = mfma16z(x, b0[0]);
                 cur[1] = mfma16z(x, b1[0]);
             } else {
@@ -348,34 +361,25 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
                 cur[1] = mfma16(x, b1[g], cur[1]);
             }
             if constexpr (TEST) {
-                // keys 4 m .. 4 m + 3 (m = g % 4) of block g / 4: rows 8 m + 4 h .. + 3
-                const int m = g & 3, r = 4 * m;
-                f32x16& pv = g < 4 ? prev[0] : prev[1];
-                if (!keys_ready) {
-                    if (L2) {
-                        nv = nvn;
-                        if (g + 1 < NG)
-                            nvn = *reinterpret_cast<const float4*>(tn + 8 * ((g + 1) & 3) + 4 * h);
-                    }
-                    const float nn[4] = {nv.x, nv.y, nv.z, nv.w};
+                // D 4 m .. 4 m + 3 (m = g % 4) of block g / 4: rows 8 m + 4 h .. + 3; the
+                // group's largest against nct (the tests are rare: the branch falls through)
+                const int r = 4 * (g & 3);
+                const f32x16& pv = g < 4 ? prev[0] : prev[1];
+                float dv[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) pv[r + e] = key_of(pv[r + e], nn[e]);
-                }
-                float kv[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) kv[e] = pv[r + e];
-                const float kmin = fminf(fminf(kv[0], kv[1]), fminf(kv[2], kv[3]));
+                for (int e = 0; e < 4; ++e) dv[e] = pv[r + e];
+                const float dmax = fmaxf(fmaxf(dv[0], dv[1]), fmaxf(dv[2], dv[3]));
                 if (g < 4) {
-                    if constexpr (DYN) vmin0 = fminf(vmin0, kmin);
-                    if (__ballot(kmin <= ctest[0])) {
+                    if constexpr (DYN) vmax0 = fmaxf(vmax0, dmax);
+                    if (__builtin_expect(__ballot(dmax >= nct[0]) != 0, 0)) {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) test_row(Q0{}, kv[e], pt0 + mfma_row(r + e, h));
+                        for (int e = 0; e < 4; ++e) test_row(Q0{}, dv[e], pt0 + mfma_row(r + e, h));
                     }
                 } else {
-                    if constexpr (DYN) vmin1 = fminf(vmin1, kmin);
-                    if (__ballot(kmin <= ctest[1])) {
+                    if constexpr (DYN) vmax1 = fmaxf(vmax1, dmax);
+                    if (__builtin_expect(__ballot(dmax >= nct[1]) != 0, 0)) {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) test_row(Q1{}, kv[e], pt0 + mfma_row(r + e, h));
+                        for (int e = 0; e < 4; ++e) test_row(Q1{}, dv[e], pt0 + mfma_row(r + e, h));
                     }
                 }
             }
@@ -385,7 +389,7 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         __builtin_amdgcn_sched_barrier(0);
         bool pub0 = false, pub1 = false;
         if constexpr (TEST && DYN) {
-            const int tk0 = total_key(vmin0), tk1 = total_key(vmin1);
+            const int tk0 = total_key(kF * vmax0), tk1 = total_key(kF * vmax1);
             pub0 = qvalid[0] && tk0 < cpub[0];
             pub1 = qvalid[1] && tk1 < cpub[1];
             cpub[0] = pub0 ? tk0 : cpub[0];
@@ -400,8 +404,11 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
                 }
                 next_refresh = (t - 1) + max(1, (t - 1) >> 1);
             }
-            ctest[0] = fminf(cthr[0], gbound[0]);
-            ctest[1] = fminf(cthr[1], gbound[1]);
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) {
+                ctest[qb] = fminf(cthr[qb], gbound[qb]);
+                nct[qb] = nct_of(qb);
+            }
         }
         auto publish_minima = [&]() __attribute__((always_inline)) {
             if constexpr (DYN) {
@@ -411,19 +418,24 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         };
         if constexpr (SUB < kTilesPerStage16 - 1) {
             if (t + 1 < ntiles) {
-                // the stage's next tile: its first A operand from the same buffer, no sync
+                // the stage's next tile: its first A operand and accumulator starts from the
+                // same buffer, no sync
                 an = *reinterpret_cast<const f16x8*>(tile_at(rb_cur, SUB + 1));
+                load_start(t + 1, prev);
                 publish_minima();
                 return;
             }
         }
-        // the next stage's first A operand and this wave's part of stage s + 2, once every
-        // wave has committed stage s + 1
+        // the next stage's first A operand and accumulator starts, and this wave's part of
+        // stage s + 2, once every wave has committed stage s + 1
         wait_committed(s + 1);
         pair_priority(__hip_atomic_load(committed + (wave ^ 4), __ATOMIC_RELAXED,
                                         __HIP_MEMORY_SCOPE_WORKGROUP),
                       s + 1);
-        if (s + 1 < nstages) an = *reinterpret_cast<const f16x8*>(tile_at(rb_nxt, 0));
+        if (s + 1 < nstages) {
+            an = *reinterpret_cast<const f16x8*>(tile_at(rb_nxt, 0));
+            load_start(t + 1, prev);
+        }
         commit(s + 2, rb_wr);
         stage_publish(committed, wave, lane, s + 2);
         // published after the commit, whose waits then do not wait for the atomics
@@ -449,21 +461,20 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         if (t + 3 < ntiles) run_tile(T{}, F{}, S3{}, t + 3, accB, accA);
     }
 
-    // the last tile's keys: all at once, with no MFMAs to hide behind
+    // the last tile's D values: all tested at once, with no MFMAs to hide behind
     auto finish = [&](f32x16 (&acc)[2]) __attribute__((always_inline)) {
         const int tl = ntiles - 1;
         const int t0 = row0 + tl * kTile16;
         const int rem = min(row1 - t0, kTile16);
-        all_keys(acc, tnorm[tl & (kNormSlots16 - 1)]);
         if constexpr (DYN) {
             if (tl == 0) first_tile_bound(acc, rem);
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                float vmin = kInf;
+                float vmax = -kInf;
 #pragma unroll
                 for (int x = 0; x < 16; ++x)
-                    vmin = mfma_row(x, h) < rem ? fminf(vmin, acc[qb][x]) : vmin;
-                const int tk = total_key(vmin);
+                    vmax = mfma_row(x, h) < rem ? fmaxf(vmax, acc[qb][x]) : vmax;
+                const int tk = total_key(kF * vmax);
                 if (qvalid[qb] && tk < cpub[qb])
                     atomicMin(gbest_of(qb) + (int64_t)(split & 31) * a.gbest_ld, tk);
             }
@@ -472,17 +483,17 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         for (int x = 0; x < 16; x += 2) {
             const int o0 = mfma_row(x, h), o1 = mfma_row(x + 1, h);
             {
-                const float k0 = acc[0][x], k1 = acc[0][x + 1];
-                if (__ballot((o0 < rem && k0 <= ctest[0]) || (o1 < rem && k1 <= ctest[0]))) {
-                    if (o0 < rem) test_row(Q0{}, k0, t0 + o0);
-                    if (o1 < rem) test_row(Q0{}, k1, t0 + o1);
+                const float d0 = acc[0][x], d1 = acc[0][x + 1];
+                if (__ballot((o0 < rem && d0 >= nct[0]) || (o1 < rem && d1 >= nct[0]))) {
+                    if (o0 < rem) test_row(Q0{}, d0, t0 + o0);
+                    if (o1 < rem) test_row(Q0{}, d1, t0 + o1);
                 }
             }
             {
-                const float k0 = acc[1][x], k1 = acc[1][x + 1];
-                if (__ballot((o0 < rem && k0 <= ctest[1]) || (o1 < rem && k1 <= ctest[1]))) {
-                    if (o0 < rem) test_row(Q1{}, k0, t0 + o0);
-                    if (o1 < rem) test_row(Q1{}, k1, t0 + o1);
+                const float d0 = acc[1][x], d1 = acc[1][x + 1];
+                if (__ballot((o0 < rem && d0 >= nct[1]) || (o1 < rem && d1 >= nct[1]))) {
+                    if (o0 < rem) test_row(Q1{}, d0, t0 + o0);
+                    if (o1 < rem) test_row(Q1{}, d1, t0 + o1);
                 }
             }
         }
