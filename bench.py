@@ -214,6 +214,7 @@ def read_counters(name: str, default_workload: bool):
 COUNTER_PROFILES = {
     (3, 1_000_000, 10_000, 10, "collect-bounded"):
         "flat_collect_scan_bounded_l2_1Mx128_q10k_k10_mfma_counters.md",
+    (3, 1_000_000, 10_000, 100, "collect-sampled"): "flat_collect_scan_l2_1Mx128_q10k_k100.md",
     (2, 100_000, 1_000, 10, "lists"): "flat_scan_kernel_ip_100kx384_q1k_k10_mfma_counters.md",
     (5, 10_000_000, 16_384, 100, "collect-sampled"):
         "flat_collect_scan_ip_10Mx384_q16k_k100_mask10_mfma_counters.md",
@@ -278,6 +279,7 @@ def host_buffer_qps(search, nq, reps=7):
 TRAFFIC_PROFILES = {
     (3, 1_000_000, 10_000, 10, "lists"): "flat_scan_kernel_l2_1Mx128_q10k_k10.md",
     (3, 1_000_000, 10_000, 10, "collect-bounded"): "flat_collect_scan_bounded_l2_1Mx128_q10k_k10.md",
+    (3, 1_000_000, 10_000, 100, "collect-sampled"): "flat_collect_scan_l2_1Mx128_q10k_k100.md",
     (2, 100_000, 1_000, 10, "lists"): "flat_scan_kernel_ip_100kx384_q1k_k10.md",
     (5, 10_000_000, 16_384, 100, "collect-sampled"):
         "flat_collect_scan_ip_10Mx384_q16k_k100_mask10.md",

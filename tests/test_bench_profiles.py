@@ -36,9 +36,11 @@ def test_traffic_only_for_the_profiled_run():
     assert bench.read_traffic(name, False) is None
     assert bench.read_traffic("", True) is None
     assert bench.read_traffic("no_such_profile.md", True) is None
-    # the headline's sampled path and other workloads have no traffic summary
+    # the headline's sampled path at k = 10 has no traffic summary; at k = 100 (its default
+    # path there, a default-run extra) it has one
     assert (3, 1_000_000, 10_000, 10, "collect-sampled") not in bench.TRAFFIC_PROFILES
-    assert (3, 1_000_000, 10_000, 100, "collect-sampled") not in bench.TRAFFIC_PROFILES
+    name = bench.TRAFFIC_PROFILES[(3, 1_000_000, 10_000, 100, "collect-sampled")]
+    assert bench.read_traffic(name, True) > 512_000_000
 
 
 @pytest.mark.parametrize("argv,env", [(["--gpus", "2"], {}), ([], {"WORLD_SIZE": "8"})])
