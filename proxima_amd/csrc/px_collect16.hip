@@ -92,6 +92,21 @@ __device__ __forceinline__ float first_tile_kth16(const f32x16& acc, float f, in
     return last == kNoKey ? __int_as_float(0x7f800000) : from_total_key(last);
 }
 
+// Largest of three / two D values as one v_max3_f32 / v_max_f32: fmaxf of values the compiler
+// cannot prove canonical (MFMA results) costs two canonicalising instructions more (IEEE
+// maxNum); D values are finite here (every row and query finite, checked on entry). The
+// operands are MFMA results of the previous tile, far past any MFMA-to-VALU hazard window.
+__device__ __forceinline__ float max3_raw(float a, float b, float c) {
+    float r;
+    asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+__device__ __forceinline__ float max_raw(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 template <bool L2, bool FILT, bool DYN>
 __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
     constexpr int NT = 512;
@@ -233,6 +248,9 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         cpub[qb] = kTotalKeyInf;  // DYN: this lane's published running minimum
     }
     int next_refresh = 0;  // DYN: tile index of the next refresh
+    // DYN: the largest D of the split's tiles tested so far, a block (its key f D is the
+    // running minimum a lane publishes)
+    float vmax0 = -kInf, vmax1 = -kInf;
     // the block's query's shared-bound slots: slot s at gbest_of(qb)[s * gbest_ld]
     auto gbest_of = [&](int qb) __attribute__((always_inline)) {
         return a.gbest + opaque(qidx[qb]);
@@ -344,7 +362,6 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         constexpr bool first = DYN && TEST && decltype(first_tag)::value;
         if constexpr (first) first_tile_bound(prev, kTile16);
         const int pt0 = row0 + (t - 1) * kTile16;  // first position of tile t - 1
-        float vmax0 = -kInf, vmax1 = -kInf;        // DYN: largest D of tile t - 1, a block
         const char* ta = tile_at(rb_cur, SUB);
         // A operands are read two groups ahead (xa: group g + 1, xb: g + 2)
         f16x8 xa = an, xb = *reinterpret_cast<const f16x8*>(ta + 32);
@@ -368,15 +385,15 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
                 float dv[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) dv[e] = pv[r + e];
-                const float dmax = fmaxf(fmaxf(dv[0], dv[1]), fmaxf(dv[2], dv[3]));
+                const float dmax = max_raw(max3_raw(dv[0], dv[1], dv[2]), dv[3]);
                 if (g < 4) {
-                    if constexpr (DYN) vmax0 = fmaxf(vmax0, dmax);
+                    if constexpr (DYN) vmax0 = max_raw(vmax0, dmax);
                     if (__builtin_expect(__ballot(dmax >= nct[0]) != 0, 0)) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) test_row(Q0{}, dv[e], pt0 + mfma_row(r + e, h));
                     }
                 } else {
-                    if constexpr (DYN) vmax1 = fmaxf(vmax1, dmax);
+                    if constexpr (DYN) vmax1 = max_raw(vmax1, dmax);
                     if (__builtin_expect(__ballot(dmax >= nct[1]) != 0, 0)) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e) test_row(Q1{}, dv[e], pt0 + mfma_row(r + e, h));
@@ -387,27 +404,28 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         // the LDS commit stays after the MFMAs: the scheduler would otherwise hoist it (to
         // shorten the prefetch registers' lives) and wait for the global loads there
         __builtin_amdgcn_sched_barrier(0);
+        // DYN, on a doubling schedule of tiles (t - 1 = 0, 1, 2, 4, 8, ...): each block's
+        // running minimum published (after this tile's commit) where it improved, and the
+        // bound refreshed from the 32 published slots, whose kl-th smallest bounds the best kl.
+        // Between those tiles only the running maxima are kept (one instruction a group):
+        // publishing every tile measured slower, the vector instructions being the bound.
         bool pub0 = false, pub1 = false;
         if constexpr (TEST && DYN) {
-            const int tk0 = total_key(kF * vmax0), tk1 = total_key(kF * vmax1);
-            pub0 = qvalid[0] && tk0 < cpub[0];
-            pub1 = qvalid[1] && tk1 < cpub[1];
-            cpub[0] = pub0 ? tk0 : cpub[0];
-            cpub[1] = pub1 ? tk1 : cpub[1];
             if (t - 1 == next_refresh) {
-                // each block's 32 published slots; their kl-th smallest bounds its best kl
+                const int tk0 = total_key(kF * vmax0), tk1 = total_key(kF * vmax1);
+                pub0 = qvalid[0] && tk0 < cpub[0];
+                pub1 = qvalid[1] && tk1 < cpub[1];
+                cpub[0] = pub0 ? tk0 : cpub[0];
+                cpub[1] = pub1 ? tk1 : cpub[1];
 #pragma unroll
                 for (int qb = 0; qb < 2; ++qb) {
                     int v[16];
                     load_slots16(gbest_of(qb), a.gbest_ld, h, v);
                     gbound[qb] = fminf(gbound[qb], from_total_key(kth_smallest32(v, a.kl)));
+                    ctest[qb] = fminf(cthr[qb], gbound[qb]);
+                    nct[qb] = nct_of(qb);
                 }
-                next_refresh = (t - 1) + max(1, (t - 1) >> 1);
-            }
-#pragma unroll
-            for (int qb = 0; qb < 2; ++qb) {
-                ctest[qb] = fminf(cthr[qb], gbound[qb]);
-                nct[qb] = nct_of(qb);
+                next_refresh = (t - 1) + max(1, t - 1);
             }
         }
         auto publish_minima = [&]() __attribute__((always_inline)) {
@@ -470,7 +488,8 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
             if (tl == 0) first_tile_bound(acc, rem);
 #pragma unroll
             for (int qb = 0; qb < 2; ++qb) {
-                float vmax = -kInf;
+                // the split's running maximum with the last tile's rows
+                float vmax = qb == 0 ? vmax0 : vmax1;
 #pragma unroll
                 for (int x = 0; x < 16; ++x)
                     vmax = mfma_row(x, h) < rem ? fmaxf(vmax, acc[qb][x]) : vmax;
