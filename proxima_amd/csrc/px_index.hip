@@ -772,6 +772,8 @@ int64_t collect_bytes() {
     return v;
 }
 constexpr int64_t kCollectBatch = 16384;
+// rows of the threshold sample that seeds a bounded first round (CollectJob::seed_rows)
+constexpr int64_t kSeedRows = 512;
 // Whether the MFMA collect scan also applies the splits' shared bound (default on;
 // PX_COLLECT_SHARED_BOUND=0 turns it off, for measurement; read once).
 bool shared_collect_bound() {
@@ -803,6 +805,11 @@ struct CollectJob {
     // ladder, every query's threshold +inf; bound_expect sizes its regions.
     bool bound_only = false;
     double bound_expect = 0.0;
+    // bound_only with seed_rows > 0: the first round's thresholds come from a sample of
+    // seed_rows rows (each query's k'-th smallest sampled key, so at least k' rows of the
+    // corpus are at or below it) and the shared bound applies on top. Before the bound
+    // tightens, a split's first tiles would otherwise pass about half their rows.
+    int64_t seed_rows = 0;
     // set by scan: the shared-bound slots of its launch (null when it applied none) and
     // its regions' smallest dropped keys (null when it keeps none: an overflow retries)
     const int* sel_gbest = nullptr;
@@ -826,7 +833,12 @@ int run_collect(CollectJob& j) {
 
     // expected candidates per query in the first round
     double expect = (double)n_eff;
-    if (n_eff <= kk || j.bound_only) {
+    if (n_eff > kk && j.bound_only && j.seed_rows > 0) {
+        const int64_t S = std::min(n_eff, j.seed_rows);
+        const int r0 = (int)std::min<int64_t>(S, kk);
+        PX_TRY(j.sample(S, r0, (int)std::min<int64_t>(S, 2 * kk + 8)));
+        expect = j.bound_expect;
+    } else if (n_eff <= kk || j.bound_only) {
         // every row is a candidate
         PX_HIP(px::launch_fill_int(ws.thr_k.as<int>(), nq, px::kTotalKeyInf, s));
         PX_HIP(px::launch_fill_int(ws.thr_p.as<int>(), nq, 0x7fffffff, s));
@@ -1263,6 +1275,9 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         // 2 k' + 1 (an overflowing region holds enough to tighten from)
         j.bound_only = collect_bound_only(n_eff, nq, j.kk, f->dp, cus, rowidx != nullptr);
         if (j.bound_only) f->last_path = PX_PATH_COLLECT_BOUNDED;
+        // the fp16 scan's first round seeded by a 512-row sample (its row tests were a tenth
+        // of the scan; the fp32 scan hides them behind its MFMAs)
+        if (j.bound_only && qh) j.seed_rows = kSeedRows;
         int64_t splits = 1, rps = 64;
         collect_splits(n_eff, nq, cus, &splits, &rps, qpb);
         j.bound_expect = (double)(2 * splits) *
