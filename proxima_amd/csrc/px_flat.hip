@@ -1705,9 +1705,82 @@ __global__ __launch_bounds__(1024) void flat_ladder_kernel(LadderArgs a) {
     }
 }
 
+// The ladder of a small sample (at most kSmallLadder keys a query, the seed of a bounded
+// round): one wave a query sorts its keys in registers (bitonic, eight a lane) and takes each
+// rung's rank-th smallest key exactly, where flat_ladder_kernel's 1,024 threads a query
+// would mostly idle (139 us for 10,000 queries of 512 keys). As there, +inf keys are left
+// out, a rung past the keys is +inf, and every position at the rung's key passes.
+constexpr int kSmallLadder = 512;
+__global__ __launch_bounds__(256) void flat_ladder_small_kernel(LadderArgs a) {
+    constexpr unsigned kNone = 0xffffffffu;
+    const int lane = threadIdx.x & 63;
+    const int q = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (q >= a.nq) return;  // whole waves; no barrier below
+    const float* base = a.keys + (int64_t)q * a.ld;
+    // element n = 8 lane + i of the sorting network in u[i]
+    unsigned u[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int e = lane + 64 * i;
+        const float kv = e < a.count ? base[e] : __int_as_float(0x7f800000);
+        u[i] = kv < __int_as_float(0x7f800000) ? (unsigned)total_key(kv) ^ 0x80000000u : kNone;
+    }
+#pragma unroll
+    for (int k = 2; k <= 512; k <<= 1) {
+#pragma unroll
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            if (j >= 8) {
+                // partner n ^ j is lane ^ (j / 8), same register; the lower of the two keeps
+                // the smaller key where the run ascends ((n & k) == 0)
+                const int pl = j >> 3;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const unsigned o = (unsigned)__shfl_xor((int)u[i], pl);
+                    const bool asc = ((8 * lane + i) & k) == 0;
+                    const bool keep_min = ((lane & pl) == 0) == asc;
+                    u[i] = keep_min ? min(u[i], o) : max(u[i], o);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    if ((i & j) == 0) {
+                        const bool asc = ((8 * lane + i) & k) == 0;
+                        const unsigned lo = min(u[i], u[i | j]), hi = max(u[i], u[i | j]);
+                        u[i] = asc ? lo : hi;
+                        u[i | j] = asc ? hi : lo;
+                    }
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < kRungs; ++r) {
+        const int n = a.ranks[r] - 1;  // uniform
+        unsigned mine = u[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) mine = (n & 7) == i ? u[i] : mine;
+        const unsigned v = (n >= 0 && n < 512) ? (unsigned)__shfl((int)mine, n >> 3) : kNone;
+        const int tk = v == kNone ? kTotalKeyInf : (int)(v ^ 0x80000000u);
+        if (lane == 0) {
+            a.ladder_key[(int64_t)q * kRungs + r] = tk;
+            a.ladder_pos[(int64_t)q * kRungs + r] = kIdNone;
+            if (r == 0) {
+                a.thr_key[q] = tk;
+                a.thr_pos[q] = kIdNone;
+                a.rung[q] = 0;
+            }
+        }
+    }
+}
+
 hipError_t launch_ladder(const LadderArgs& a, hipStream_t s) {
     if (a.nq <= 0) return hipSuccess;
     if (a.count > kMaxLadderEntries || a.ld < a.count) return hipErrorInvalidValue;
+    if (a.count <= kSmallLadder) {
+        hipLaunchKernelGGL(flat_ladder_small_kernel, dim3((unsigned)((a.nq + 3) / 4)), dim3(256),
+                           0, s, a);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(flat_ladder_kernel, dim3((unsigned)a.nq), dim3(1024), 0, s, a);
     return hipGetLastError();
 }
