@@ -34,6 +34,15 @@ __device__ __forceinline__ int total_key(float f) {
     return b ^ (int)(((unsigned)(b >> 31)) >> 1);
 }
 
+// The largest float below v (v not NaN; -inf stays -inf), so that for every non-NaN key,
+// key <= next_below(v) is exactly key < v (with -0 == +0 as float compares have them).
+__device__ __forceinline__ float next_below(float v) {
+    const int b = __float_as_int(v);
+    if (v > 0.f) return __int_as_float(b - 1);
+    if (v == 0.f) return __int_as_float((int)0x80000001);
+    return v == -__int_as_float(0x7f800000) ? v : __int_as_float(b + 1);
+}
+
 // Canonical candidate order: (key in total order, id) lexicographic.
 __device__ __forceinline__ bool cand_less(float ka, int ia, float kb, int ib) {
     int ta = total_key(ka), tb = total_key(kb);
@@ -82,8 +91,16 @@ __device__ __forceinline__ void list_insert(float* lk, IdT* li, int base, int kl
         const bool live = slot < kl;
         okey[u] = live ? lk[slot] : __int_as_float(0x7f800000);
         oid[u] = live ? id_load(li[slot], base) : kIdNone;
-        pkey[u] = (live && slot > 0) ? lk[slot - 1] : 0.f;
-        pid[u] = (live && slot > 0) ? id_load(li[slot - 1], base) : 0;
+        if constexpr (U == 1) {
+            // slot s - 1 is lane s - 1's okey: a DPP wave_shr:1 (lane 0 keeps 0; it never
+            // shifts) rather than two more LDS reads on the insertion's critical path
+            pkey[u] = __int_as_float(
+                __builtin_amdgcn_update_dpp(0, __float_as_int(okey[u]), 0x138, 0xF, 0xF, false));
+            pid[u] = __builtin_amdgcn_update_dpp(0, oid[u], 0x138, 0xF, 0xF, false);
+        } else {
+            pkey[u] = (live && slot > 0) ? lk[slot - 1] : 0.f;
+            pid[u] = (live && slot > 0) ? id_load(li[slot - 1], base) : 0;
+        }
         after[u] = __ballot(live && cand_less(ck, cid, okey[u], oid[u]));
     }
     int pos = kl;

@@ -239,9 +239,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     // 50% filter 12.87 -> 13.05)
     constexpr bool LDEFER = !COLLECT && !MULTI && !(FILT && L2);
     float pkey[COLLECT ? 32 : (LDEFER ? 16 : 1)];  // keys of the previous tile tested during this one
-    float pthr = -kInf;            // list mode: the previous tile's threshold ...
-    bool peq = false;              // ... and whether keys equal to it may still enter
-    int pt0 = 0, prem = 0;         // its first position and row count
+    float pthr = -kInf;            // list mode: the previous tile's threshold (as thr2 below)
+    int pt0 = 0, prem = 0;         // its first position and (collect mode) row count
     bool pend = false;             // some lane of the wave has a key at or below its threshold
     auto collect_x = [&](int x) {
         if constexpr (COLLECT) {
@@ -266,9 +265,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     auto list_x = [&](int x) {
         if constexpr (LDEFER) {
             const int r = x & 15;
-            const int off = 32 + mfma_row(r, h);
-            unsigned long long m =
-                __ballot(off < prem && (pkey[r] < pthr || (pkey[r] == pthr && peq)));
+            unsigned long long m = __ballot(pkey[r] <= pthr);
             while (m) {
                 const int src = __builtin_ctzll(m);
                 m &= m - 1;
@@ -647,7 +644,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                 }
             } else {
             // Padding queries get a threshold nothing passes; rows past the split's end
-            // (last tile only) are excluded in the slow path below.
+            // (last tile only) compare as NaN below.
             if (ti == next_refresh) {
                 // loaded here rather than ahead: refreshes are rare, and holding 16 more
                 // registers across the MFMAs would spill
@@ -674,16 +671,25 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                 const bool eq_ok = thr < tau_k || tau_i >= t0;
                 // rows of the first block now (all of them without LDEFER)
                 constexpr int XN = LDEFER ? 16 : 32;
+                // one compare a row: key <= thr2 is key < thr, or key == thr where equal
+                // keys may still enter; rows past the split's end (its last tile) are NaN,
+                // which no compare passes and fminf skips (the test took 17 instructions and
+                // two branches a row with the tie rule and the row bound in it)
+                const float thr2 = eq_ok ? thr : next_below(thr);
+                if (rem < kTileRows) {
+#pragma unroll
+                    for (int x = 0; x < 32; ++x)
+                        key[x] = (x >> 4) * 32 + mfma_row(x & 15, h) < rem
+                                     ? key[x] : __int_as_float(0x7fc00000);
+                }
                 float kmin0 = kInf;
 #pragma unroll
                 for (int x = 0; x < XN; ++x) kmin0 = fminf(kmin0, key[x]);
-                if (__ballot(kmin0 <= thr)) {
+                if (__ballot(kmin0 <= thr2)) {
 #pragma unroll
                     for (int x = 0; x < XN; ++x) {
                         const int rb = x >> 4, r = x & 15;
-                        const int off = rb * 32 + mfma_row(r, h);
-                        unsigned long long m = __ballot(
-                            off < rem && (key[x] < thr || (key[x] == thr && eq_ok)));
+                        unsigned long long m = __ballot(key[x] <= thr2);
                         while (m) {
                             const int src = __builtin_ctzll(m);
                             m &= m - 1;
@@ -714,10 +720,8 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
                         kmin1 = fminf(kmin1, key[16 + r]);
                     }
                     pt0 = (int)t0;
-                    prem = rem;
-                    pthr = thr;
-                    peq = eq_ok;
-                    pend = __ballot(kmin1 <= thr) != 0;
+                    pthr = thr2;
+                    pend = __ballot(kmin1 <= thr2) != 0;
                 }
             }
             }  // !COLLECT
