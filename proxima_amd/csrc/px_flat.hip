@@ -163,20 +163,29 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, j = lane & 31, h = lane >> 5;
     // Several query chunks (MULTI) over several rounds of workgroups (a.xcd_major): every
-    // stage reloads the next chunk of its 256 queries, so the workgroups an XCD runs at once
-    // should share query tiles. Blocks reach the eight XCDs round-robin by index (block b
-    // runs on XCD b % 8), so with the grid padded to a multiple of 8, block b takes position
-    // (b % 8) * (grid / 8) + b / 8 of the (query tile, split) order: each XCD works through a
-    // contiguous range, a query tile's splits together (10M x 384 with a 10% filter, 16,384
-    // queries: 288 -> 64 GB fetched a scan, 109.6 -> 108.5 ms; one round, 100k x 384 with
-    // 1,000 queries: 0.771 -> 0.779 ms, so not there).
-    int bid = (int)blockIdx.x;
+    // stage reloads the next chunk of its 256 queries from L2, and every query tile streams
+    // the rows of every split. Blocks reach the eight XCDs round-robin by index (block b runs
+    // on XCD b % 8), so with the grid padded to a multiple of 8, block b takes position
+    // p = (b % 8) * (grid / 8) + b / 8: each XCD works through a contiguous eighth of an
+    // order of the (query tile, split) pairs that takes the query tiles in groups of four,
+    // a group's splits in turn with its query tiles fastest. The 32 workgroups an XCD holds
+    // at once are then about four query tiles x eight splits: their query chunks (1.5 MB)
+    // stay in L2 and each row stream serves four of them (10M x 384 with a 10% filter, 16,384
+    // queries, HBM fetched a scan: blocks in index order 288 GB at 109.6 ms; a query tile's
+    // splits together 77 GB; eight query tiles x four splits 45 GB; four x eight 30 GB, these
+    // three within 0.5% of 106.3 ms: HBM is not the bound. One round, 100k x 384 with 1,000
+    // queries: 0.771 -> 0.779 ms, so not there).
+    int qt = (int)blockIdx.x / a.splits, split = (int)blockIdx.x % a.splits;
     if (MULTI && a.xcd_major) {
-        const int nblocks = ((a.nq + WAVES * 32 - 1) / (WAVES * 32)) * a.splits;
-        bid = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
-        if (bid >= nblocks) return;  // grid padding: before any barrier
+        const int qtiles = (a.nq + WAVES * 32 - 1) / (WAVES * 32);
+        const int p = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+        if (p >= qtiles * a.splits) return;  // grid padding: before any barrier
+        const int grp = p / (4 * a.splits);      // the group of (up to) four query tiles
+        const int w = min(4, qtiles - 4 * grp);  // its width: the last may be narrower
+        const int rem = p - grp * 4 * a.splits;  // < w splits
+        qt = grp * 4 + rem % w;
+        split = rem / w;
     }
-    const int qt = bid / a.splits, split = bid % a.splits;
     const int slot = qt * (WAVES * 32) + wave * 32 + j;
     const bool qvalid = slot < a.nq;
     // collect mode: a wave whose 32 queries are all padding (last query tile) skips its
