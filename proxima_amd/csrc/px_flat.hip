@@ -823,8 +823,418 @@ static hipError_t launch_scan_t(const FlatScanArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Lists of 32 over rows of 129-384 padded dims (list_resident_queries): 8 waves x 16 queries
+// a workgroup on v_mfma_f32_16x16x4f32, each wave holding all of its queries' dims in
+// registers (24-96 VGPRs), so no stage reloads a query chunk (flat_scan_kernel's multi-chunk
+// lists reload each lane's next 128 dims every stage: 16 loads and their address arithmetic).
+// Per stage (64 rows x 128 dims) a wave multiplies 4 row blocks of 16 rows by 8 groups of 16
+// dims, 4 MFMAs a group and block, the 4 blocks' accumulators interleaved. MFMA operands:
+// lane l = (i, d) with i = l % 16, d = l / 16; in group u, sub-step e, lane l feeds
+// A[i][d] = x[row 16 b + i][16 u + 4 d + e] and B[d][j] = q[j = l % 16][16 u + 4 d + e], so
+// both sides agree on the dim of every K slot and each lane reads 16 contiguous bytes a
+// group (b128 LDS reads; the 132-float pitch keeps them conflict-free); the result holds
+// D[4 d + r][j] in register r, so lane l has the keys of query l % 16 for rows
+// 16 b + 4 d + r, and the four lanes l % 16 + 16 d share a query. Staging, stage sync, the
+// shared bounds and the list insertions are flat_scan_kernel's (lists of 32, three stage
+// buffers, no barrier per stage), with two differences: a wave commits its part of stage
+// s + 2 before its tile epilogue rather than after it, so that its insertions hold up no
+// other wave (100k x 384, 1,000 queries: 0.709 -> 0.702 ms), and the waves of a SIMD keep
+// one issue priority (pair_priority measured 0.3% slower here). The split's first tile fills
+// the lists by ordered extraction over the query's four lanes. The queries are held scaled by the key's factor
+// (-2 for L2, -1 for IP; a power of two, so products and sums round as the unscaled ones
+// do, products in the subnormal range aside): the accumulators end as -2 q.x or -q.x, and
+// a key is one add of ||x||^2 (the single rounding of fma(-2, q.x, ||x||^2)) or the
+// accumulator itself; these keys only choose the candidates the merge re-ranks exactly
+// (k + 8 of them a split, against which their rounding is tested). FULL (dp =
+// NCH x 128): every dim group is real and the group loop runs unguarded, so the compiler
+// can keep LDS reads in flight ahead of the MFMAs (1.4% on 100k x 384).
+template <bool L2, bool FILT, int NCH, bool FULL>
+__global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
+    if (a.abort && *a.abort == a.abort_seq) return;
+    constexpr int WAVES = 8, NT = 512, KP = 32, QW = 16;
+    constexpr int kF4PerRow = kChunk / 4, kRowStep = NT / kF4PerRow, kPF = kTileRows / kRowStep;
+    constexpr int kBufs = 3, kNorms = 4;
+    static_assert(NCH >= 2 && NCH <= 3, "rows of 129-384 padded dims");
+    __shared__ __attribute__((aligned(16))) float tile[kBufs][kTileRows * kLdsStride];
+    __shared__ __attribute__((aligned(16))) float tnorm[kNorms][kTileRows];
+    __shared__ int committed[8];
+    __shared__ float lkeys[WAVES][QW][KP];
+    __shared__ unsigned short lids[WAVES][QW][KP];
+
+    const int tid = threadIdx.x;
+    const int wave = tid >> 6, lane = tid & 63, j = lane & 15, d = (lane >> 4) & 3, h = lane >> 5;
+    int qt = (int)blockIdx.x / a.splits, split = (int)blockIdx.x % a.splits;
+    if (a.xcd_major) {
+        // flat_scan_kernel's XCD-major order of (query tile, split) pairs
+        const int qtiles = (a.nq + WAVES * QW - 1) / (WAVES * QW);
+        const int p = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+        if (p >= qtiles * a.splits) return;  // grid padding: before any barrier
+        const int grp = p / (4 * a.splits), w = min(4, qtiles - 4 * grp);
+        const int rem = p - grp * 4 * a.splits;
+        qt = grp * 4 + rem % w;
+        split = rem / w;
+    }
+    const int slot = qt * (WAVES * QW) + wave * QW + j;
+    const bool qvalid = slot < a.nq;
+    const int q = slot;
+    const int64_t row0 = (int64_t)split * a.rows_per_split;
+    const int64_t row1 = min(a.n_eff, row0 + a.rows_per_split);
+    const float kInf = __int_as_float(0x7f800000);
+    const int64_t ntiles = (row1 - row0 + kTileRows - 1) / kTileRows;
+    const int64_t nstages = ntiles * NCH;
+    const int cc = tid % kF4PerRow, rr0 = tid / kF4PerRow;
+
+    for (int x = lane; x < QW * KP; x += 64) {
+        lkeys[wave][x / KP][x % KP] = kInf;
+        lids[wave][x / KP][x % KP] = 0xffff;
+    }
+    float tau_k = kInf;  // the list tail of query j (slot kl - 1), in all four of its lanes
+    int tau_i = kIdNone;
+    int published = 0x7fffffff;
+    const int pub_m = (a.kl + min(a.splits, 32) - 1) / min(a.splits, 32);
+    const int pub_rank = (a.kl + pub_m - 1) / pub_m;
+    int published_best = kTotalKeyInf;
+    float gbound = kInf;
+    int64_t next_refresh = 1;
+    int* gtau = a.gtau + (qvalid ? q : 0);
+    int* gbest = a.gbest + (qvalid ? q : 0);
+    auto publish = [&]() {
+        const int tk = total_key(tau_k);
+        if (d == 0 && qvalid && tau_i != kIdNone && tk < published) {
+            atomicMin(gtau, tk);
+            published = tk;
+        }
+        const int bk = total_key(lkeys[wave][j][pub_m - 1]);
+        if (d == 0 && qvalid && bk < published_best) {
+            atomicMin(gbest + (int64_t)(split & 31) * a.gbest_ld, bk);
+            published_best = bk;
+        }
+    };
+
+    // the queries (B operands) times the key's factor, held for the whole scan: chunk c,
+    // group u: dims c 128 + 16 u + 4 d .. + 3 (whole float4s inside or past dp, dp being a
+    // multiple of 8)
+    float4 bq[NCH][8];
+    {
+        const float* qrow = a.queries + (int64_t)(qvalid ? q : 0) * a.dp;
+        const float f = L2 ? -2.0f : -1.0f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int dim = c * kChunk + 16 * u + 4 * d;
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (qvalid && dim < a.dp) v = *reinterpret_cast<const float4*>(qrow + dim);
+                bq[c][u] = make_float4(f * v.x, f * v.y, f * v.z, f * v.w);
+            }
+    }
+
+    auto zero_unless = [](bool keep, float4 v) {
+        v.x = keep ? v.x : 0.f;
+        v.y = keep ? v.y : 0.f;
+        v.z = keep ? v.z : 0.f;
+        v.w = keep ? v.w : 0.f;
+        return v;
+    };
+    int rid[kPF], pid;
+    auto tile_ids = [&](int64_t t) {
+        const int64_t t0 = row0 + t * kTileRows;
+#pragma unroll
+        for (int u = 0; u < kPF; ++u) {
+            const int64_t pos = t0 + rr0 + u * kRowStep;
+            const int v = FILT ? a.rowidx[min(pos, row1 - 1)] : (int)pos;
+            rid[u] = pos < row1 ? v : -1;
+            PX_DCHECK(a.dbg, kDbgFlat, pos >= row1 || (v >= 0 && v < a.rows));
+        }
+        const int64_t pos = t0 + tid;
+        const int v = FILT ? a.rowidx[min(pos, row1 - 1)] : (int)pos;
+        pid = (tid < kTileRows && pos < row1) ? v : -1;
+    };
+    float4 pf[kPF];
+    float pn = 0.f;
+    unsigned pvalid = 0;
+    auto fetch = [&](int c) {
+        const int f4r = min(kChunk, a.dp - c * kChunk) >> 2;
+        pvalid = 0;
+#pragma unroll
+        for (int u = 0; u < kPF; ++u) {
+            pf[u] = *reinterpret_cast<const float4*>(
+                a.corpus + (int64_t)max(rid[u], 0) * a.dp + c * kChunk + min(cc, f4r - 1) * 4);
+            pvalid |= (rid[u] >= 0 && cc < f4r) ? 1u << u : 0u;
+        }
+        if (L2) {
+            pn = a.norms[max(pid, 0)];
+            pvalid |= pid >= 0 ? 1u << kPF : 0u;
+        }
+    };
+    auto commit = [&](int sb, int c, int tp) {
+        char* tb = reinterpret_cast<char*>(tile[sb]);
+#pragma unroll
+        for (int u = 0; u < kPF; ++u)
+            *reinterpret_cast<float4*>(tb + (rr0 + u * kRowStep) * (kLdsStride * 4) + cc * 16) =
+                zero_unless((pvalid >> u) & 1u, pf[u]);
+        if (L2 && c == 0 && tid < kTileRows) tnorm[tp][tid] = (pvalid >> kPF) & 1u ? pn : 0.f;
+    };
+    auto next_stage = [&](int c, int64_t t, int& cn, int64_t& tn) {
+        cn = c + 1 == NCH ? 0 : c + 1;
+        tn = cn == 0 ? t + 1 : t;
+    };
+
+    if (nstages > 0) {
+        tile_ids(0);
+        fetch(0);
+        commit(0, 0, 0);
+        int c1, c2;
+        int64_t t1, t2;
+        next_stage(0, 0, c1, t1);
+        next_stage(c1, t1, c2, t2);
+        tile_ids(t1);
+        fetch(c1);
+        commit(1, c1, (int)(t1 & (kNorms - 1)));
+        tile_ids(t2);
+    }
+    if (tid < 8) committed[tid] = 1;
+    __syncthreads();
+    const unsigned caddr = (unsigned)(uintptr_t)(committed + (lane & 7));
+
+    // a wave whose 16 queries are all padding only helps stage the rows
+    if (qt * (WAVES * QW) + wave * QW >= a.nq) {
+        int c = 0;
+        int64_t t = 0;
+        int rb = 0;
+        for (int64_t s = 0; s < nstages; ++s) {
+            int c1, c2, c3;
+            int64_t t1, t2, t3;
+            next_stage(c, t, c1, t1);
+            next_stage(c1, t1, c2, t2);
+            next_stage(c2, t2, c3, t3);
+            fetch(c2);
+            tile_ids(t3);
+            if (stage_wait(caddr, (int)(s + 1), a.spin_limit) >= a.spin_limit && a.spin_fail &&
+                lane == 0)
+                atomicOr(a.spin_fail, 1);
+            commit(rb == 0 ? 2 : rb - 1, c2, (int)(t2 & (kNorms - 1)));
+            stage_publish(committed, wave, lane, (int)(s + 2));
+            rb = rb == 2 ? 0 : rb + 1;
+            c = c1;
+            t = t1;
+        }
+        return;
+    }
+
+    f32x4v acc[4];
+    int c = 0;
+    int64_t ti = 0;
+    int rb = 0;
+    for (int64_t s = 0; s < nstages; ++s) {
+        int c1, c2, c3;
+        int64_t t1, t2, t3;
+        next_stage(c, ti, c1, t1);
+        next_stage(c1, t1, c2, t2);
+        next_stage(c2, t2, c3, t3);
+        const int64_t t0 = row0 + ti * kTileRows;
+        int gt_raw = kTotalKeyInf;
+        if (c == NCH - 1)
+            gt_raw = __hip_atomic_load(gtau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        fetch(c2);
+        tile_ids(t3);
+        if (c == 0) {
+#pragma unroll
+            for (int b = 0; b < 4; ++b) acc[b] = (f32x4v){0.f, 0.f, 0.f, 0.f};
+        }
+        // 16-dim groups holding real dims (the tile is zero past them, and so are the
+        // queries' registers)
+        const int ng = FULL ? 8 : (min(kChunk, a.dp - c * kChunk) + 15) >> 4;
+        const float* tb = tile[rb] + j * kLdsStride + 4 * d;
+        auto mfma_chunk = [&](const float4 (&bc)[8]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (FULL || u < ng) {
+                    float4 av[4];
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        av[b] = *reinterpret_cast<const float4*>(tb + 16 * b * kLdsStride + 16 * u);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[b].x, bc[u].x, acc[b], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[b].y, bc[u].y, acc[b], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[b].z, bc[u].z, acc[b], 0, 0, 0);
+#pragma unroll
+                    for (int b = 0; b < 4; ++b)
+                        acc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[b].w, bc[u].w, acc[b], 0, 0, 0);
+                }
+            }
+        };
+        if (c == 0) mfma_chunk(bq[0]);
+        else if (NCH == 2 || c == 1) mfma_chunk(bq[1]);
+        else mfma_chunk(bq[NCH - 1]);
+
+        // every wave has committed stage s + 1, then this wave's part of stage s + 2
+        if (stage_wait(caddr, (int)(s + 1), a.spin_limit) >= a.spin_limit && a.spin_fail &&
+            lane == 0)
+            atomicOr(a.spin_fail, 1);
+        commit(rb == 0 ? 2 : rb - 1, c2, (int)(t2 & (kNorms - 1)));
+        stage_publish(committed, wave, lane, (int)(s + 2));
+        // the epilogue after the commit: one wave's insertions then hold up no other wave's
+        // next stage
+        if (c == NCH - 1) {
+            // keys of this lane's 16 rows (row 16 b + 4 d + r in key[4 b + r]); L2 drops the
+            // per-query ||q||^2 as flat_scan_kernel does
+            const float* tn = tnorm[ti & (kNorms - 1)];
+            float key[16];
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (L2) nv = *reinterpret_cast<const float4*>(tn + 16 * b + 4 * d);
+                const float nn[4] = {nv.x, nv.y, nv.z, nv.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) key[4 * b + r] = L2 ? acc[b][r] + nn[r] : acc[b][r];
+            }
+            if (ti == next_refresh) {
+                int v[16];
+                load_slots16(gbest, a.gbest_ld, h, v);
+                gbound = fminf(gbound, from_total_key(kth_smallest32(v, pub_rank)));
+                next_refresh = ti + max<int64_t>(1, ti >> 1);
+            }
+            const float thr = qvalid ? fminf(fminf(tau_k, from_total_key(gt_raw)), gbound) : -kInf;
+            const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
+            if (t0 == row0) {
+                // first tile: the query's best kl of its four lanes' 16 rows each, in
+                // ascending (key, row) order, one extraction a slot
+                constexpr int kNoKey = 0x7fffffff;
+                int tk[16];
+#pragma unroll
+                for (int x = 0; x < 16; ++x)
+                    tk[x] = (qvalid && 16 * (x >> 2) + 4 * d + (x & 3) < rem) ? total_key(key[x])
+                                                                             : kNoKey;
+                int last_t = kNoKey, last_i = kIdNone;
+                for (int r = 0; r < a.kl; ++r) {
+                    int bt = kNoKey, bx = 0;
+#pragma unroll
+                    for (int x = 0; x < 16; ++x) {
+                        const bool lt = tk[x] < bt;
+                        bt = lt ? tk[x] : bt;
+                        bx = lt ? x : bx;
+                    }
+                    const int bi = bt == kNoKey ? kIdNone
+                                                : (int)(t0 + 16 * (bx >> 2) + 4 * d + (bx & 3));
+                    // the smallest (key, row) over the four lanes of the query
+                    int wt = bt, wi = bi;
+#pragma unroll
+                    for (int m = 16; m <= 32; m <<= 1) {
+                        const int ot = __shfl_xor(wt, m), oi = __shfl_xor(wi, m);
+                        const bool take = ot < wt || (ot == wt && oi < wi);
+                        wt = take ? ot : wt;
+                        wi = take ? oi : wi;
+                    }
+                    if (__ballot(wt != kNoKey) == 0) break;  // fewer than kl rows anywhere
+                    const bool mine = bt != kNoKey && bt == wt && bi == wi;
+#pragma unroll
+                    for (int x = 0; x < 16; ++x) tk[x] = (mine && x == bx) ? kNoKey : tk[x];
+                    if (d == 0 && wt != kNoKey) {
+                        lkeys[wave][j][r] = from_total_key(wt);
+                        lids[wave][j][r] = (unsigned short)(wi - (int)row0);
+                    }
+                    last_t = wt;
+                    last_i = r == a.kl - 1 ? wi : kIdNone;
+                }
+                const bool full = last_i != kIdNone;
+                tau_k = full ? from_total_key(last_t) : kInf;
+                tau_i = full ? last_i : kIdNone;
+                publish();
+            } else {
+                const bool eq_ok = thr < tau_k || tau_i >= t0;
+                // one compare a row, as in flat_scan_kernel (rows past the split's end NaN)
+                const float thr2 = eq_ok ? thr : next_below(thr);
+                if (rem < kTileRows) {
+#pragma unroll
+                    for (int x = 0; x < 16; ++x)
+                        key[x] = 16 * (x >> 2) + 4 * d + (x & 3) < rem ? key[x]
+                                                                     : __int_as_float(0x7fc00000);
+                }
+                float kmin = kInf;
+#pragma unroll
+                for (int x = 0; x < 16; ++x) kmin = fminf(kmin, key[x]);
+                if (__ballot(kmin <= thr2)) {
+#pragma unroll
+                    for (int x = 0; x < 16; ++x) {
+                        unsigned long long m = __ballot(key[x] <= thr2);
+                        while (m) {
+                            const int src = __builtin_ctzll(m);
+                            m &= m - 1;
+                            const float ck = readlane_f(key[x], src);
+                            const int cid =
+                                (int)(t0 + 16 * (x >> 2) + 4 * ((src >> 4) & 3) + (x & 3));
+                            const float tk = readlane_f(tau_k, src);
+                            const int tid_ = readlane_i(tau_i, src);
+                            if (!cand_less(ck, cid, tk, tid_)) continue;
+                            const int ql = src & 15;
+                            float nk;
+                            int ni;
+                            list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], (int)row0,
+                                            a.kl, ck, cid, nk, ni);
+                            if (j == ql) {
+                                tau_k = nk;
+                                tau_i = ni;
+                            }
+                        }
+                    }
+                    publish();
+                }
+            }
+        }
+
+        rb = rb == 2 ? 0 : rb + 1;
+        c = c1;
+        ti = t1;
+    }
+
+    // this split's lists: part[q][split][0..kl)
+    const int qbase = qt * (WAVES * QW) + wave * QW;
+    for (int ql = 0; ql < QW; ++ql) {
+        const int qq = qbase + ql;
+        if (qq >= a.nq) break;
+        float* pk = a.part_keys + ((int64_t)qq * a.splits + split) * a.kl;
+        int* pi = a.part_ids + ((int64_t)qq * a.splits + split) * a.kl;
+        for (int s = lane; s < a.kl; s += 64) {
+            pk[s] = lkeys[wave][ql][s];
+            pi[s] = id_load(lids[wave][ql][s], (int)row0);
+            PX_DCHECK(a.dbg, kDbgFlat, pi[s] == kIdNone || (pi[s] >= row0 && pi[s] < row1));
+        }
+    }
+}
+
+bool list_resident_queries(int kp, int64_t dp) { return kp == 32 && dp > kChunk && dp <= 3 * kChunk; }
+int flat_list_queries_per_block(int kp, int64_t dp) {
+    return list_resident_queries(kp, dp) ? 128 : flat_queries_per_block(kp);
+}
+
+template <int NCH, bool FULL>
+static void launch_list16q_n(const FlatScanArgs& a, hipStream_t s) {
+    const int64_t qtiles = (a.nq + 127) / 128;
+    const dim3 grid((unsigned)(a.xcd_major ? (qtiles * a.splits + 7) / 8 * 8 : qtiles * a.splits));
+    if (a.metric == 0) {
+        if (a.rowidx) hipLaunchKernelGGL((flat_list16q_kernel<true, true, NCH, FULL>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((flat_list16q_kernel<true, false, NCH, FULL>), grid, dim3(512), 0, s, a);
+    } else {
+        if (a.rowidx) hipLaunchKernelGGL((flat_list16q_kernel<false, true, NCH, FULL>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((flat_list16q_kernel<false, false, NCH, FULL>), grid, dim3(512), 0, s, a);
+    }
+}
+
 hipError_t launch_flat_scan(const FlatScanArgs& a0, hipStream_t s) {
     const FlatScanArgs a = with_spin_limit(a0);
+    if (list_resident_queries(flat_list_capacity(a.kl), a.dp) && !a.corpus_h) {
+        if (a.dp == 3 * kChunk) launch_list16q_n<3, true>(a, s);
+        else if (a.dp > 2 * kChunk) launch_list16q_n<3, false>(a, s);
+        else if (a.dp == 2 * kChunk) launch_list16q_n<2, true>(a, s);
+        else launch_list16q_n<2, false>(a, s);
+        return hipGetLastError();
+    }
     switch (flat_list_capacity(a.kl)) {
         case 32: return launch_scan_t<32, flat_waves(32)>(a, s);
         case 56: return launch_scan_t<56, flat_waves(56)>(a, s);

@@ -723,10 +723,10 @@ struct ListPlan {
     int64_t rps = 64, groups = 1;
 };
 // max_splits (>= 1) caps the split count (the no-allocation entry point's fixed scratch).
-int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int cus, ListPlan* out, int64_t k,
-                   int64_t max_splits = INT32_MAX) {
+int plan_list_scan(int64_t n_eff, int64_t nq, int kl, int64_t dp, int cus, ListPlan* out,
+                   int64_t k, int64_t max_splits = INT32_MAX) {
     const int kp = px::flat_list_capacity(kl);
-    const int64_t qpb = px::flat_queries_per_block(kp);
+    const int64_t qpb = px::flat_list_queries_per_block(kp, dp);
     const int64_t groups = (nq + qpb - 1) / qpb;
     const bool narrow = px::flat_list_narrow_ids(kp);
     int splits = (int)std::min<int64_t>(choose_flat_splits(n_eff, groups, kl, cus, narrow),
@@ -1409,7 +1409,8 @@ int flat_run_lists(px_flat* f, const float* d_q, int64_t nq, int64_t k, int64_t 
     a.abort_seq = seq;
     a.spin_fail = b.spin;
     a.spin_limit = f->spin_limit;
-    a.xcd_major = xcd_major_for(a, px::flat_queries_per_block(kl), std::max(f->dev.cus, 1));
+    a.xcd_major = xcd_major_for(
+        a, px::flat_list_queries_per_block(px::flat_list_capacity(kl), f->dp), std::max(f->dev.cus, 1));
     a.corpus_h = qh ? f->d_xh : nullptr;
     a.queries_h = qh;
     if (n_eff > 0) PX_HIP(px::launch_flat_scan(a, s));
@@ -1550,7 +1551,7 @@ int flat_run_paths(px_flat* f, const float* d_q, int64_t nq, int64_t k, const ui
     }
     f->last_f16 = qh != nullptr;
     ListPlan lp;
-    PX_TRY(plan_list_scan(n_eff, nq, kl, f->dev.cus, &lp, k));
+    PX_TRY(plan_list_scan(n_eff, nq, kl, f->dp, f->dev.cus, &lp, k));
     PX_TRY(ws.part_k.reserve(sizeof(float) * nq * lp.splits * kl));
     PX_TRY(ws.part_i.reserve(sizeof(int) * nq * lp.splits * kl));
     PX_TRY(ws.gtau.reserve(sizeof(int) * nq));
@@ -2199,7 +2200,7 @@ int px_flat_search_device_noalloc(const px_flat* cf, const float* d_queries, int
     if (masked)
         PX_TRY(compact_mask_into(d_mask, n, rowidx, cscr, flag + 1, &h, nullptr, s, &n_eff));
     ListPlan lp;
-    PX_TRY(plan_list_scan(n_eff, nq, kl, f->dev.cus, &lp, k, max_splits));
+    PX_TRY(plan_list_scan(n_eff, nq, kl, f->dp, f->dev.cus, &lp, k, max_splits));
     ListBufs b{L.take<float>((size_t)(nq * lp.splits * kl)), nullptr, gtau, gbest, flag + 2,
                nullptr, nullptr};
     b.part_i = L.take<int>((size_t)(nq * lp.splits * kl));

@@ -88,6 +88,10 @@ struct FlatScanArgs {
 // Waves per workgroup and list capacity used for a list length kl.
 int flat_list_capacity(int kl);
 int flat_queries_per_block(int kp);
+// Lists of capacity kp over rows of dp padded dims: whether launch_flat_scan takes
+// flat_list16q_kernel (lists of 32, 129-384 dims), and the query slots a workgroup holds.
+bool list_resident_queries(int kp, int64_t dp);
+int flat_list_queries_per_block(int kp, int64_t dp);
 hipError_t launch_flat_scan(const FlatScanArgs& a, hipStream_t s);
 // Total-order int of +inf: the starting value of FlatScanArgs::gtau.
 constexpr int kTotalKeyInf = 0x7f800000;
