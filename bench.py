@@ -215,7 +215,7 @@ COUNTER_PROFILES = {
     (3, 1_000_000, 10_000, 10, "collect-bounded"):
         "flat_collect_scan_bounded_l2_1Mx128_q10k_k10_mfma_counters.md",
     (3, 1_000_000, 10_000, 100, "collect-sampled"): "flat_collect_scan_l2_1Mx128_q10k_k100.md",
-    (2, 100_000, 1_000, 10, "lists"): "flat_scan_kernel_ip_100kx384_q1k_k10_mfma_counters.md",
+    (2, 100_000, 1_000, 10, "lists"): "flat_list16q_kernel_ip_100kx384_q1k_k10_mfma_counters.md",
     (5, 10_000_000, 16_384, 100, "collect-sampled"):
         "flat_collect_scan_ip_10Mx384_q16k_k100_mask10_mfma_counters.md",
 }
@@ -280,7 +280,7 @@ TRAFFIC_PROFILES = {
     (3, 1_000_000, 10_000, 10, "lists"): "flat_scan_kernel_l2_1Mx128_q10k_k10.md",
     (3, 1_000_000, 10_000, 10, "collect-bounded"): "flat_collect_scan_bounded_l2_1Mx128_q10k_k10.md",
     (3, 1_000_000, 10_000, 100, "collect-sampled"): "flat_collect_scan_l2_1Mx128_q10k_k100.md",
-    (2, 100_000, 1_000, 10, "lists"): "flat_scan_kernel_ip_100kx384_q1k_k10.md",
+    (2, 100_000, 1_000, 10, "lists"): "flat_list16q_kernel_ip_100kx384_q1k_k10.md",
     (5, 10_000_000, 16_384, 100, "collect-sampled"):
         "flat_collect_scan_ip_10Mx384_q16k_k100_mask10.md",
 }
@@ -433,6 +433,10 @@ def bench_flat(args, dev):
     # rows of exactly 128 padded dims take flat_collect_kernel, other widths the collect mode
     # of flat_scan_kernel
     collect_kernel = "flat_collect_kernel" if (dim + 7) // 8 * 8 == 128 else "flat_scan_kernel"
+    # lists of 32 (k + 8 <= 32) over rows of 129-384 padded dims take flat_list16q_kernel (the
+    # queries resident in registers), other lists flat_scan_kernel
+    list_kernel = ("flat_list16q_kernel" if k + 8 <= 32 and 128 < (dim + 7) // 8 * 8 <= 384
+                   else "flat_scan_kernel")
     achieved = flops / (np.mean(scan_ms) * 1e-3) / 1e12
     headline = (c, n, nq, k) == (3, 1_000_000, 10_000, 10) and not args.sift
     desc = (f"FlatIndex exact {'L2' if l2 else 'inner product'}, corpus {n} x {dim} fp32 "
@@ -451,7 +455,7 @@ def bench_flat(args, dev):
                      "unit": "TFLOP/s", "frac": achieved / FP32_MFMA_PEAK_TFLOPS,
                      "traffic": read_traffic(TRAFFIC_PROFILES.get((c, n, nq, k, info["path"]), ""),
                                              not args.sift),
-                     "kernel": {"lists": "flat_scan_kernel (per-split lists)",
+                     "kernel": {"lists": f"{list_kernel} (per-split lists)",
                                 "collect-sampled": f"{collect_kernel} (threshold-collect: sample "
                                                    "scan, ladder and collect scan)",
                                 "collect-bounded": f"{collect_kernel} (threshold-collect: "
