@@ -549,193 +549,200 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
             }
         }
 
-        if (c == nch - 1 && wave_live) {
-            // Epilogue, branch-free: keys of the 32 rows this lane holds for query j.
-            // L2 drops the per-query constant ||q||^2 (it does not change a query's order;
-            // the merge re-ranks exactly), so key = ||x||^2 - 2 q.x; IP key = -q.x.
-            // (collect mode writes them straight into pkey, where the next tile's MFMA loop
-            // tests them: the previous tile's keys there have been tested already)
-            const float* tn = tnorm[ti & (kNorms - 1)];
-            float key_own[COLLECT ? 1 : 32];
-            auto& key = [&]() -> float(&)[32] {
-                if constexpr (COLLECT) return pkey;
-                else return key_own;
-            }();
-            float kmin = kInf;
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb) {
-#pragma unroll
-                for (int r4 = 0; r4 < 4; ++r4) {
-                    const int lr = rb * 32 + 8 * r4 + 4 * h;  // rows lr .. lr+3
-                    float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
-                    if (L2) nv = *reinterpret_cast<const float4*>(tn + lr);
-                    const float nn[4] = {nv.x, nv.y, nv.z, nv.w};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int r = 4 * r4 + e;
-                        const float dot = rb == 0 ? acc0[r] : acc1[r];
-                        const float kv = L2 ? __builtin_fmaf(-2.0f, dot, nn[e]) : -dot;
-                        key[rb * 16 + r] = kv;
-                        kmin = fminf(kmin, kv);
+        // The tile epilogue (keys, tests, list insertions). Lists of 32 and collect mode run it
+        // after their commit of stage s + 2, so that one wave's tests and insertions hold up no
+        // other wave's next stage (100k x 384 lists: 0.709 -> 0.702 ms on the resident-query
+        // kernel; 1M x 128 lists, 1,000 queries: 2.325 -> 2.313 ms); with a barrier per stage
+        // it runs before the commit, as the barrier waits for it either way.
+        auto tile_epilogue = [&]() __attribute__((always_inline)) {
+            if (c == nch - 1 && wave_live) {
+                // Epilogue, branch-free: keys of the 32 rows this lane holds for query j.
+                // L2 drops the per-query constant ||q||^2 (it does not change a query's order;
+                // the merge re-ranks exactly), so key = ||x||^2 - 2 q.x; IP key = -q.x.
+                // (collect mode writes them straight into pkey, where the next tile's MFMA loop
+                // tests them: the previous tile's keys there have been tested already)
+                const float* tn = tnorm[ti & (kNorms - 1)];
+                float key_own[COLLECT ? 1 : 32];
+                auto& key = [&]() -> float(&)[32] {
+                    if constexpr (COLLECT) return pkey;
+                    else return key_own;
+                }();
+                float kmin = kInf;
+    #pragma unroll
+                for (int rb = 0; rb < 2; ++rb) {
+    #pragma unroll
+                    for (int r4 = 0; r4 < 4; ++r4) {
+                        const int lr = rb * 32 + 8 * r4 + 4 * h;  // rows lr .. lr+3
+                        float4 nv = make_float4(0.f, 0.f, 0.f, 0.f);
+                        if (L2) nv = *reinterpret_cast<const float4*>(tn + lr);
+                        const float nn[4] = {nv.x, nv.y, nv.z, nv.w};
+    #pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const int r = 4 * r4 + e;
+                            const float dot = rb == 0 ? acc0[r] : acc1[r];
+                            const float kv = L2 ? __builtin_fmaf(-2.0f, dot, nn[e]) : -dot;
+                            key[rb * 16 + r] = kv;
+                            kmin = fminf(kmin, kv);
+                        }
                     }
                 }
-            }
-            if constexpr (COLLECT) {
-                const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
-                if (a.dense) {
-                    // every key of the tile, row-major by position (+inf past the split's
-                    // end), so that each query's keys are contiguous for the ladder: keys
-                    // 4 m .. 4 m + 3 of this lane are four consecutive rows
-                    if (qvalid) {
-                        float* dst = a.cand_keys + (int64_t)slot * a.dense_ld + t0;
-#pragma unroll
-                        for (int m = 0; m < 8; ++m) {
-                            float v[4];
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) {
-                                const int x = 4 * m + e;
-                                v[e] = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? key[x] : kInf;
+                if constexpr (COLLECT) {
+                    const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
+                    if (a.dense) {
+                        // every key of the tile, row-major by position (+inf past the split's
+                        // end), so that each query's keys are contiguous for the ladder: keys
+                        // 4 m .. 4 m + 3 of this lane are four consecutive rows
+                        if (qvalid) {
+                            float* dst = a.cand_keys + (int64_t)slot * a.dense_ld + t0;
+    #pragma unroll
+                            for (int m = 0; m < 8; ++m) {
+                                float v[4];
+    #pragma unroll
+                                for (int e = 0; e < 4; ++e) {
+                                    const int x = 4 * m + e;
+                                    v[e] = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? key[x] : kInf;
+                                }
+                                const int lr = (m >> 2) * 32 + 8 * (m & 3) + 4 * h;
+                                *reinterpret_cast<float4*>(dst + lr) = make_float4(v[0], v[1], v[2], v[3]);
                             }
-                            const int lr = (m >> 2) * 32 + 8 * (m & 3) + 4 * h;
-                            *reinterpret_cast<float4*>(dst + lr) = make_float4(v[0], v[1], v[2], v[3]);
                         }
+                    } else {
+                    // tested during the next tile's MFMAs (or after the last tile); with MULTI
+                    // (several chunks per tile, and the next query chunk held in registers) the
+                    // keys are tested here instead, so that they are not held across the MFMAs
+                    if (dyn) {
+                        // this lane's smallest key of the split's rows so far (the last tile
+                        // of a split may end early: rows past its end do not count)
+                        float vmin = kmin;
+                        if (rem < kTileRows) {
+                            vmin = kInf;
+    #pragma unroll
+                            for (int x = 0; x < 32; ++x)
+                                vmin = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? fminf(vmin, key[x])
+                                                                                 : vmin;
+                        }
+                        // (only where some query of the wave has no threshold: a sampled one
+                        // already bounds the first tile far below its k'-th key)
+                        if (t0 == row0 && __ballot(qvalid && cthr == kInf))
+                            gbound = first_tile_kth(key, rem, qvalid, a.kl);
+                        // published after the stage's commit: its waits then do not wait for the
+                        // atomic, which has the next tile's MFMAs to complete
+                        const int tk = total_key(vmin);
+                        pub_now = qvalid && tk < cpub;
+                        cpub = pub_now ? tk : cpub;
+                        if (ti == next_refresh) {
+                            int v[16];
+                            load_slots16(gbest, a.gbest_ld, h, v);
+                            gbound = fminf(gbound, from_total_key(kth_smallest32(v, a.kl)));
+                            // sparser than the lists' schedule: each refresh waits for its loads
+                            // in the epilogue (t -> t + t/4: 21.73 ms a scan on 1M x 128, t + t/2:
+                            // 21.58, t -> 2t: 21.58)
+                            next_refresh = ti + max<int64_t>(1, ti >> 1);
+                        }
+                    }
+                    ctest = fminf(cthr, gbound);
+                    pt0 = (int)t0;
+                    prem = rem;
+                    pend = __ballot(kmin <= ctest) != 0;
+                    if constexpr (MULTI) {
+                        if (pend) {
+    #pragma unroll
+                            for (int g = 0; g < 16; ++g) {
+                                if (__ballot(pkey[2 * g] <= ctest || pkey[2 * g + 1] <= ctest)) {
+                                    collect_x(2 * g);
+                                    collect_x(2 * g + 1);
+                                }
+                            }
+                        }
+                        pend = false;
+                    }
                     }
                 } else {
-                // tested during the next tile's MFMAs (or after the last tile); with MULTI
-                // (several chunks per tile, and the next query chunk held in registers) the
-                // keys are tested here instead, so that they are not held across the MFMAs
-                if (dyn) {
-                    // this lane's smallest key of the split's rows so far (the last tile
-                    // of a split may end early: rows past its end do not count)
-                    float vmin = kmin;
-                    if (rem < kTileRows) {
-                        vmin = kInf;
-#pragma unroll
-                        for (int x = 0; x < 32; ++x)
-                            vmin = (x >> 4) * 32 + mfma_row(x & 15, h) < rem ? fminf(vmin, key[x])
-                                                                             : vmin;
-                    }
-                    // (only where some query of the wave has no threshold: a sampled one
-                    // already bounds the first tile far below its k'-th key)
-                    if (t0 == row0 && __ballot(qvalid && cthr == kInf))
-                        gbound = first_tile_kth(key, rem, qvalid, a.kl);
-                    // published after the stage's commit: its waits then do not wait for the
-                    // atomic, which has the next tile's MFMAs to complete
-                    const int tk = total_key(vmin);
-                    pub_now = qvalid && tk < cpub;
-                    cpub = pub_now ? tk : cpub;
-                    if (ti == next_refresh) {
-                        int v[16];
-                        load_slots16(gbest, a.gbest_ld, h, v);
-                        gbound = fminf(gbound, from_total_key(kth_smallest32(v, a.kl)));
-                        // sparser than the lists' schedule: each refresh waits for its loads
-                        // in the epilogue (t -> t + t/4: 21.73 ms a scan on 1M x 128, t + t/2:
-                        // 21.58, t -> 2t: 21.58)
-                        next_refresh = ti + max<int64_t>(1, ti >> 1);
-                    }
+                // Padding queries get a threshold nothing passes; rows past the split's end
+                // (last tile only) compare as NaN below.
+                if (ti == next_refresh) {
+                    // loaded here rather than ahead: refreshes are rare, and holding 16 more
+                    // registers across the MFMAs would spill
+                    int v[16];
+                    load_slots16(gbest, a.gbest_ld, h, v);
+                    gbound = fminf(gbound, from_total_key(kth_smallest32(v, pub_rank)));
+                    // t -> t + t/2: each refresh stalls both waves of a SIMD for its loads (on
+                    // 100k x 384 x 1,000 queries, 25 tiles a split: 0.81 -> 0.80 ms against
+                    // t + t/4; t -> 2t loses 1% on 1M x 128 and on 128 queries at k = 100)
+                    next_refresh = ti + max<int64_t>(1, ti >> 1);
                 }
-                ctest = fminf(cthr, gbound);
-                pt0 = (int)t0;
-                prem = rem;
-                pend = __ballot(kmin <= ctest) != 0;
-                if constexpr (MULTI) {
-                    if (pend) {
-#pragma unroll
-                        for (int g = 0; g < 16; ++g) {
-                            if (__ballot(pkey[2 * g] <= ctest || pkey[2 * g + 1] <= ctest)) {
-                                collect_x(2 * g);
-                                collect_x(2 * g + 1);
-                            }
-                        }
-                    }
-                    pend = false;
-                }
-                }
-            } else {
-            // Padding queries get a threshold nothing passes; rows past the split's end
-            // (last tile only) compare as NaN below.
-            if (ti == next_refresh) {
-                // loaded here rather than ahead: refreshes are rare, and holding 16 more
-                // registers across the MFMAs would spill
-                int v[16];
-                load_slots16(gbest, a.gbest_ld, h, v);
-                gbound = fminf(gbound, from_total_key(kth_smallest32(v, pub_rank)));
-                // t -> t + t/2: each refresh stalls both waves of a SIMD for its loads (on
-                // 100k x 384 x 1,000 queries, 25 tiles a split: 0.81 -> 0.80 ms against
-                // t + t/4; t -> 2t loses 1% on 1M x 128 and on 128 queries at k = 100)
-                next_refresh = ti + max<int64_t>(1, ti >> 1);
-            }
-            const float thr =
-                qvalid ? fminf(fminf(tau_k, from_total_key(gt_raw)), gbound) : -kInf;
-            if (t0 == row0) {
-                // First tile of the split: the lists are empty, so instead of inserting the
-                // tile's candidates one by one, sort them. Each lane sorts its 32 (key, row)
-                // pairs, merges them with its partner lane's (same query, other 32 rows)
-                // and the pair writes the query's best kl as its list.
-                first_tile_lists(key, t0, row1, qvalid, a.kl, &lkeys[wave][j][0],
-                                 &lids[wave][j][0], (int)row0, tau_k, tau_i);
-                publish();
-            } else {
-                const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
-                const bool eq_ok = thr < tau_k || tau_i >= t0;
-                // rows of the first block now (all of them without LDEFER)
-                constexpr int XN = LDEFER ? 16 : 32;
-                // one compare a row: key <= thr2 is key < thr, or key == thr where equal
-                // keys may still enter; rows past the split's end (its last tile) are NaN,
-                // which no compare passes and fminf skips (the test took 17 instructions and
-                // two branches a row with the tie rule and the row bound in it)
-                const float thr2 = eq_ok ? thr : next_below(thr);
-                if (rem < kTileRows) {
-#pragma unroll
-                    for (int x = 0; x < 32; ++x)
-                        key[x] = (x >> 4) * 32 + mfma_row(x & 15, h) < rem
-                                     ? key[x] : __int_as_float(0x7fc00000);
-                }
-                float kmin0 = kInf;
-#pragma unroll
-                for (int x = 0; x < XN; ++x) kmin0 = fminf(kmin0, key[x]);
-                if (__ballot(kmin0 <= thr2)) {
-#pragma unroll
-                    for (int x = 0; x < XN; ++x) {
-                        const int rb = x >> 4, r = x & 15;
-                        unsigned long long m = __ballot(key[x] <= thr2);
-                        while (m) {
-                            const int src = __builtin_ctzll(m);
-                            m &= m - 1;
-                            const float ck = readlane_f(key[x], src);
-                            const int cid = (int)(t0 + rb * 32 + mfma_row(r, src >> 5));
-                            const float tk = readlane_f(tau_k, src);
-                            const int ti = readlane_i(tau_i, src);
-                            if (!cand_less(ck, cid, tk, ti)) continue;
-                            const int ql = src & 31;
-                            float nk;
-                            int ni;
-                            list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], (int)row0,
-                                            a.kl, ck, cid, nk, ni);
-                            if (j == ql) {
-                                tau_k = nk;
-                                tau_i = ni;
-                            }
-                        }
-                    }
+                const float thr =
+                    qvalid ? fminf(fminf(tau_k, from_total_key(gt_raw)), gbound) : -kInf;
+                if (t0 == row0) {
+                    // First tile of the split: the lists are empty, so instead of inserting the
+                    // tile's candidates one by one, sort them. Each lane sorts its 32 (key, row)
+                    // pairs, merges them with its partner lane's (same query, other 32 rows)
+                    // and the pair writes the query's best kl as its list.
+                    first_tile_lists(key, t0, row1, qvalid, a.kl, &lkeys[wave][j][0],
+                                     &lids[wave][j][0], (int)row0, tau_k, tau_i);
                     publish();
-                }
-                if constexpr (LDEFER) {
-                    // the second block: during the next tile's MFMAs (or after the last)
-                    float kmin1 = kInf;
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        pkey[r] = key[16 + r];
-                        kmin1 = fminf(kmin1, key[16 + r]);
+                } else {
+                    const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
+                    const bool eq_ok = thr < tau_k || tau_i >= t0;
+                    // rows of the first block now (all of them without LDEFER)
+                    constexpr int XN = LDEFER ? 16 : 32;
+                    // one compare a row: key <= thr2 is key < thr, or key == thr where equal
+                    // keys may still enter; rows past the split's end (its last tile) are NaN,
+                    // which no compare passes and fminf skips (the test took 17 instructions and
+                    // two branches a row with the tie rule and the row bound in it)
+                    const float thr2 = eq_ok ? thr : next_below(thr);
+                    if (rem < kTileRows) {
+    #pragma unroll
+                        for (int x = 0; x < 32; ++x)
+                            key[x] = (x >> 4) * 32 + mfma_row(x & 15, h) < rem
+                                         ? key[x] : __int_as_float(0x7fc00000);
                     }
-                    pt0 = (int)t0;
-                    pthr = thr2;
-                    pend = __ballot(kmin1 <= thr2) != 0;
+                    float kmin0 = kInf;
+    #pragma unroll
+                    for (int x = 0; x < XN; ++x) kmin0 = fminf(kmin0, key[x]);
+                    if (__ballot(kmin0 <= thr2)) {
+    #pragma unroll
+                        for (int x = 0; x < XN; ++x) {
+                            const int rb = x >> 4, r = x & 15;
+                            unsigned long long m = __ballot(key[x] <= thr2);
+                            while (m) {
+                                const int src = __builtin_ctzll(m);
+                                m &= m - 1;
+                                const float ck = readlane_f(key[x], src);
+                                const int cid = (int)(t0 + rb * 32 + mfma_row(r, src >> 5));
+                                const float tk = readlane_f(tau_k, src);
+                                const int ti = readlane_i(tau_i, src);
+                                if (!cand_less(ck, cid, tk, ti)) continue;
+                                const int ql = src & 31;
+                                float nk;
+                                int ni;
+                                list_insert<KP>(&lkeys[wave][ql][0], &lids[wave][ql][0], (int)row0,
+                                                a.kl, ck, cid, nk, ni);
+                                if (j == ql) {
+                                    tau_k = nk;
+                                    tau_i = ni;
+                                }
+                            }
+                        }
+                        publish();
+                    }
+                    if constexpr (LDEFER) {
+                        // the second block: during the next tile's MFMAs (or after the last)
+                        float kmin1 = kInf;
+    #pragma unroll
+                        for (int r = 0; r < 16; ++r) {
+                            pkey[r] = key[16 + r];
+                            kmin1 = fminf(kmin1, key[16 + r]);
+                        }
+                        pt0 = (int)t0;
+                        pthr = thr2;
+                        pend = __ballot(kmin1 <= thr2) != 0;
+                    }
                 }
+                }  // !COLLECT
             }
-            }  // !COLLECT
-        }
-
+        };
+        if constexpr (!RELAXED) tile_epilogue();
         if constexpr (RELAXED) {
             // every wave has committed stage s + 1 (so none still reads stage s - 1, whose
             // buffer and norm slot stage s + 2 takes), then this wave's part of stage s + 2
@@ -750,6 +757,7 @@ __global__ __launch_bounds__(WAVES * 64) void flat_scan_kernel(FlatScanArgs a) {
         } else {
             commit((int)((s + 1) & 1), c1, (int)(t1 & 1));
         }
+        if constexpr (RELAXED) tile_epilogue();
         if (dyn && pub_now) {
             atomicMin(gbest + (int64_t)(split & 31) * a.gbest_ld, cpub);
             pub_now = false;
