@@ -553,9 +553,12 @@ __global__ __launch_bounds__(512) void flat_collect_kernel(FlatScanArgs a) {
 }  // namespace
 
 hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s) {
-    // rows of exactly 128 padded dims (one full chunk: the 1M x 128 workload); other widths
-    // take the collect mode of flat_scan_kernel
-    if (a.dp != kChunk) return launch_flat_collect_v1(a, s);
+    // rows of exactly 128 padded dims (one full chunk: the 1M x 128 workload); rows of 129-384
+    // take flat_list16q_kernel's collect mode (the queries resident in registers), except the
+    // dense threshold-sample scans; other widths the collect mode of flat_scan_kernel
+    if (a.dp != kChunk)
+        return !a.dense && collect_resident_queries(a.dp) ? launch_flat_collect16q(a, s)
+                                                          : launch_flat_collect_v1(a, s);
     const int64_t qtiles = (a.nq + 255) / 256;
     const dim3 grid((unsigned)(qtiles * a.splits)), block(512);
     const bool dyn = a.gbest != nullptr;

@@ -831,10 +831,11 @@ static hipError_t launch_scan_t(const FlatScanArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Lists of 32 over rows of 129-384 padded dims (list_resident_queries): 8 waves x 16 queries
-// a workgroup on v_mfma_f32_16x16x4f32, each wave holding all of its queries' dims in
-// registers (24-96 VGPRs), so no stage reloads a query chunk (flat_scan_kernel's multi-chunk
-// lists reload each lane's next 128 dims every stage: 16 loads and their address arithmetic).
+// Lists of 32 over rows of 129-384 padded dims (list_resident_queries), and the collect scan
+// of such rows (COLLECT): 8 waves x 16 queries a workgroup on v_mfma_f32_16x16x4f32, each
+// wave holding all of its queries' dims in registers (24-96 VGPRs), so no stage reloads a
+// query chunk (flat_scan_kernel's multi-chunk scans reload each lane's next 128 dims every
+// stage: 16 loads and their address arithmetic).
 // Per stage (64 rows x 128 dims) a wave multiplies 4 row blocks of 16 rows by 8 groups of 16
 // dims, 4 MFMAs a group and block, the 4 blocks' accumulators interleaved. MFMA operands:
 // lane l = (i, d) with i = l % 16, d = l / 16; in group u, sub-step e, lane l feeds
@@ -842,21 +843,25 @@ static hipError_t launch_scan_t(const FlatScanArgs& a, hipStream_t s) {
 // both sides agree on the dim of every K slot and each lane reads 16 contiguous bytes a
 // group (b128 LDS reads; the 132-float pitch keeps them conflict-free); the result holds
 // D[4 d + r][j] in register r, so lane l has the keys of query l % 16 for rows
-// 16 b + 4 d + r, and the four lanes l % 16 + 16 d share a query. Staging, stage sync, the
-// shared bounds and the list insertions are flat_scan_kernel's (lists of 32, three stage
-// buffers, no barrier per stage), with two differences: a wave commits its part of stage
-// s + 2 before its tile epilogue rather than after it, so that its insertions hold up no
-// other wave (100k x 384, 1,000 queries: 0.709 -> 0.702 ms), and the waves of a SIMD keep
-// one issue priority (pair_priority measured 0.3% slower here). The split's first tile fills
-// the lists by ordered extraction over the query's four lanes. The queries are held scaled by the key's factor
-// (-2 for L2, -1 for IP; a power of two, so products and sums round as the unscaled ones
-// do, products in the subnormal range aside): the accumulators end as -2 q.x or -q.x, and
-// a key is one add of ||x||^2 (the single rounding of fma(-2, q.x, ||x||^2)) or the
-// accumulator itself; these keys only choose the candidates the merge re-ranks exactly
-// (k + 8 of them a split, against which their rounding is tested). FULL (dp =
-// NCH x 128): every dim group is real and the group loop runs unguarded, so the compiler
-// can keep LDS reads in flight ahead of the MFMAs (1.4% on 100k x 384).
-template <bool L2, bool FILT, int NCH, bool FULL>
+// 16 b + 4 d + r, and the four lanes l % 16 + 16 d share a query.
+// The queries are held scaled by the key's factor (-2 for L2, -1 for IP; a power of two, so
+// products and sums round as the unscaled ones do, products in the subnormal range aside):
+// the accumulators end as -2 q.x or -q.x, and a key is one add of ||x||^2 (the single
+// rounding of fma(-2, q.x, ||x||^2)) or the accumulator itself; these keys only choose the
+// candidates the merge or the select re-ranks exactly. FULL (dp = NCH x 128): every dim
+// group is real and the group loop runs unguarded, so the compiler can keep LDS reads in
+// flight ahead of the MFMAs (1.4% on 100k x 384).
+// Staging, stage sync, the shared bounds and the list insertions are flat_scan_kernel's
+// (lists of 32, three stage buffers, no barrier per stage), with two differences: a wave
+// commits its part of stage s + 2 before its tile epilogue rather than after it, so that its
+// insertions hold up no other wave (100k x 384, 1,000 queries: 0.709 -> 0.702 ms), and the
+// waves of a SIMD keep one issue priority (pair_priority measured 0.3% slower here). The
+// split's first tile fills the lists by ordered extraction over the query's four lanes.
+// COLLECT (not the dense threshold-sample scans, which stay on flat_scan_kernel): per query a
+// threshold (key, position) and two regions a split, as flat_scan_kernel's collect mode lays
+// them out; region d / 2 is shared by the lanes d = 0, 1 (and 2, 3), which append a key
+// index's rows in lane order, each keeping the region's count.
+template <bool L2, bool FILT, int NCH, bool FULL, bool COLLECT>
 __global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
     if (a.abort && *a.abort == a.abort_seq) return;
     constexpr int WAVES = 8, NT = 512, KP = 32, QW = 16;
@@ -866,25 +871,28 @@ __global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
     __shared__ __attribute__((aligned(16))) float tile[kBufs][kTileRows * kLdsStride];
     __shared__ __attribute__((aligned(16))) float tnorm[kNorms][kTileRows];
     __shared__ int committed[8];
-    __shared__ float lkeys[WAVES][QW][KP];
-    __shared__ unsigned short lids[WAVES][QW][KP];
+    __shared__ float lkeys[COLLECT ? 1 : WAVES][QW][KP];
+    __shared__ unsigned short lids[COLLECT ? 1 : WAVES][QW][KP];
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6, lane = tid & 63, j = lane & 15, d = (lane >> 4) & 3, h = lane >> 5;
     int qt = (int)blockIdx.x / a.splits, split = (int)blockIdx.x % a.splits;
     if (a.xcd_major) {
-        // flat_scan_kernel's XCD-major order of (query tile, split) pairs
+        // flat_scan_kernel's XCD-major order of (query tile, split) pairs, in groups of 16
+        // query tiles: with the queries in registers, an XCD's L2 holds only row streams, so
+        // about 16 query tiles x 2 splits at once share each (10M x 384 with a 10% filter,
+        // 16,384 queries, HBM fetched a collect scan: groups of 4 56 GB, of 16 12.5 GB)
         const int qtiles = (a.nq + WAVES * QW - 1) / (WAVES * QW);
         const int p = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
         if (p >= qtiles * a.splits) return;  // grid padding: before any barrier
-        const int grp = p / (4 * a.splits), w = min(4, qtiles - 4 * grp);
-        const int rem = p - grp * 4 * a.splits;
-        qt = grp * 4 + rem % w;
+        const int grp = p / (16 * a.splits), w = min(16, qtiles - 16 * grp);
+        const int rem = p - grp * 16 * a.splits;
+        qt = grp * 16 + rem % w;
         split = rem / w;
     }
     const int slot = qt * (WAVES * QW) + wave * QW + j;
     const bool qvalid = slot < a.nq;
-    const int q = slot;
+    const int q = (COLLECT && a.qlist) ? a.qlist[qvalid ? slot : 0] : slot;
     const int64_t row0 = (int64_t)split * a.rows_per_split;
     const int64_t row1 = min(a.n_eff, row0 + a.rows_per_split);
     const float kInf = __int_as_float(0x7f800000);
@@ -892,9 +900,11 @@ __global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
     const int64_t nstages = ntiles * NCH;
     const int cc = tid % kF4PerRow, rr0 = tid / kF4PerRow;
 
-    for (int x = lane; x < QW * KP; x += 64) {
-        lkeys[wave][x / KP][x % KP] = kInf;
-        lids[wave][x / KP][x % KP] = 0xffff;
+    if constexpr (!COLLECT) {
+        for (int x = lane; x < QW * KP; x += 64) {
+            lkeys[wave][x / KP][x % KP] = kInf;
+            lids[wave][x / KP][x % KP] = 0xffff;
+        }
     }
     float tau_k = kInf;  // the list tail of query j (slot kl - 1), in all four of its lanes
     int tau_i = kIdNone;
@@ -904,8 +914,20 @@ __global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
     int published_best = kTotalKeyInf;
     float gbound = kInf;
     int64_t next_refresh = 1;
-    int* gtau = a.gtau + (qvalid ? q : 0);
-    int* gbest = a.gbest + (qvalid ? q : 0);
+    int* gtau = COLLECT ? nullptr : a.gtau + (qvalid ? q : 0);
+    int* gbest = COLLECT ? nullptr : a.gbest + (qvalid ? q : 0);
+    // collect mode: the query's threshold (key, position; nothing passes -inf) and the count
+    // of its region of this split: region h = d / 2, shared by lanes d = 2 h and 2 h + 1
+    // (rows 16 b + 8 h .. + 7 of each block: at most half the split's rows), the even lane's
+    // rows of a key index x first; both lanes keep the same count
+    float cthr = -kInf;
+    int cpos = -1, ccount = 0;
+    if constexpr (COLLECT) {
+        if (qvalid) {
+            cthr = from_total_key(a.thr_key[q]);
+            cpos = a.thr_pos[q];
+        }
+    }
     auto publish = [&]() {
         const int tk = total_key(tau_k);
         if (d == 0 && qvalid && tau_i != kIdNone && tk < published) {
@@ -1042,7 +1064,7 @@ __global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
         next_stage(c2, t2, c3, t3);
         const int64_t t0 = row0 + ti * kTileRows;
         int gt_raw = kTotalKeyInf;
-        if (c == NCH - 1)
+        if (!COLLECT && c == NCH - 1)
             gt_raw = __hip_atomic_load(gtau, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         fetch(c2);
         tile_ids(t3);
@@ -1102,6 +1124,39 @@ __global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) key[4 * b + r] = L2 ? acc[b][r] + nn[r] : acc[b][r];
             }
+            const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
+            if constexpr (COLLECT) {
+                // every row at or below the threshold (key, then position) is appended
+                if (rem < kTileRows) {
+#pragma unroll
+                    for (int x = 0; x < 16; ++x)
+                        key[x] = 16 * (x >> 2) + 4 * d + (x & 3) < rem ? key[x]
+                                                                     : __int_as_float(0x7fc00000);
+                }
+                float kmin = kInf;
+#pragma unroll
+                for (int x = 0; x < 16; ++x) kmin = fminf(kmin, key[x]);
+                if (__ballot(kmin <= cthr)) {
+                    const int64_t region =
+                        (((int64_t)slot * a.splits + split) * 2 + (d >> 1)) * a.cap;
+#pragma unroll
+                    for (int x = 0; x < 16; ++x) {
+                        const int pos = (int)(t0 + 16 * (x >> 2) + 4 * d + (x & 3));
+                        const bool p = key[x] < cthr || (key[x] == cthr && pos <= cpos);
+                        const unsigned long long m = __ballot(p);
+                        if (m) {
+                            const bool pp = (m >> (lane ^ 16)) & 1ull;  // the region's other lane
+                            const int at = ccount + ((d & 1) && pp ? 1 : 0);
+                            if (p && at < a.cap) {
+                                PX_DCHECK(a.dbg, kDbgFlat, qvalid && pos < a.n_eff);
+                                a.cand_keys[region + at] = key[x];
+                                a.cand_pos[region + at] = pos;
+                            }
+                            ccount += (p ? 1 : 0) + (pp ? 1 : 0);
+                        }
+                    }
+                }
+            } else {
             if (ti == next_refresh) {
                 int v[16];
                 load_slots16(gbest, a.gbest_ld, h, v);
@@ -1109,7 +1164,6 @@ __global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
                 next_refresh = ti + max<int64_t>(1, ti >> 1);
             }
             const float thr = qvalid ? fminf(fminf(tau_k, from_total_key(gt_raw)), gbound) : -kInf;
-            const int rem = (int)min<int64_t>(row1 - t0, (int64_t)kTileRows);
             if (t0 == row0) {
                 // first tile: the query's best kl of its four lanes' 16 rows each, in
                 // ascending (key, row) order, one extraction a slot
@@ -1194,6 +1248,7 @@ __global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
                     publish();
                 }
             }
+            }  // !COLLECT
         }
 
         rb = rb == 2 ? 0 : rb + 1;
@@ -1201,6 +1256,12 @@ __global__ __launch_bounds__(512) void flat_list16q_kernel(FlatScanArgs a) {
         ti = t1;
     }
 
+    if constexpr (COLLECT) {
+        // the region's count (past cap when it overflowed: the select sees it), from its even lane
+        if (qvalid && (d & 1) == 0)
+            a.cand_count[((int64_t)slot * a.splits + split) * 2 + (d >> 1)] = ccount;
+        return;
+    }
     // this split's lists: part[q][split][0..kl)
     const int qbase = qt * (WAVES * QW) + wave * QW;
     for (int ql = 0; ql < QW; ++ql) {
@@ -1221,26 +1282,38 @@ int flat_list_queries_per_block(int kp, int64_t dp) {
     return list_resident_queries(kp, dp) ? 128 : flat_queries_per_block(kp);
 }
 
-template <int NCH, bool FULL>
+template <int NCH, bool FULL, bool COLLECT>
 static void launch_list16q_n(const FlatScanArgs& a, hipStream_t s) {
     const int64_t qtiles = (a.nq + 127) / 128;
     const dim3 grid((unsigned)(a.xcd_major ? (qtiles * a.splits + 7) / 8 * 8 : qtiles * a.splits));
     if (a.metric == 0) {
-        if (a.rowidx) hipLaunchKernelGGL((flat_list16q_kernel<true, true, NCH, FULL>), grid, dim3(512), 0, s, a);
-        else hipLaunchKernelGGL((flat_list16q_kernel<true, false, NCH, FULL>), grid, dim3(512), 0, s, a);
+        if (a.rowidx) hipLaunchKernelGGL((flat_list16q_kernel<true, true, NCH, FULL, COLLECT>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((flat_list16q_kernel<true, false, NCH, FULL, COLLECT>), grid, dim3(512), 0, s, a);
     } else {
-        if (a.rowidx) hipLaunchKernelGGL((flat_list16q_kernel<false, true, NCH, FULL>), grid, dim3(512), 0, s, a);
-        else hipLaunchKernelGGL((flat_list16q_kernel<false, false, NCH, FULL>), grid, dim3(512), 0, s, a);
+        if (a.rowidx) hipLaunchKernelGGL((flat_list16q_kernel<false, true, NCH, FULL, COLLECT>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((flat_list16q_kernel<false, false, NCH, FULL, COLLECT>), grid, dim3(512), 0, s, a);
     }
+}
+template <bool COLLECT>
+static void launch_list16q(const FlatScanArgs& a, hipStream_t s) {
+    if (a.dp == 3 * kChunk) launch_list16q_n<3, true, COLLECT>(a, s);
+    else if (a.dp > 2 * kChunk) launch_list16q_n<3, false, COLLECT>(a, s);
+    else if (a.dp == 2 * kChunk) launch_list16q_n<2, true, COLLECT>(a, s);
+    else launch_list16q_n<2, false, COLLECT>(a, s);
+}
+bool collect_resident_queries(int64_t dp) { return dp > kChunk && dp <= 3 * kChunk; }
+hipError_t launch_flat_collect16q(const FlatScanArgs& a0, hipStream_t s) {
+    const FlatScanArgs a = with_spin_limit(a0);
+    if (a.dense || a.corpus_h || !collect_resident_queries(a.dp) || a.gbest)
+        return hipErrorInvalidValue;
+    launch_list16q<true>(a, s);
+    return hipGetLastError();
 }
 
 hipError_t launch_flat_scan(const FlatScanArgs& a0, hipStream_t s) {
     const FlatScanArgs a = with_spin_limit(a0);
     if (list_resident_queries(flat_list_capacity(a.kl), a.dp) && !a.corpus_h) {
-        if (a.dp == 3 * kChunk) launch_list16q_n<3, true>(a, s);
-        else if (a.dp > 2 * kChunk) launch_list16q_n<3, false>(a, s);
-        else if (a.dp == 2 * kChunk) launch_list16q_n<2, true>(a, s);
-        else launch_list16q_n<2, false>(a, s);
+        launch_list16q<false>(a, s);
         return hipGetLastError();
     }
     switch (flat_list_capacity(a.kl)) {

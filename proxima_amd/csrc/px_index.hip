@@ -1056,7 +1056,9 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
         f->scan_f16 && f->d_xh && f->dp == 128 && vec_collect(nq, f->dp) ? f->d_xh : nullptr;
     f->last_f16 = qh != nullptr || vh != nullptr;
     // query slots a workgroup of the (non-dense) MFMA collect scan
-    const int64_t qpb = qh ? px::flat_collect16_queries_per_block() : 256;
+    const int64_t qpb = qh                                      ? px::flat_collect16_queries_per_block()
+                        : px::collect_resident_queries(f->dp) ? 128
+                                                                : 256;
     CollectJob j;
     j.ws = &ws;
     j.stream = s;
@@ -1259,7 +1261,7 @@ int flat_run_collect_batch(px_flat* f, const float* d_q, int64_t nq, int64_t k, 
             a.kl = (int)j.kk;
             j.sel_gbest = a.gbest;
         }
-        a.xcd_major = xcd_major_for(a, 256, std::max(f->dev.cus, 1));
+        a.xcd_major = xcd_major_for(a, qpb, std::max(f->dev.cus, 1));
         PX_HIP(px::launch_flat_collect(a, s));
         if (round == 0) {
             f->timing.splits = (int)splits;

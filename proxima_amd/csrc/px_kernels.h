@@ -100,6 +100,10 @@ constexpr int kTotalKeyInf = 0x7f800000;
 // tight or too loose go round again.
 hipError_t launch_flat_collect(const FlatScanArgs& a, hipStream_t s);
 hipError_t launch_flat_collect_v1(const FlatScanArgs& a, hipStream_t s);
+// The collect scan of rows of 129-384 padded dims (not dense, no shared bound): 16 queries a
+// wave resident in registers, 128 query slots a workgroup (flat_list16q_kernel's collect mode).
+bool collect_resident_queries(int64_t dp);
+hipError_t launch_flat_collect16q(const FlatScanArgs& a, hipStream_t s);
 // The collect scan of fp16 rows (corpus_h and queries_h given, dp 128, not dense): 64
 // queries a wave, flat_collect16_queries_per_block() query slots a workgroup; called by
 // launch_flat_collect.
