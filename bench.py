@@ -430,9 +430,12 @@ def bench_flat(args, dev):
         idx._scan_f16(False)
 
     flops = 2.0 * nq * n_eff * dim
-    # rows of exactly 128 padded dims take flat_collect_kernel, other widths the collect mode
-    # of flat_scan_kernel
-    collect_kernel = "flat_collect_kernel" if (dim + 7) // 8 * 8 == 128 else "flat_scan_kernel"
+    # rows of exactly 128 padded dims take flat_collect_kernel, rows of 129-384 the collect
+    # mode of flat_list16q_kernel (the threshold sample's dense scan staying on
+    # flat_scan_kernel), other widths the collect mode of flat_scan_kernel
+    dp_ = (dim + 7) // 8 * 8
+    collect_kernel = ("flat_collect_kernel" if dp_ == 128 else
+                      "flat_list16q_kernel" if 128 < dp_ <= 384 else "flat_scan_kernel")
     # lists of 32 (k + 8 <= 32) over rows of 129-384 padded dims take flat_list16q_kernel (the
     # queries resident in registers), other lists flat_scan_kernel
     list_kernel = ("flat_list16q_kernel" if k + 8 <= 32 and 128 < (dim + 7) // 8 * 8 <= 384
