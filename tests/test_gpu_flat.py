@@ -76,7 +76,7 @@ def test_config3_reduced_sift_integers_bit_exact(gpu, k):
     assert np.array_equal(d, o_d)
 
 
-@pytest.mark.parametrize("dim", [1, 4, 7, 12, 24, 100, 130, 200, 384, 1000, 2051])
+@pytest.mark.parametrize("dim", [1, 4, 7, 12, 24, 100, 130, 200, 256, 384, 1000, 2051])
 def test_odd_dims(gpu, dim):
     data = datagen.gaussian(3000, dim, 11 + dim)
     q = datagen.gaussian(40, dim, 12 + dim)
@@ -84,9 +84,10 @@ def test_odd_dims(gpu, dim):
         _check(data, q, 10, metric)
 
 
-@pytest.mark.parametrize("dim", [3, 1000, 2051])
+@pytest.mark.parametrize("dim", [3, 200, 256, 384, 1000, 2051])
 def test_odd_dims_collect_path(gpu, dim):
-    # 260 queries and k = 20: the threshold-collect path, with 1 and with 8 / 17 query chunks
+    # 260 queries and k = 20: the threshold-collect path, with 1, 2-3 (the queries resident in
+    # registers) and 8 / 17 query chunks
     data = datagen.gaussian(4000, dim, 21 + dim)
     q = datagen.gaussian(260, dim, 22 + dim)
     for metric in (oracle.L2, oracle.IP):
@@ -98,6 +99,17 @@ def test_filtered(gpu, p):
     data = datagen.gaussian(20_000, 48, 5)
     q = datagen.gaussian(50, 48, 6)
     mask = datagen.mask(20_000, p, 7)
+    for metric in (oracle.L2, oracle.IP):
+        _check(data, q, 10, metric, mask=mask)
+
+
+@pytest.mark.parametrize("dim", [256, 384])
+def test_filtered_resident_query_lists(gpu, dim):
+    # lists of 32 over rows of 129-384 padded dims (the queries resident in registers, every
+    # chunk full) behind a filter, both metrics
+    data = datagen.gaussian(12_000, dim, 90 + dim)
+    q = datagen.gaussian(60, dim, 91 + dim)
+    mask = datagen.mask(12_000, 0.3, 92)
     for metric in (oracle.L2, oracle.IP):
         _check(data, q, 10, metric, mask=mask)
 

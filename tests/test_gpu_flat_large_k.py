@@ -169,6 +169,25 @@ def test_sample_far_overflow_round(gpu):
     assert rounds >= 2
 
 
+@pytest.mark.parametrize("dim", [200, 384])
+def test_resident_query_collect_overflow_rounds(gpu, dim):
+    # the far-overflow layout on rows of 129-384 padded dims, whose collect scan holds the
+    # queries in registers (four lanes a query, a pair of them sharing each region): every
+    # region overflows in the first round and the retry rounds list their queries; dim 200
+    # ends on a partial 128-dim chunk, 384 is three full ones
+    n, k = 40_000, 992
+    sampled = sample_positions(n, k + 8)
+    rng = np.random.default_rng(47)
+    data = rng.integers(0, 4, size=(n, dim)).astype(np.float32)
+    data[sampled] = 255.0
+    q = rng.integers(0, 3, size=(40, dim)).astype(np.float32)
+    idx, ids, d = _search(data, q, k, oracle.L2)
+    o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2)
+    assert np.array_equal(ids, o_ids) and np.array_equal(d, o_d)
+    assert idx._last_timing()["path"] == "collect-sampled"
+    assert _rounds(idx) >= 2
+
+
 def test_sample_near_underflow_rounds(gpu):
     # The sampled rows are the near ones: the sample's thresholds admit too few rows, the
     # ladder runs out, and the query finishes from an unbounded round.
@@ -338,9 +357,11 @@ def test_more_queries_than_one_collect_batch(gpu):
     assert rounds >= 1
 
 
-def test_retry_rounds_in_memory_bounded_chunks(gpu, tmp_path):
+@pytest.mark.parametrize("dim", [48, 384])
+def test_retry_rounds_in_memory_bounded_chunks(gpu, tmp_path, dim):
     # The overflow layout of test_sample_far_overflow_round with 300 queries and a 1 MB
-    # budget for the candidate regions: each retry round runs in several chunks of queries.
+    # budget for the candidate regions: each retry round runs in several chunks of queries
+    # (dim 384: the collect scan with the queries resident in registers).
     import os
     import subprocess
     import sys
@@ -355,10 +376,10 @@ from proxima_amd import FlatIndex, Metric, datagen
 n, k = 40_000, 992
 s = max(1, min(n, 16384, 80 * n // (k + 8)))
 rng = np.random.default_rng(45)
-data = rng.integers(0, 4, size=(n, 48)).astype(np.float32)
+data = rng.integers(0, 4, size=(n, {dim})).astype(np.float32)
 data[np.arange(s) * n // s] = 255.0  # the sampled positions, floor(i * n / s)
-q = rng.integers(0, 3, size=(300, 48)).astype(np.float32)
-idx = FlatIndex(48, Metric.L2)
+q = rng.integers(0, 3, size=(300, {dim})).astype(np.float32)
+idx = FlatIndex({dim}, Metric.L2)
 idx.add(data)
 ids, d = idx.search_batch(q, k=k)
 o_ids, o_d, _ = oracle.flat_search(data, q, k, oracle.L2)
