@@ -8,9 +8,11 @@ slots -- the padding waves of its last query tile stage the corpus and run ahead
 live ones -- give up, while every kernel still runs to its end. The search must then fail
 with PX_ERR_DEVICE ("stage sync"), leave its device outputs as they were, and a search on the
 same handle with the limit restored must equal the oracle (flat.rs:106-148 restated).
-Covered: the lists in fp32 and fp16, the bounded collect scan in fp32 and fp16, the sampled
-collect scan of 128-dim rows (its sample and collect scans) and of 384-dim rows
-(flat_scan_kernel's collect mode), the no-allocation entry point, and the host-array form.
+Covered: the lists in fp32 and fp16 (128-dim rows) and of 384-dim rows (flat_list16q_kernel,
+the queries resident in registers), the bounded collect scan in fp32 and fp16, the sampled
+collect scan of 128-dim rows (its sample and collect scans) and of 384-dim rows (its sample
+scan on flat_scan_kernel, its collect scan on flat_list16q_kernel), the no-allocation entry
+point, and the host-array form.
 """
 import ctypes
 
@@ -123,6 +125,14 @@ def test_lists_filtered_ip(dev):
                           "lists", mask=mask)
 
 
+def test_lists_384(dev):
+    # 40 queries on 384-dim rows: one query tile of 128 slots (16 a wave), five of its eight
+    # waves padding
+    data = datagen.unit_gaussian(200_000, 384, 518)
+    _give_up_then_recover(dev, data, datagen.unit_gaussian(40, 384, 519), 10, oracle.IP,
+                          "lists")
+
+
 def test_noalloc_lists(dev):
     data = datagen.gaussian(200_000, 128, 508)
     _give_up_then_recover(dev, data, datagen.gaussian(100, 128, 509), 10, oracle.L2, "lists",
@@ -151,7 +161,8 @@ def test_sampled_collect_128(dev):
 
 
 def test_sampled_collect_384(dev):
-    # rows of three 128-dim chunks: flat_scan_kernel's collect mode (k = 16, 300,000 rows)
+    # rows of three 128-dim chunks (k = 16, 300,000 rows): the sample scan on
+    # flat_scan_kernel's collect mode, the collect scan on flat_list16q_kernel's
     data = datagen.unit_gaussian(300_000, 384, 516)
     _give_up_then_recover(dev, data, datagen.unit_gaussian(300, 384, 517), 16, oracle.IP,
                           "collect-sampled")
