@@ -349,9 +349,10 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
     // values, in prev, tested between them. sub 0 begins the stage (its global loads); sub 3,
     // or the split's last tile, ends it (the sync and commit).
     auto run_tile = [&](auto test_tag, auto first_tag, auto sub_tag, int t, f32x16 (&cur)[2],
-                        f32x16 (&prev)[2]) __attribute__((always_inline)) {
+                        f32x16 (&prev)[2], auto whole_tag) __attribute__((always_inline)) {
         constexpr bool TEST = decltype(test_tag)::value;
         constexpr int SUB = decltype(sub_tag)::value;
+        constexpr bool WHOLE = decltype(whole_tag)::value;  // tile t + 1 is in this stage
         const int rb_nxt = rb_cur == kBufs16 - 1 ? 0 : rb_cur + 1;
         const int rb_wr = rb_nxt == kBufs16 - 1 ? 0 : rb_nxt + 1;
         if constexpr (SUB == 0) {
@@ -410,8 +411,10 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         // Between those tiles only the running maxima are kept (one instruction a group):
         // publishing every tile measured slower, the vector instructions being the bound.
         bool pub0 = false, pub1 = false;
+        bool refreshed = false;  // uniform: only a refresh tile publishes
         if constexpr (TEST && DYN) {
             if (t - 1 == next_refresh) {
+                refreshed = true;
                 const int tk0 = total_key(kF * vmax0), tk1 = total_key(kF * vmax1);
                 pub0 = qvalid[0] && tk0 < cpub[0];
                 pub1 = qvalid[1] && tk1 < cpub[1];
@@ -430,12 +433,14 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
         }
         auto publish_minima = [&]() __attribute__((always_inline)) {
             if constexpr (DYN) {
-                if (pub0) atomicMin(gbest_of(0) + (int64_t)(split & 31) * a.gbest_ld, cpub[0]);
-                if (pub1) atomicMin(gbest_of(1) + (int64_t)(split & 31) * a.gbest_ld, cpub[1]);
+                if (refreshed) {
+                    if (pub0) atomicMin(gbest_of(0) + (int64_t)(split & 31) * a.gbest_ld, cpub[0]);
+                    if (pub1) atomicMin(gbest_of(1) + (int64_t)(split & 31) * a.gbest_ld, cpub[1]);
+                }
             }
         };
         if constexpr (SUB < kTilesPerStage16 - 1) {
-            if (t + 1 < ntiles) {
+            if (WHOLE || t + 1 < ntiles) {
                 // the stage's next tile: its first A operand and accumulator starts from the
                 // same buffer, no sync
                 an = *reinterpret_cast<const f16x8*>(tile_at(rb_cur, SUB + 1));
@@ -468,15 +473,22 @@ __global__ __launch_bounds__(512) void flat_collect16_kernel(FlatScanArgs a) {
     using S2 = std::integral_constant<int, 2>;
     using S3 = std::integral_constant<int, 3>;
     // stage 0 (tile 1 tests tile 0, the split's first), then whole stages
-    run_tile(F{}, F{}, S0{}, 0, accA, accB);
-    if (ntiles > 1) run_tile(T{}, T{}, S1{}, 1, accB, accA);
-    if (ntiles > 2) run_tile(T{}, F{}, S2{}, 2, accA, accB);
-    if (ntiles > 3) run_tile(T{}, F{}, S3{}, 3, accB, accA);
-    for (int t = 4; t < ntiles; t += 4) {
-        run_tile(T{}, F{}, S0{}, t, accA, accB);
-        if (t + 1 < ntiles) run_tile(T{}, F{}, S1{}, t + 1, accB, accA);
-        if (t + 2 < ntiles) run_tile(T{}, F{}, S2{}, t + 2, accA, accB);
-        if (t + 3 < ntiles) run_tile(T{}, F{}, S3{}, t + 3, accB, accA);
+    run_tile(F{}, F{}, S0{}, 0, accA, accB, F{});
+    if (ntiles > 1) run_tile(T{}, T{}, S1{}, 1, accB, accA, F{});
+    if (ntiles > 2) run_tile(T{}, F{}, S2{}, 2, accA, accB, F{});
+    if (ntiles > 3) run_tile(T{}, F{}, S3{}, 3, accB, accA, F{});
+    // whole stages, then the split's last (partial) one with its per-tile checks
+    int tw = 4;
+    for (; tw + 4 <= ntiles; tw += 4) {
+        run_tile(T{}, F{}, S0{}, tw, accA, accB, T{});
+        run_tile(T{}, F{}, S1{}, tw + 1, accB, accA, T{});
+        run_tile(T{}, F{}, S2{}, tw + 2, accA, accB, T{});
+        run_tile(T{}, F{}, S3{}, tw + 3, accB, accA, F{});
+    }
+    if (tw < ntiles) {
+        run_tile(T{}, F{}, S0{}, tw, accA, accB, F{});
+        if (tw + 1 < ntiles) run_tile(T{}, F{}, S1{}, tw + 1, accB, accA, F{});
+        if (tw + 2 < ntiles) run_tile(T{}, F{}, S2{}, tw + 2, accA, accB, F{});
     }
 
     // the last tile's D values: all tested at once, with no MFMAs to hide behind
