@@ -102,6 +102,25 @@ def test_bounded_path(gpu, metric):
         assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
 
 
+@pytest.mark.parametrize("n", [57_560, 57_600, 57_686, 57_816, 59_000])
+def test_bounded_path_split_ends(gpu, n):
+    # the scan runs whole stages of four 32-row tiles, then a split's last partial stage with
+    # per-tile checks. Splits hold a multiple of 64 rows (an even tile count); with 2,048
+    # queries these row counts give 60-62 splits of 960 rows (30 tiles: two past the last
+    # whole stage) and a last split of 920, 960, 86, 216 and 440 rows (29, 30, 3, 7 and 14
+    # tiles), so a partial stage of each length, and a split shorter than one stage, is met
+    data = datagen.sift_like(n, 128, 731)
+    q = datagen.sift_like(2048, 128, 732)
+    idx = _index(data, oracle.L2)
+    print(f"case sift-like {n} x 128, 2048 queries, k=10, L2", flush=True)
+    ids, d, info = _run(idx, q, 10)
+    print(f"  path {info['path']}, f16 {info['scan_f16']}, splits {info['splits']}", flush=True)
+    assert info["path"] == "collect-bounded" and info["scan_f16"]
+    o_ids, o_d, _ = oracle.flat_search(data, q, 10, oracle.L2)
+    assert np.array_equal(ids, o_ids)
+    assert np.array_equal(d.view(np.uint32), o_d.view(np.uint32))
+
+
 def test_fp16_exact_fractions_and_signs(gpu):
     # multiples of 1/16 with signs: exact in fp16 (normal numbers or zero), not integers
     rng = np.random.default_rng(731)
