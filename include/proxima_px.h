@@ -185,8 +185,10 @@ int px_device_info(int device, char* name, size_t name_len, int* cu_count, int64
  * CUDA runtime and driver versions the same way. */
 int px_hip_versions(int* runtime_version, int* driver_version);
 
-/* Per-handle kernel timing with HIP events on the handle's stream. When enabled, each
- * search records the duration of its scan kernel and of the whole device pipeline. */
+/* Per-handle kernel timing with HIP events on the handle's stream (off by default). When
+ * enabled, each search records the duration of its scan kernel and of the whole device
+ * pipeline; the event markers between its kernels cost a few microseconds a search, so
+ * throughput is measured with it off. */
 int px_flat_set_timing(px_flat* idx, int enable);
 int px_flat_last_timing(const px_flat* idx, float* scan_ms, float* total_ms, int* splits,
                         int* blocks);
